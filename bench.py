@@ -1,0 +1,201 @@
+"""Benchmark of the low-bit GEMM hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+A step is one launch of the 1-bit sign-weight GEMM on BASELINE.json's configs[0] workload, at the M = 128 row count
+the metric quotes: A = int8 [128, 1024] per-token quantized from fp16 N(0,1) with fp16 scales, W = uniform random bits
+[4096, 1024] (export codes -> native layout), fp16 per-channel scales U(0.01, 0.1), fp16 output [128, 4096] (the
+int32 accumulators are written only by the parity tests, not in the timed step). Inputs are resident in HBM before
+timing. Launches go through the product C ABI (kea_lowbit_gemm) on torch's current stream; to keep the host out of the
+measurement the K launches are captured into HIP graphs of up to 100 launches each and replayed back to back.
+
+Prints one JSON line: value = int8 TOPS (2*M*N*K ops per step), `roofline` for the GEMM kernel (achieved = algorithmic
+ops per launch / average launch time from HIP events on the launch stream), `cpu_baseline` = the oracle's C port of the
+reference's b1_fallback arithmetic (unpack -> exact int32 dot -> FP32 epilogue -> fp16) timed on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "kea-kernels_amd"))
+sys.path.insert(0, str(ROOT))
+
+M, N, K = 128, 4096, 1024
+OPS = 2 * M * N * K
+# algorithmic HBM bytes per launch: A + W (1 bit) + alpha (fp16) + per-token scales (fp16) + Y (fp16)
+BYTES = M * K + N * K // 8 + 2 * N + 2 * M + 2 * M * N
+PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
+METRIC = "low-bit GEMM TOPS + % int8/HBM roofline; ms per 10-s clip encoder forward"
+
+
+def make_inputs(device):
+    import torch
+    from kea_kernels.binary import bits, kernels
+    g = torch.Generator().manual_seed(1234)
+    x = torch.randn(M, K, generator=g).to(torch.float16)
+    s32 = x.float().abs().amax(dim=1) / 127.0
+    qs = s32.to(torch.float16)                                   # fp16 per-token scales
+    q = torch.clamp(torch.round(x.float() / qs.float()[:, None]), -127, 127).to(torch.int8)
+    signs = torch.where(torch.rand(N, K, generator=g) < 0.5, -1, 1).to(torch.int8)
+    codes = bits.pack_signs(signs)                               # the export layout
+    alpha = (torch.rand(N, generator=g) * 0.09 + 0.01).to(torch.float16)
+    words = kernels.relayout_codes(codes, K, 1)
+    host = dict(q=q, qs=qs, codes=codes, alpha=alpha)
+    dev = dict(q=q.view(1, M, K).to(device), qs=qs.view(1, M).to(device), words=words.to(device),
+               alpha=alpha.to(device), y=torch.empty(M, N, dtype=torch.float16, device=device))
+    return host, dev
+
+
+def gpu_bench(steps: int, warmup: int):
+    import torch
+    from kea_kernels import _hip, lowbit
+    from kea_kernels.binary import configs
+    device = torch.device("cuda", 0)
+    _hip.require_gfx950(device)
+    host, d = make_inputs(device)
+
+    def step():
+        lowbit.gemm(1, d["q"], d["qs"], d["words"], N, K, d["alpha"], None, d["y"], None)
+
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        step()  # eager warm-up outside capture
+    torch.cuda.synchronize()
+
+    def capture(count):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(count):
+                step()
+        return graph
+
+    chunk = max(1, min(100, steps))
+    graphs = [(capture(chunk), chunk)] * (steps // chunk)
+    if steps % chunk:
+        graphs.append((capture(steps % chunk), steps % chunk))
+    wgraph = capture(max(1, min(100, warmup))) if warmup else None
+    torch.cuda.synchronize()
+
+    with torch.cuda.stream(stream):
+        done = 0
+        while wgraph is not None and done < warmup:
+            wgraph.replay()
+            done += max(1, min(100, warmup))
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for graph, _ in graphs:
+            graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    ms_per_step = ms / steps
+
+    # eager launch rate through the Python operator (host launch path included), for DESIGN.md only
+    with torch.cuda.stream(stream):
+        t0 = time.perf_counter()
+        for _ in range(200):
+            step()
+        torch.cuda.synchronize()
+        eager_us = (time.perf_counter() - t0) / 200 * 1e6
+
+    cfg = configs.choose(M, N, K, parts=1, wbits=1)
+    return ms_per_step, eager_us, cfg, host
+
+
+def cpu_baseline(host, seconds: float = 10.0):
+    """The oracle's C port of b1_fallback on the same workload, repeated for about `seconds` on this host's cores."""
+    import numpy as np
+    from oracle import oracle as O
+    cores = len(os.sched_getaffinity(0))
+    threads = O.set_threads(min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
+    q = host["q"].numpy().reshape(1, M, K)
+    codes = host["codes"].numpy()
+    qs = host["qs"].float().numpy().reshape(1, M)
+    alpha = host["alpha"].float().numpy()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        acc = O.b1_gemm(q, codes, K)
+        y = O.to_f16_bits(O.epilogue(acc, qs, alpha))
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    elapsed = time.perf_counter() - t0
+    del y
+    return {"value": round(OPS * reps / elapsed / 1e12, 6), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"{reps} full config-1 GEMMs (M=128, N=4096, K=1024, unpack + exact int32 dot + FP32 epilogue "
+                      f"+ fp16 rounding) in {elapsed:.1f} s, OpenMP over output columns"}
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if one exists (else None)."""
+    path = ROOT / "profiles" / "b1_gemm_config1_traffic.json"
+    if not path.is_file():
+        return None
+    try:
+        return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="low-bit GEMM benchmark (BASELINE.json config 1)")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the GEMM shards by clip; see "
+              "DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+    if args.steps < 1:
+        print("--steps must be >= 1", file=sys.stderr)
+        return 2
+    ms_per_step, eager_us, cfg, host = gpu_bench(args.steps, args.warmup)
+    tops = OPS / (ms_per_step * 1e-3) / 1e12
+    mfma_time = OPS / (PEAK_INT8_TOPS * 1e12)
+    hbm_time = BYTES / (PEAK_HBM_GBS * 1e9)
+    bound = "mfma" if mfma_time >= hbm_time else "hbm"
+    if bound == "mfma":
+        achieved, peak, unit = tops, PEAK_INT8_TOPS, "TFLOP/s"
+    else:
+        achieved, peak, unit = BYTES / (ms_per_step * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
+    line = {
+        "metric": METRIC,
+        "value": round(tops, 3),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "config1: 1-bit sign-weight x int8 GEMM, M=128 K=1024 N=4096, 1 activation part, "
+                               "fp16 per-token and per-channel scales, fp16 output, inputs resident in HBM, HIP-graph "
+                               "replay of back-to-back launches",
+                   "M": M, "N": N, "K": K, "parts": 1, "weight_bits": 1, "tile": cfg.label()},
+        "roofline": {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+                     "frac": round(achieved / peak, 5), "traffic": traffic_from_profiles(),
+                     "algorithmic_bytes": BYTES, "ops": OPS},
+        "eager_launch_us": round(eager_us, 3),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

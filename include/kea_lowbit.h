@@ -1,0 +1,164 @@
+/*
+ * kea_lowbit.h - C ABI of libkea_hip.so, the MI355X (gfx950) low-bit GEMM library.
+ *
+ * 1-bit (sign) and 2-bit (ternary) weights x int8 activations, int32 accumulation on CDNA4 int8 MFMA,
+ * fused FP32 epilogue (per-token and per-channel / per-group scales, bias, optional SiLU) to f32/f16/bf16.
+ *
+ * Conventions
+ *   - Every pointer named *_dev is a device pointer (hipMalloc / torch CUDA tensor memory); *_host is host memory.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream). Calls are stream-ordered and never
+ *     synchronize the host. No function allocates device memory: the caller passes every buffer.
+ *   - Functions return KEA_OK (0) on success, a negative KEA_E* code for a contract violation (nothing is
+ *     launched), or a positive hipError_t when the HIP runtime refused a launch. kea_last_error() returns a
+ *     thread-local message describing the last failure of the calling thread.
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout, kk/ = src/kea_kernels/):
+ *   kea_lowbit_gemm    <- the NVRTC kernel entry `b1_dot_*` (kk/binary/kernels.py:556-565) launched by
+ *                         kk/binary/layer.py:182-201 and kk/binary/layer_parts.py:322-340, the fallback
+ *                         `b1_fallback` (kk/binary/kernels.py:619-637), and the ternary Triton `_int8_dot` +
+ *                         `_finish` pair (kk/ternary/fused_kernels.py:53-120, kk/ternary/kernels.py:122-137)
+ *   kea_b1_relayout_host / kea_b1_unlayout_host
+ *                      <- `relayout` / `unlayout` (kk/binary/kernels.py:730-752), re-targeted to the gfx950
+ *                         native word layout described below
+ *   kea_t2_relayout_host / kea_t2_unlayout_host
+ *                      <- the int32 `packed_t` words of PackedLinear (kk/ternary/runtime.py:182-184) and the
+ *                         one-time `_expand` (kk/ternary/encoder4.py:51-61): the 2-bit codes stay resident
+ *   kea_quantize       <- `b1_quantize` (kk/binary/kernels.py:578-616) and the Triton `_quantize`
+ *                         (kk/ternary/fused_kernels.py:31-50), with LayerNorm / input SiLU fused
+ */
+#ifndef KEA_LOWBIT_H
+#define KEA_LOWBIT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define KEA_OK 0
+#define KEA_EINVAL (-1)     /* bad argument value (sizes, flags, dtype enums) */
+#define KEA_EALIGN (-2)     /* pointer or leading dimension not aligned as required */
+#define KEA_ECODES (-3)     /* invalid packed weight codes (tail bits, the unused ternary 11 pattern) */
+#define KEA_ESPACE (-4)     /* workspace missing or too small */
+#define KEA_ENODEV (-5)     /* no usable gfx950 device */
+
+/* element types of scales, bias and outputs */
+#define KEA_F32 0
+#define KEA_F16 1
+#define KEA_BF16 2
+
+/* epilogue flags */
+#define KEA_FLAG_SILU 1     /* y = y * sigmoid(y) after scale and bias */
+#define KEA_FLAG_ORDER 2    /* P = 2 / 3: first FP32 contraction fma(a1, s1, a0 * s0) instead of fma(a0, s0, a1 * s1) */
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Weight layouts
+ *
+ * Export layouts (the on-disk formats the library accepts; identical to the reference's):
+ *   1-bit   uint8 [N][ceil(K/8)]: code k of row n is bit k%8 of byte k/8 (LSB first); 1 = +1, 0 = -1;
+ *           unused tail bits 0 (kk/binary/bits.py:3-5).
+ *   2-bit   uint8 [N][ceil(K/4)]: code k at bits 2*(k%4) of byte k/4; 00 = 0, 01 = +1, 10 = -1; 11 invalid;
+ *           tail codes 0 (kk/formats.py:5-7, :62-81).
+ *
+ * Native layouts (device resident, built once by the relayout functions): uint32 words grouped per 16-row
+ * "n-tile" t (rows 16t .. 16t+15, zero padded past N) and per lane l = 0..63 of a wavefront:
+ *   1-bit   J = ceil(K/128) words per lane; word j of lane l holds, at bit 8*i + 4*h + d (i, d in 0..3,
+ *           h in 0..1), the INVERTED sign (1 = -1) of w[n = 16t + l%16][k = 128j + 64h + 16(l/16) + 4d + i].
+ *   2-bit   J = ceil(K/64) words per lane; word j of lane l holds, at bits 8*i + 2*d .. +1, the 2-bit code of
+ *           w[n = 16t + l%16][k = 64j + 16(l/16) + 4d + i] (k >= K: code 00).
+ *   Words are stored quad-major so that one 128-bit load per lane fetches 4 consecutive words: word j of lane
+ *   l of tile t is at index  t*J*64 + (j/4)*256 + l*wq + j%4,  wq = min(4, J - 4*(j/4)).
+ * --------------------------------------------------------------------------------------------------------- */
+
+/* Number of uint32 words of the native layout for an N x K weight matrix (0 on bad sizes). */
+int64_t kea_b1_native_words(int64_t n, int64_t k);
+int64_t kea_t2_native_words(int64_t n, int64_t k);
+
+/* Export codes (host) -> native words (host). KEA_ECODES on nonzero tail bits (1-bit) or on the 11 pattern /
+ * nonzero tail codes (2-bit). `words_host` must hold kea_*_native_words(n, k) words. */
+int kea_b1_relayout_host(const uint8_t *codes_host, int64_t n, int64_t k, uint32_t *words_host);
+int kea_t2_relayout_host(const uint8_t *codes_host, int64_t n, int64_t k, uint32_t *words_host);
+
+/* Inverse: native words (host) -> export codes (host). */
+int kea_b1_unlayout_host(const uint32_t *words_host, int64_t n, int64_t k, uint8_t *codes_host);
+int kea_t2_unlayout_host(const uint32_t *words_host, int64_t n, int64_t k, uint8_t *codes_host);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * The low-bit GEMM
+ *
+ *   acc_c[m][n] = sum_k q[c*part_stride + m*ldq + k] * w[n][k]        (exact int32, c = 0 .. parts-1)
+ *   per-channel scales (ws_group == 0):
+ *     r = comb_P(acc, qs[c*qs_stride + m])       P = 1: f(a0)*s0
+ *                                                P = 2: fma(f(a0), s0, f(a1)*s1)   (ORDER: fma(f(a1), s1, f(a0)*s0))
+ *                                                P = 3: fma(f(a2), s2, <P = 2 form>)
+ *     r = bias ? fma(r, alpha[n], bias[n]) : r * alpha[n]
+ *   per-group scales (ws_group > 0, a multiple of 64; alpha is [N][ceil(K/ws_group)]):
+ *     r = 0; for g in groups: r = fma(comb_P(acc_g, s), alpha[n][g], r);  r = bias ? r + bias[n] : r
+ *   SiLU (flags & KEA_FLAG_SILU): r = r / (1 + exp(-r)); then y[m*ldy + n] = RN(r) in y_dtype.
+ *   f() is int32 -> fp32 round-to-nearest; every FP32 operation is IEEE round-to-nearest-even, unfused
+ *   except where an fma is written (kk/binary/kernels_parts.py:28-39, kk/binary/kernels.py:76-93).
+ *
+ *   q          int8, rows 16-byte aligned: q_dev % 16 == 0, ldq % 16 == 0, part_stride % 16 == 0, ldq >= k.
+ *              Bytes at k .. ldq-1 are never read as data (they are masked to zero in-kernel).
+ *   qs         per-token scales [parts][m] (stride qs_stride), dtype KEA_F32 or KEA_F16.
+ *   w          native words (kea_b1_relayout_host / kea_t2_relayout_host), 16-byte aligned.
+ *   wscale     alpha, dtype KEA_F32 or KEA_F16.  bias: NULL or [n] of bias_dtype (KEA_F32 / KEA_F16).
+ *   y          NULL (no dequantized output) or [m][ldy] of y_dtype (KEA_F32 / KEA_F16 / KEA_BF16), ldy >= n.
+ *   acc_out    NULL or int32 [parts][m][acc_ld] raw accumulators (acc_ld >= n); exact for every split.
+ *   split_k    1 = one launch; > 1 = K split over split_k slices with an exact int32 reduction in a fixed
+ *              order (a second, finishing launch). Needs workspace_dev of kea_lowbit_gemm_workspace() bytes.
+ *              0 = the library chooses (a pure function of the shape).
+ *   config     0 = the library's tile table (a pure function of wbits, parts, m, n, k); > 0 selects a tile
+ *              configuration by id (results are identical for every config; see kea_config_count()).
+ * --------------------------------------------------------------------------------------------------------- */
+int kea_lowbit_gemm(int wbits,
+                    const int8_t *q_dev, int64_t part_stride, int64_t ldq, int parts,
+                    const void *qs_dev, int qs_dtype, int64_t qs_stride,
+                    const uint32_t *w_dev, int64_t n, int64_t k,
+                    const void *wscale_dev, int ws_dtype, int64_t ws_group,
+                    const void *bias_dev, int bias_dtype,
+                    void *y_dev, int y_dtype, int64_t ldy,
+                    int32_t *acc_out_dev, int64_t acc_ld,
+                    int64_t m, int flags, int split_k, int config,
+                    void *workspace_dev, int64_t workspace_bytes, void *stream);
+
+/* Workspace bytes kea_lowbit_gemm needs for these arguments (0 when split_k resolves to 1). */
+int64_t kea_lowbit_gemm_workspace(int wbits, int parts, int64_t m, int64_t n, int64_t k, int64_t ws_group,
+                                  int split_k, int config);
+
+/* The tile configuration id config == 0 resolves to for this shape (-1 on bad arguments). */
+int kea_lowbit_gemm_tile(int wbits, int parts, int64_t m, int64_t n, int64_t k);
+
+/* The split factor split_k == 0 resolves to for this shape (results are identical for every split). */
+int kea_lowbit_gemm_split(int wbits, int parts, int64_t m, int64_t n, int64_t k, int64_t ws_group, int config);
+
+/* Number of tile configurations (valid ids are 1 .. count) and a description of one ("BMxBN waves ..."). */
+int kea_config_count(void);
+const char *kea_config_name(int config);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Residual int8 activation quantizer (optional fused LayerNorm and input SiLU), one row per token:
+ *   x[m][k] at x_dev + (m / t) * xb + (m % t) * xt + k * xk   (elements of x_dtype, KEA_F32 / KEA_F16)
+ *   z = LayerNorm(x) * norm_w + norm_b   if norm_w_dev != NULL (FP32 weights, eps)
+ *   z = z * sigmoid(z)                   if input_silu
+ *   for c < parts:  s_c = max(max|z| / 127, 1e-30);  q_c = rint(z / s_c);  z = z - q_c * s_c
+ * q_dev int8 [parts][m][ldq] (zero padded from k to ldq), qs_dev [parts][m] of qs_dtype. With qs_dtype ==
+ * KEA_F16 the scale is rounded to fp16 first (floored at the smallest fp16 subnormal) and q is clamped to
+ * [-127, 127] (kk/binary/kernels.py:567-616, kk/ternary/fused_kernels.py:31-50).
+ * --------------------------------------------------------------------------------------------------------- */
+int kea_quantize(const void *x_dev, int x_dtype, int64_t xb, int64_t xt, int64_t xk, int64_t t,
+                 int64_t m, int64_t k, int parts,
+                 const float *norm_w_dev, const float *norm_b_dev, float eps, int input_silu,
+                 int8_t *q_dev, int64_t ldq, void *qs_dev, int qs_dtype, void *stream);
+
+/* Message of the calling thread's last failure ("" if none). */
+const char *kea_last_error(void);
+
+/* Library ABI version (major * 100 + minor). */
+int kea_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KEA_LOWBIT_H */

@@ -1,0 +1,75 @@
+"""Build libkea_hip.so (the gfx950 kernels and the C ABI of include/kea_lowbit.h) in-tree with hipcc.
+
+    python kea-kernels_amd/build.py [-j JOBS]
+
+Objects go to kea-kernels_amd/_build/, the library to kea-kernels_amd/kea_kernels/lib/libkea_hip.so.
+Every source is compiled for gfx950 only; device FP contraction is off (the epilogue's FP32 op order is part
+of the contract) and packed-FP32 instruction selection is disabled.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+BUILD = HERE / "_build"
+LIB = HERE / "kea_kernels" / "lib" / "libkea_hip.so"
+SOURCES = ["kea_gemm.hip", "kea_quantize.hip", "kea_layout.cpp"]
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build libkea_hip.so)")
+
+
+def flags() -> list[str]:
+    return ["-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off",
+            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function",
+            f"-I{HERE.parent / 'include'}"]
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [hipcc(), *flags()]
+    if src.suffix == ".cpp":
+        cmd += ["-x", "c++"]  # host-only translation unit
+    cmd += ["-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(line for line in res.stderr.splitlines() if noise not in line)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+
+
+def build(jobs: int | None = None) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    LIB.parent.mkdir(parents=True, exist_ok=True)
+    objs = [BUILD / (Path(s).stem + ".o") for s in SOURCES]
+    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        futures = [pool.submit(_compile, CSRC / s, o) for s, o in zip(SOURCES, objs)]
+        for f in futures:
+            f.result()
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("-j", "--jobs", type=int, default=None)
+    print(build(ap.parse_args().jobs))

@@ -1,0 +1,715 @@
+// Low-bit GEMM for MI355X (gfx950): 1-bit sign / 2-bit ternary weights x int8 activations on int8 MFMA.
+//
+// What it computes is the reference's b1_dot / _int8_dot contract (kk/binary/kernels.py:7-16, :134-565;
+// kk/binary/kernels_parts.py:28-55; kk/ternary/fused_kernels.py:53-120): P residual int8 activation parts, exact
+// int32 accumulators acc_c = sum_k q_c[m, k] * w[n, k], then the FP32 epilogue
+//     r = comb_P(acc, s) ; r = bias ? fma(r, alpha, bias) : r * alpha ; optional SiLU ; RN to the output type.
+// How it computes it is gfx950-native:
+//   * weights stay 1 or 2 bits per value in HBM in a wavefront-native word layout (kea_layout.cpp): a lane's four
+//     consecutive words arrive with one 128-bit global load, and one word yields the int8 MFMA operand of its lane
+//     for 2 (1-bit) or 1 (2-bit) k-steps of 64;
+//   * expansion to int8 is a mask (v_and_b32) plus a byte permute (v_perm_b32) per 4 weights, with the permute's
+//     constant table mapping the masked selector bytes to 0x01 / 0xFF (1-bit) or 0x00 / 0x01 / 0xFF (2-bit);
+//   * activations are staged in LDS (double buffered, padded rows), weights go global -> VGPR directly;
+//   * v_mfma_i32_16x16x64_i8 with the weight fragment as the A operand, so each lane ends up owning 4 consecutive
+//     output columns of one row: the epilogue stores 8-byte (fp16/bf16) or 16-byte (fp32) vectors;
+//   * split-K writes exact int32 slices [S][P][M][N] and a second kernel sums them in slice order (integer
+//     addition is exact, so every split gives the unsplit result bit for bit).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "kea_internal.h"
+
+namespace kea {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string &message) {
+    g_last_error = message;
+    return code;
+}
+
+}  // namespace kea
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct Params {
+    const int8_t *q;
+    long long part_stride, ldq;
+    const void *qs;
+    long long qs_stride;
+    const uint32_t *w;
+    const void *ws;
+    const void *bias;
+    void *y;
+    long long ldy;
+    int32_t *acc;
+    long long acc_ld;
+    int32_t *slices;  // split-K partials [S][P][M][N]
+    int M, N, K, J;   // J = native words per lane per n-tile
+    int NT;           // n-tiles present in the weight buffer
+    int quads_per_slice;
+    int flags;
+    int qs_dtype, ws_dtype, bias_dtype, y_dtype;
+    int y_vec;      // 1: y rows allow aligned 4-element vector stores
+    int acc_vec;    // 1: acc_out rows allow aligned int4 stores
+    int slice_vec;  // 1: the dense [S][P][M][N] slices allow aligned int4 access (N % 4 == 0)
+};
+
+__device__ __forceinline__ float load_scalar(const void *p, int dtype, long long i) {
+    if (dtype == KEA_F16) return (float)(((const _Float16 *)p)[i]);
+    return ((const float *)p)[i];
+}
+
+// 1-bit: plane (4h + d) of a native word -> four int8 weights. Stored bits are inverted signs, so after the mask
+// each selector byte is 0 (weight +1) or 2^(4h+d) (weight -1). The permute table {S0:S1} = {0x000000FF:0x00FFFF01}
+// maps selector 0 -> byte 0 = 0x01, 1 -> 0xFF, 2 -> 0xFF, 4 -> byte 4 = 0xFF, 8 -> sign of byte 1 = 0xFF and
+// every selector >= 13 -> 0xFF.
+template <int PLANE>
+__device__ __forceinline__ int b1_expand(uint32_t w) {
+    return (int)__builtin_amdgcn_perm(0x000000FFu, 0x00FFFF01u, w & (0x01010101u << PLANE));
+}
+// 2-bit: codes 00 / 01 / 10 (0, +1, -1) at bits 2d of each byte. Low pair: selectors {0, 1, 2} pick bytes
+// {0x00, 0x01, 0xFF} of 0x00FF0100. High pair (mask 0x0C): selectors {0, 4, 8} pick byte 0 = 0x00, byte 4 = 0x01
+// and the sign of byte 1 (0x80) = 0xFF.
+__device__ __forceinline__ int t2_lo(uint32_t w) {
+    return (int)__builtin_amdgcn_perm(0x00000000u, 0x00FF0100u, w & 0x03030303u);
+}
+__device__ __forceinline__ int t2_hi(uint32_t w) {
+    return (int)__builtin_amdgcn_perm(0x00000001u, 0x00008000u, w & 0x0C0C0C0Cu);
+}
+
+// The reference's P-part combination (comb<P>, kk/binary/kernels_parts.py:28-39). Built with -ffp-contract=off:
+// each * is one IEEE multiply, each fma an explicit fused multiply-add.
+template <int P>
+__device__ __forceinline__ float combine(const int *a, const float *s, int flags) {
+    if constexpr (P == 1) {
+        return (float)a[0] * s[0];
+    } else {
+        float r = (flags & KEA_FLAG_ORDER) ? __builtin_fmaf((float)a[1], s[1], (float)a[0] * s[0])
+                                           : __builtin_fmaf((float)a[0], s[0], (float)a[1] * s[1]);
+        if constexpr (P == 3) r = __builtin_fmaf((float)a[2], s[2], r);
+        return r;
+    }
+}
+
+__device__ __forceinline__ float finish(float r, float alpha, bool has_bias, float b, int flags) {
+    r = has_bias ? __builtin_fmaf(r, alpha, b) : r * alpha;
+    if (flags & KEA_FLAG_SILU) r = r / (1.0f + expf(-r));
+    return r;
+}
+
+__device__ __forceinline__ uint16_t to_f16_bits(float v) {
+    _Float16 h = (_Float16)v;  // IEEE round to nearest even
+    return __builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ uint16_t to_bf16_bits(float v) {
+    __bf16 h = (__bf16)v;  // IEEE round to nearest even
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+// Stores 4 consecutive outputs y[row][nb .. nb+3] (nb + r < N checked per element unless the vector path applies).
+__device__ __forceinline__ void store4(const Params &p, long long off, int nb, const float *v) {
+    const bool full = p.y_vec && nb + 3 < p.N;
+    if (p.y_dtype == KEA_F32) {
+        float *y = (float *)p.y + off;
+        if (full) {
+            *(float4 *)y = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+            for (int r = 0; r < 4; ++r)
+                if (nb + r < p.N) y[r] = v[r];
+        }
+    } else {
+        uint16_t h[4];
+        for (int r = 0; r < 4; ++r) h[r] = p.y_dtype == KEA_F16 ? to_f16_bits(v[r]) : to_bf16_bits(v[r]);
+        uint16_t *y = (uint16_t *)p.y + off;
+        if (full) {
+            uint2 packed;
+            packed.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+            packed.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+            *(uint2 *)y = packed;
+        } else {
+            for (int r = 0; r < 4; ++r)
+                if (nb + r < p.N) y[r] = h[r];
+        }
+    }
+}
+
+__device__ __forceinline__ void store_int4(int32_t *dst, bool vec, int nb, int N, const int *v) {
+    if (vec && nb + 3 < N) {
+        *(int4 *)dst = make_int4(v[0], v[1], v[2], v[3]);
+    } else {
+        for (int r = 0; r < 4; ++r)
+            if (nb + r < N) dst[r] = v[r];
+    }
+}
+
+// Epilogue operands of one row m and 4 consecutive columns nb..nb+3 (indices clamped into range; the clamped
+// values are never stored).
+struct EpiOperands {
+    float s[3];      // per-token scales of the P parts
+    float alpha[4];  // per-channel scales
+    float bias[4];
+};
+
+template <int P>
+__device__ __forceinline__ void load_row_scales(const Params &p, int m, EpiOperands &e) {
+    const int mm = m < p.M ? m : p.M - 1;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) e.s[c] = c < P ? load_scalar(p.qs, p.qs_dtype, c * p.qs_stride + mm) : 0.f;
+}
+
+__device__ __forceinline__ void load_col_scales(const Params &p, int nb, EpiOperands &e) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int n = nb + r < p.N ? nb + r : p.N - 1;
+        e.alpha[r] = load_scalar(p.ws, p.ws_dtype, n);
+        e.bias[r] = p.bias ? load_scalar(p.bias, p.bias_dtype, n) : 0.f;
+    }
+}
+
+// The epilogue of 4 consecutive columns nb..nb+3 of row m from exact accumulators a[c][r].
+template <int P>
+__device__ __forceinline__ void epilogue4(const Params &p, int m, int nb, const int (*a)[4], const EpiOperands &e) {
+    if (p.y) {
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            int ar[3] = {a[0][r], P > 1 ? a[1][r] : 0, P > 2 ? a[2][r] : 0};
+            v[r] = finish(combine<P>(ar, e.s, p.flags), e.alpha[r], p.bias != nullptr, e.bias[r], p.flags);
+        }
+        store4(p, (long long)m * p.ldy + nb, nb, v);
+    }
+    if (p.acc) {
+#pragma unroll
+        for (int c = 0; c < P; ++c)
+            store_int4(p.acc + ((long long)c * p.M + m) * p.acc_ld + nb, p.acc_vec, nb, p.N, a[c]);
+    }
+}
+
+// Stage geometry shared by the kernels and the host launcher. A stage is 256 k (2 native words at 1 bit, 4 at 2
+// bits), i.e. 16 activation units of 16 bytes per row. The ring depth NS is as deep as the LDS budget (kLdsBudget,
+// up to the 160 KB a gfx950 workgroup may allocate) and the 6-bit vmcnt counter allow (at least 2).
+struct StageShape {
+    int sw;           // native words per stage
+    int stage_bytes;  // LDS bytes per ring buffer
+    int copies;       // global->LDS copies per wavefront per stage
+    int ns;           // ring buffers
+};
+constexpr int kLdsBudget = 160 * 1024;
+
+__host__ __device__ constexpr StageShape stage_shape(int wbits, int parts, int rm, int rn, int wm, int wn) {
+    const int nw = wm * wn, bm = wm * rm * 16, bn = wn * rn * 16;
+    const int sw = wbits == 1 ? 2 : 4;
+    const int a_units = parts * bm * 16;
+    const int b_words = (bn / 16) * sw;
+    const int stage = a_units * 16 + b_words * 256;
+    const int copies = a_units / 64 / nw + b_words / nw;
+    int ns = kLdsBudget / stage;
+    if (ns > 63 / copies + 1) ns = 63 / copies + 1;
+    if (ns > 8) ns = 8;
+    if (ns < 2) ns = 2;
+    return StageShape{sw, stage, copies, ns};
+}
+
+// Waits until at most N vector-memory operations of this wavefront are outstanding (gfx9 s_waitcnt encoding:
+// vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their "no wait" maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier without the release/acquire fences of __syncthreads(): those make the compiler wait for every
+// in-flight global->LDS copy (vmcnt(0)), which would drain the ring. The kernel's explicit vmcnt waits already
+// guarantee that the copies a stage needs have landed; the empty asm statements keep the compiler from moving LDS
+// accesses across the barrier.
+__device__ __forceinline__ void stage_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+typedef __attribute__((address_space(1))) const void *gptr_t;
+typedef __attribute__((address_space(3))) void *lptr_t;
+
+__device__ __forceinline__ void dma16(const void *g, void *lds_wave_base) {
+    __builtin_amdgcn_global_load_lds((gptr_t)g, (lptr_t)lds_wave_base, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void *g, void *lds_wave_base) {
+    __builtin_amdgcn_global_load_lds((gptr_t)g, (lptr_t)lds_wave_base, 4, 0, 0);
+}
+
+// One workgroup: BM = WM*RM*16 activation rows x BN = WN*RN*16 output columns, WM x WN wavefronts; a wavefront owns
+// RM x RN 16x16 tiles for each of the P parts. SLICED: blockIdx.z is a K slice writing int32 partials.
+//
+// K is streamed in stages of SW native words (SW*128 k for 1-bit, SW*64 k for 2-bit) through a ring of NS LDS
+// buffers. Every byte arrives by direct global->LDS copies (global_load_lds: 16 bytes per lane for activations, 4 per
+// lane for weight words), issued NS-1 stages ahead and tracked with vmcnt, so up to (NS-1)*SW words of K are in
+// flight per workgroup and no VGPR holds staging data. Each wavefront issues the same number of copies per stage
+// (out-of-range sources are clamped to a valid address and their bytes are never used), which keeps the vmcnt
+// arithmetic exact. Activation rows are stored as 16-byte units with an XOR swizzle so that the 16 rows read by one
+// MFMA operand fetch land in distinct LDS bank groups.
+template <int WBITS, int P, int RM, int RN, int WM, int WN, bool SLICED>
+__global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
+    constexpr StageShape SHAPE = stage_shape(WBITS, P, RM, RN, WM, WN);
+    constexpr int SW = SHAPE.sw, NS = SHAPE.ns;
+    constexpr int NW = WM * WN;                 // wavefronts
+    constexpr int BM = WM * RM * 16, BN = WN * RN * 16;
+    constexpr int KW = WBITS == 1 ? 128 : 64;   // k per native word
+    constexpr int KS = KW / 64;                 // MFMA k-steps per word
+    constexpr int CHS = SW * KW / 16;           // 16-byte activation units per row per stage
+    constexpr int SWZ_DIV = CHS >= 16 ? 1 : 16 / CHS;
+    constexpr int SWZ_MASK = (CHS >= 16 ? 16 : CHS) - 1;
+    constexpr int A_UNITS = P * BM * CHS;
+    constexpr int A_BYTES = A_UNITS * 16;
+    constexpr int B_WORDS = (BN / 16) * SW;     // (tile, word) pairs per stage, 64 lanes each
+    constexpr int STAGE_BYTES = A_BYTES + B_WORDS * 256;
+    constexpr int LA = A_UNITS / 64 / NW;       // activation copies per wavefront per stage
+    constexpr int LB = B_WORDS / NW;            // weight copies per wavefront per stage
+    constexpr int L = LA + LB;
+    static_assert(A_UNITS % (64 * NW) == 0, "activation stage must split evenly over the wavefronts");
+    static_assert(B_WORDS % NW == 0, "weight stage must split evenly over the wavefronts");
+    static_assert(L * (NS - 1) < 64, "in-flight copies exceed the vmcnt range");
+    static_assert(L == SHAPE.copies && STAGE_BYTES == SHAPE.stage_bytes, "host and device stage geometry differ");
+    static_assert(NS >= 2, "at least double buffering");
+    extern __shared__ __attribute__((aligned(16))) int8_t lds[];  // NS * STAGE_BYTES
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    const int nquads = (p.J + 3) >> 2;
+    const int qa = SLICED ? (int)blockIdx.z * p.quads_per_slice : 0;
+    const int qb = SLICED ? min(nquads, qa + p.quads_per_slice) : nquads;
+    const int ja = 4 * qa, jb = min(4 * qb, p.J);
+    const int nst = (jb - ja + SW - 1) / SW;    // stages
+
+    auto swz = [](int r) { return (r / SWZ_DIV) & SWZ_MASK; };
+
+    // Issue the copies of stage s into ring buffer s % NS.
+    auto issue = [&](int s) {
+        int8_t *buf = lds + (s % NS) * STAGE_BYTES;
+        const int k0 = (ja + s * SW) * KW;
+#pragma unroll
+        for (int i = 0; i < LA; ++i) {
+            const int u0 = (i * NW + wave) * 64, u = u0 + lane;
+            const int row = u / CHS, chp = u - row * CHS;
+            const int c = row / BM, r = row - c * BM;
+            const int k = k0 + (chp ^ swz(r)) * 16;
+            const int m = m0 + r;
+            const int8_t *src = (m < p.M && k < p.K) ? p.q + c * p.part_stride + (long long)m * p.ldq + k : p.q;
+            dma16(src, buf + u0 * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < LB; ++i) {
+            const int b = i * NW + wave;
+            const int tt = b / SW, w = b - tt * SW;
+            const int t = (n0 >> 4) + tt, j = ja + s * SW + w;
+            const uint32_t *src = p.w;
+            if (t < p.NT && j < jb) {
+                const int jq = j >> 2, wq = min(4, p.J - 4 * jq);
+                src = p.w + (long long)t * p.J * 64 + (long long)jq * 256 + lane * wq + (j & 3);
+            }
+            dma4(src, buf + A_BYTES + b * 256);
+        }
+    };
+
+    v4i acc[P][RM][RN];
+#pragma unroll
+    for (int c = 0; c < P; ++c)
+#pragma unroll
+        for (int i = 0; i < RM; ++i)
+#pragma unroll
+            for (int jn = 0; jn < RN; ++jn) acc[c][i][jn] = (v4i){0, 0, 0, 0};
+
+    auto compute = [&](int s) {
+        const int8_t *buf = lds + (s % NS) * STAGE_BYTES;
+#pragma unroll
+        for (int w = 0; w < SW; ++w) {
+            const int j = ja + s * SW + w;
+            if (j >= jb) break;  // uniform: the stage runs past the K range
+            uint32_t wv[RN];
+#pragma unroll
+            for (int jn = 0; jn < RN; ++jn)
+                wv[jn] = *(const uint32_t *)(buf + A_BYTES + ((wn * RN + jn) * SW + w) * 256 + lane * 4);
+#pragma unroll
+            for (int h = 0; h < KS; ++h) {
+                v4i af[P][RM];
+#pragma unroll
+                for (int c = 0; c < P; ++c)
+#pragma unroll
+                    for (int i = 0; i < RM; ++i) {
+                        const int r = (wm * RM + i) * 16 + (lane & 15);
+                        const int ch = w * (KW / 16) + h * 4 + (lane >> 4);
+                        af[c][i] = *(const v4i *)(buf + ((c * BM + r) * CHS + (ch ^ swz(r))) * 16);
+                    }
+                const int kstep = j * KW + h * 64;
+                const bool tail = WBITS == 1 && kstep + 64 > p.K;  // uniform; 2-bit padding codes are already 0
+#pragma unroll
+                for (int jn = 0; jn < RN; ++jn) {
+                    const uint32_t w32 = wv[jn];
+                    v4i bf;
+                    if constexpr (WBITS == 1) {
+                        if (h == 0) {
+                            bf[0] = b1_expand<0>(w32); bf[1] = b1_expand<1>(w32); bf[2] = b1_expand<2>(w32); bf[3] = b1_expand<3>(w32);
+                        } else {
+                            bf[0] = b1_expand<4>(w32); bf[1] = b1_expand<5>(w32); bf[2] = b1_expand<6>(w32); bf[3] = b1_expand<7>(w32);
+                        }
+                        if (tail) {  // weights past K act as 0
+#pragma unroll
+                            for (int d = 0; d < 4; ++d) {
+                                const int valid = p.K - (kstep + (lane >> 4) * 16 + 4 * d);
+                                const uint32_t keep = valid >= 4 ? 0xFFFFFFFFu : (valid <= 0 ? 0u : (1u << (8 * valid)) - 1u);
+                                bf[d] = (int)((uint32_t)bf[d] & keep);
+                            }
+                        }
+                    } else {
+                        const uint32_t w4 = w32 >> 4;
+                        bf[0] = t2_lo(w32); bf[1] = t2_hi(w32); bf[2] = t2_lo(w4); bf[3] = t2_hi(w4);
+                    }
+#pragma unroll
+                    for (int c = 0; c < P; ++c)
+#pragma unroll
+                        for (int i = 0; i < RM; ++i)
+                            acc[c][i][jn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af[c][i], acc[c][i][jn], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // Waits for stage s given that `later` stages were issued after it.
+    auto wait_stage = [&](int later) {
+        switch (later) {
+            case 0: wait_vmcnt<0>(); break;
+            case 1: wait_vmcnt<(NS > 1 ? L * 1 : 0)>(); break;
+            case 2: wait_vmcnt<(NS > 2 ? L * 2 : 0)>(); break;
+            case 3: wait_vmcnt<(NS > 3 ? L * 3 : 0)>(); break;
+            case 4: wait_vmcnt<(NS > 4 ? L * 4 : 0)>(); break;
+            case 5: wait_vmcnt<(NS > 5 ? L * 5 : 0)>(); break;
+            case 6: wait_vmcnt<(NS > 6 ? L * 6 : 0)>(); break;
+            default: wait_vmcnt<(NS > 7 ? L * 7 : 0)>(); break;
+        }
+    };
+    static_assert(NS <= 8, "wait_stage covers up to 7 later stages");
+
+    // Epilogue operands are fetched before the ring so their latency overlaps the main loads (the copies below are
+    // issued after these loads, so the stage waits never depend on them).
+    EpiOperands rows[RM], cols[RN];
+    if constexpr (!SLICED) {
+#pragma unroll
+        for (int i = 0; i < RM; ++i) load_row_scales<P>(p, m0 + (wm * RM + i) * 16 + (lane & 15), rows[i]);
+#pragma unroll
+        for (int jn = 0; jn < RN; ++jn) load_col_scales(p, n0 + (wn * RN + jn) * 16 + (lane >> 4) * 4, cols[jn]);
+    }
+
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s)
+        if (s < nst) issue(s);
+    for (int s = 0; s < nst; ++s) {
+        const int issued_after = min(NS - 2, nst - 1 - s);  // stages issued after s so far
+        wait_stage(issued_after);
+        stage_barrier();  // stage s is in LDS for every wavefront; stage s-1's buffer is free
+        if (s + NS - 1 < nst) issue(s + NS - 1);
+        compute(s);
+    }
+
+    // ---- epilogue: the MFMA result row is the weight row n, the column the activation row m ----
+#pragma unroll
+    for (int i = 0; i < RM; ++i) {
+        const int m = m0 + (wm * RM + i) * 16 + (lane & 15);
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int jn = 0; jn < RN; ++jn) {
+            const int nb = n0 + (wn * RN + jn) * 16 + (lane >> 4) * 4;
+            if (nb >= p.N) continue;
+            int a[P][4];
+#pragma unroll
+            for (int c = 0; c < P; ++c)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) a[c][r] = acc[c][i][jn][r];
+            if constexpr (SLICED) {
+#pragma unroll
+                for (int c = 0; c < P; ++c)
+                    store_int4(p.slices + (((long long)blockIdx.z * P + c) * p.M + m) * p.N + nb, p.slice_vec, nb,
+                               p.N, a[c]);
+            } else {
+                EpiOperands e = cols[jn];
+#pragma unroll
+                for (int c = 0; c < 3; ++c) e.s[c] = rows[i].s[c];
+                epilogue4<P>(p, m, nb, a, e);
+            }
+        }
+    }
+}
+
+// Split-K finish: slices [S][P][M][N] summed in slice order (exact int32), then the epilogue of 4 columns.
+template <int P>
+__global__ void __launch_bounds__(256) finish_kernel(Params p, int S) {
+    const int groups = (p.N + 3) >> 2;
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (long long)p.M * groups) return;
+    const int m = (int)(idx / groups), nb = (int)(idx % groups) * 4;
+    int a[P][4];
+#pragma unroll
+    for (int c = 0; c < P; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a[c][r] = 0;
+    for (int z = 0; z < S; ++z)
+#pragma unroll
+        for (int c = 0; c < P; ++c) {
+            const int32_t *src = p.slices + (((long long)z * P + c) * p.M + m) * p.N + nb;
+            if (p.slice_vec && nb + 3 < p.N) {
+                const int4 v = *(const int4 *)src;
+                a[c][0] += v.x; a[c][1] += v.y; a[c][2] += v.z; a[c][3] += v.w;
+            } else {
+                for (int r = 0; r < 4; ++r)
+                    if (nb + r < p.N) a[c][r] += src[r];
+            }
+        }
+    EpiOperands e;
+    load_row_scales<P>(p, m, e);
+    load_col_scales(p, nb, e);
+    epilogue4<P>(p, m, nb, a, e);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Host side: tile table, validation, launch.
+
+struct Tile {
+    int rm, rn, wm, wn;
+    const char *name;
+};
+
+// Tile configurations (ids are 1-based in the ABI). Results are identical for every tile.
+constexpr Tile kTiles[] = {
+    {1, 1, 1, 4, "16x64 w1x4 r1x1"},   // 1
+    {2, 1, 1, 4, "32x64 w1x4 r2x1"},   // 2
+    {1, 2, 2, 2, "32x64 w2x2 r1x2"},   // 3
+    {1, 1, 2, 2, "32x32 w2x2 r1x1"},   // 4
+    {2, 2, 2, 2, "64x64 w2x2 r2x2"},   // 5
+    {1, 2, 4, 1, "64x32 w4x1 r1x2"},   // 6
+    {2, 4, 2, 2, "64x128 w2x2 r2x4"},  // 7
+    {4, 2, 2, 2, "128x64 w2x2 r4x2"},  // 8
+    {4, 4, 2, 2, "128x128 w2x2 r4x4"}, // 9
+};
+constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
+
+inline long long cdivl(long long a, long long b) { return (a + b - 1) / b; }
+
+using KernelFn = void (*)(Params);
+
+template <int WBITS, int P, int RM, int RN, int WM, int WN>
+KernelFn pick_sliced(bool sliced) {
+    return sliced ? gemm_kernel<WBITS, P, RM, RN, WM, WN, true> : gemm_kernel<WBITS, P, RM, RN, WM, WN, false>;
+}
+
+template <int WBITS, int P>
+KernelFn pick_tile(int id, bool sliced) {
+    switch (id) {
+        case 1: return pick_sliced<WBITS, P, 1, 1, 1, 4>(sliced);
+        case 2: return pick_sliced<WBITS, P, 2, 1, 1, 4>(sliced);
+        case 3: return pick_sliced<WBITS, P, 1, 2, 2, 2>(sliced);
+        case 4: return pick_sliced<WBITS, P, 1, 1, 2, 2>(sliced);
+        case 5: return pick_sliced<WBITS, P, 2, 2, 2, 2>(sliced);
+        case 6: return pick_sliced<WBITS, P, 1, 2, 4, 1>(sliced);
+        case 7: return pick_sliced<WBITS, P, 2, 4, 2, 2>(sliced);
+        case 8: return pick_sliced<WBITS, P, 4, 2, 2, 2>(sliced);
+        case 9: return pick_sliced<WBITS, P, 4, 4, 2, 2>(sliced);
+        default: return nullptr;
+    }
+}
+
+KernelFn pick_kernel(int wbits, int parts, int id, bool sliced) {
+    if (wbits == 1) {
+        if (parts == 1) return pick_tile<1, 1>(id, sliced);
+        if (parts == 2) return pick_tile<1, 2>(id, sliced);
+        return pick_tile<1, 3>(id, sliced);
+    }
+    if (parts == 1) return pick_tile<2, 1>(id, sliced);
+    if (parts == 2) return pick_tile<2, 2>(id, sliced);
+    return pick_tile<2, 3>(id, sliced);
+}
+
+using FinishFn = void (*)(Params, int);
+FinishFn pick_finish(int parts) {
+    if (parts == 1) return finish_kernel<1>;
+    if (parts == 2) return finish_kernel<2>;
+    return finish_kernel<3>;
+}
+
+// Tile choice: a pure function of (wbits, parts, m, n, k). Prefers the largest tile that still gives every CU a
+// workgroup (256 CUs on MI355X), else the one with the most workgroups.
+int choose_tile(int wbits, int parts, long long m, long long n, long long k) {
+    (void)wbits; (void)parts; (void)k;
+    static const int order[] = {9, 8, 7, 5, 2, 3, 6, 4, 1};
+    int best = 1;
+    long long best_wg = -1;
+    for (int id : order) {
+        const Tile &t = kTiles[id - 1];
+        const long long bm = t.wm * t.rm * 16, bn = t.wn * t.rn * 16;
+        if (bm > 16 && bm >= 2 * m) continue;  // mostly padding rows
+        const long long wgs = cdivl(m, bm) * cdivl(n, bn);
+        if (wgs >= 256) return id;
+        if (wgs > best_wg) { best_wg = wgs; best = id; }
+    }
+    return best;
+}
+
+// Split factor for split_k == 0: split K only when the (M, N) tiling leaves most CUs idle.
+int choose_split(int wbits, int parts, long long m, long long n, long long k, int id) {
+    const Tile &t = kTiles[id - 1];
+    const long long bm = t.wm * t.rm * 16, bn = t.wn * t.rn * 16;
+    const long long wgs = cdivl(m, bm) * cdivl(n, bn);
+    const long long J = wbits == 1 ? cdivl(k, 128) : cdivl(k, 64);
+    const long long quads = cdivl(J, 4);
+    (void)parts;
+    if (wgs >= 128 || quads < 2) return 1;
+    long long s = 1;
+    while (s * 2 <= quads && wgs * s * 2 <= 512) s *= 2;
+    return (int)s;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *kea_last_error(void) { return kea::g_last_error.c_str(); }
+
+int kea_version(void) { return 100; }
+
+int kea_config_count(void) { return kNumTiles; }
+
+const char *kea_config_name(int config) {
+    if (config < 1 || config > kNumTiles) return "";
+    return kTiles[config - 1].name;
+}
+
+static int resolve(int wbits, int parts, int64_t m, int64_t n, int64_t k, int split_k, int config, int *tile,
+                   int *split, int *qps) {
+    if (wbits != 1 && wbits != 2) return kea::fail(KEA_EINVAL, "wbits must be 1 or 2");
+    if (parts < 1 || parts > 3) return kea::fail(KEA_EINVAL, "parts must be 1, 2 or 3");
+    if (m < 0 || n < 1 || k < 1 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
+        return kea::fail(KEA_EINVAL, "bad sizes");
+    if (config < 0 || config > kNumTiles) return kea::fail(KEA_EINVAL, "unknown config id");
+    if (split_k < 0) return kea::fail(KEA_EINVAL, "split_k must be >= 0");
+    const int id = config ? config : choose_tile(wbits, parts, m, n, k);
+    const long long J = wbits == 1 ? cdivl(k, 128) : cdivl(k, 64);
+    const long long quads = cdivl(J, 4);
+    int s = split_k ? split_k : choose_split(wbits, parts, m, n, k, id);
+    if (s > quads) s = (int)quads;
+    if (s < 1) s = 1;
+    const int per = (int)cdivl(quads, s);
+    s = (int)cdivl(quads, per);  // no empty slices
+    *tile = id;
+    *split = s;
+    *qps = per;
+    return KEA_OK;
+}
+
+int64_t kea_lowbit_gemm_workspace(int wbits, int parts, int64_t m, int64_t n, int64_t k, int64_t ws_group,
+                                  int split_k, int config) {
+    int tile, s, qps;
+    if (ws_group) split_k = 1;
+    if (resolve(wbits, parts, m, n, k, split_k, config, &tile, &s, &qps) != KEA_OK) return -1;
+    return s > 1 ? (int64_t)s * parts * m * n * 4 : 0;
+}
+
+int kea_lowbit_gemm_tile(int wbits, int parts, int64_t m, int64_t n, int64_t k) {
+    int tile, s, qps;
+    if (resolve(wbits, parts, m, n, k, 1, 0, &tile, &s, &qps) != KEA_OK) return -1;
+    return tile;
+}
+
+int kea_lowbit_gemm_split(int wbits, int parts, int64_t m, int64_t n, int64_t k, int64_t ws_group, int config) {
+    int tile, s, qps;
+    if (ws_group) return 1;
+    if (resolve(wbits, parts, m, n, k, 0, config, &tile, &s, &qps) != KEA_OK) return -1;
+    return s;
+}
+
+int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts, const void *qs,
+                    int qs_dtype, int64_t qs_stride, const uint32_t *w, int64_t n, int64_t k, const void *wscale,
+                    int ws_dtype, int64_t ws_group, const void *bias, int bias_dtype, void *y, int y_dtype,
+                    int64_t ldy, int32_t *acc_out, int64_t acc_ld, int64_t m, int flags, int split_k, int config,
+                    void *workspace, int64_t workspace_bytes, void *stream) {
+    int tile, s, qps;
+    int rc = resolve(wbits, parts, m, n, k, ws_group ? 1 : split_k, config, &tile, &s, &qps);
+    if (rc != KEA_OK) return rc;
+    if (ws_group != 0) return kea::fail(KEA_EINVAL, "per-group weight scales are not supported by this build");
+    if (flags & ~(KEA_FLAG_SILU | KEA_FLAG_ORDER)) return kea::fail(KEA_EINVAL, "unknown flags");
+    if (m > 0 && (!w || !qs || !wscale)) return kea::fail(KEA_EINVAL, "q, qs, w and wscale are required");
+    if (m > 0 && !y && !acc_out) return kea::fail(KEA_EINVAL, "nothing to write: y and acc_out are both NULL");
+    if (qs_dtype != KEA_F32 && qs_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "qs dtype must be f32 or f16");
+    if (ws_dtype != KEA_F32 && ws_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "wscale dtype must be f32 or f16");
+    if (bias && bias_dtype != KEA_F32 && bias_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "bias dtype must be f32 or f16");
+    if (y && y_dtype != KEA_F32 && y_dtype != KEA_F16 && y_dtype != KEA_BF16)
+        return kea::fail(KEA_EINVAL, "y dtype must be f32, f16 or bf16");
+    if (y && ldy < n) return kea::fail(KEA_EINVAL, "ldy < n");
+    if (acc_out && acc_ld < n) return kea::fail(KEA_EINVAL, "acc_ld < n");
+    if (m == 0) return KEA_OK;
+    if (!q) return kea::fail(KEA_EINVAL, "q is required");
+    if (ldq < k) return kea::fail(KEA_EINVAL, "ldq < k");
+    if (parts > 1 && part_stride < m * ldq) return kea::fail(KEA_EINVAL, "part_stride < m * ldq (parts overlap)");
+    if (((uintptr_t)q & 15) || (ldq & 15) || (parts > 1 && (part_stride & 15)))
+        return kea::fail(KEA_EALIGN, "q needs 16-byte aligned rows: q % 16 == 0, ldq % 16 == 0, part_stride % 16 == 0");
+    if ((uintptr_t)w & 15) return kea::fail(KEA_EALIGN, "weight words must be 16-byte aligned");
+
+    Params p = {};
+    p.q = q; p.part_stride = part_stride; p.ldq = ldq;
+    p.qs = qs; p.qs_stride = qs_stride; p.qs_dtype = qs_dtype;
+    p.w = w; p.ws = wscale; p.ws_dtype = ws_dtype;
+    p.bias = bias; p.bias_dtype = bias_dtype;
+    p.y = y; p.ldy = ldy; p.y_dtype = y_dtype;
+    p.acc = acc_out; p.acc_ld = acc_ld;
+    p.M = (int)m; p.N = (int)n; p.K = (int)k;
+    p.J = (int)(wbits == 1 ? cdivl(k, 128) : cdivl(k, 64));
+    p.NT = (int)cdivl(n, 16);
+    p.quads_per_slice = qps;
+    p.flags = flags;
+    const int esz = (y_dtype == KEA_F32) ? 4 : 2;
+    p.y_vec = y && (ldy % 4 == 0) && ((uintptr_t)y % (4 * esz) == 0);
+    p.acc_vec = acc_out && (acc_ld % 4 == 0) && ((uintptr_t)acc_out % 16 == 0);
+
+    const Tile &t = kTiles[tile - 1];
+    const int bm = t.wm * t.rm * 16, bn = t.wn * t.rn * 16;
+    const StageShape shape = stage_shape(wbits, parts, t.rm, t.rn, t.wm, t.wn);
+    // Ring buffers actually used: a workgroup touches buffer s % NS for its stages s < nst, so with nst < NS only
+    // the first nst buffers need LDS.
+    const long long words_per_wg = std::min<long long>(4LL * qps, (long long)p.J);
+    const int nst = (int)cdivl(words_per_wg, shape.sw);
+    const int lds_bytes = std::min(shape.ns, nst) * shape.stage_bytes;
+    dim3 grid((unsigned)cdivl(n, bn), (unsigned)cdivl(m, bm), (unsigned)s);
+    dim3 block(t.wm * t.wn * 64);
+    hipStream_t st = (hipStream_t)stream;
+    if (s > 1) {
+        const int64_t need = (int64_t)s * parts * m * n * 4;
+        if (!workspace || workspace_bytes < need)
+            return kea::fail(KEA_ESPACE, "split-K workspace too small: need " + std::to_string(need) + " bytes");
+        if ((uintptr_t)workspace & 15) return kea::fail(KEA_EALIGN, "workspace must be 16-byte aligned");
+        p.slices = (int32_t *)workspace;
+        p.slice_vec = (n % 4 == 0);
+    }
+    KernelFn fn = pick_kernel(wbits, parts, tile, s > 1);
+    if (lds_bytes > 65536) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
+        if (e != hipSuccess) return kea::fail((int)e, std::string("LDS attribute refused: ") + hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(fn, grid, block, lds_bytes, st, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("gemm launch failed: ") + hipGetErrorString(e));
+    if (s > 1) {
+        const long long work = m * cdivl(n, 4);
+        hipLaunchKernelGGL(pick_finish(parts), dim3((unsigned)cdivl(work, 256)), dim3(256), 0, st, p, s);
+        e = hipGetLastError();
+        if (e != hipSuccess) return kea::fail((int)e, std::string("finish launch failed: ") + hipGetErrorString(e));
+    }
+    return KEA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,106 @@
+"""Tensor-level launchers of the C ABI: the low-bit GEMM and the residual int8 quantizer.
+
+`gemm` is the single launch path of every operator in this package (binary.layer, binary.layer_parts,
+ternary.fused_kernels): it checks tensors, resolves the split-K workspace from torch's caching allocator (as the
+reference does for its L2 workspace, kk/binary/layer.py:194-195) and enqueues kea_lowbit_gemm on the current stream.
+`quantize` enqueues kea_quantize. Neither synchronizes the host.
+"""
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from kea_kernels import _hip
+
+_SCALE_DTYPES = (torch.float32, torch.float16)
+
+
+def _on(device: torch.device, *tensors: Tensor | None) -> None:
+    for t in tensors:
+        if t is not None and t.device != device:
+            raise ValueError(f"tensor on {t.device}, expected {device}")
+
+
+def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscale: Tensor, bias: Tensor | None,
+         y: Tensor | None = None, acc_out: Tensor | None = None, *, m: int | None = None, silu: bool = False,
+         order: int = 0, config=None, ws_group: int = 0) -> None:
+    """y[:m] (rows of stride y.stride(0)) and/or acc_out [P, m, N] from q int8 [P, M, ldq] (16-byte aligned rows) and
+    qs [P, M] (f32 or f16). words: native layout of `wbits`-bit weights; wscale [N] (or [N, G] with ws_group)."""
+    if q.dtype != torch.int8 or q.dim() != 3:
+        raise ValueError(f"q must be int8 [P, M, ldq], got {q.dtype} {tuple(q.shape)}")
+    parts, rows, ldq = q.shape
+    m = rows if m is None else m
+    if m > rows:
+        raise ValueError(f"m = {m} exceeds the {rows} rows of q")
+    if q.stride(2) != 1 or q.stride(1) != ldq:
+        raise ValueError("q rows must be contiguous with row stride ldq")
+    if qs.dim() != 2 or qs.shape[0] != parts or qs.shape[1] < m or qs.stride(1) != 1 or qs.dtype not in _SCALE_DTYPES:
+        raise ValueError(f"qs must be f32/f16 [{parts}, >= {m}] with unit column stride")
+    if wscale.dtype not in _SCALE_DTYPES or not wscale.is_contiguous():
+        raise ValueError("weight scales must be contiguous f32 or f16")
+    if bias is not None and (bias.dtype not in _SCALE_DTYPES or not bias.is_contiguous() or bias.numel() != n):
+        raise ValueError("bias must be contiguous f32 or f16 [N]")
+    if y is None and acc_out is None:
+        raise ValueError("nothing to compute: y and acc_out are both None")
+    if y is not None and (y.dim() != 2 or y.shape[0] < m or y.shape[1] < n or y.stride(1) != 1):
+        raise ValueError(f"y must be a row-major [>= {m}, >= {n}] view")
+    if acc_out is not None and (acc_out.dtype != torch.int32 or acc_out.dim() != 3 or acc_out.shape[0] != parts
+                                or acc_out.shape[1] != m or acc_out.shape[2] < n or acc_out.stride(2) != 1
+                                or acc_out.stride(0) != m * acc_out.stride(1)):
+        raise ValueError(f"acc_out must be int32 [{parts}, {m}, >= {n}] with dense part planes")
+    if torch.is_grad_enabled() and (q.requires_grad or qs.requires_grad):
+        raise RuntimeError("the low-bit GEMM is inference only: an input requires grad")
+    device = q.device
+    _on(device, qs, words, wscale, bias, y, acc_out)
+    L = _hip.lib()
+    tile = 0 if config is None else int(config.tile)
+    split = 0 if config is None else int(config.split)
+    need = L.kea_lowbit_gemm_workspace(wbits, parts, max(m, 1), n, k, ws_group, split, tile)
+    if need < 0:
+        _hip.check(-1, "kea_lowbit_gemm_workspace")
+    workspace = torch.empty(need, dtype=torch.uint8, device=device) if need else None
+    rc = L.kea_lowbit_gemm(
+        wbits, q.data_ptr(), q.stride(0), ldq, parts,
+        qs.data_ptr(), _hip.dtype_code(qs.dtype), qs.stride(0),
+        words.data_ptr(), n, k,
+        wscale.data_ptr(), _hip.dtype_code(wscale.dtype), ws_group,
+        _hip.ptr(bias), _hip.dtype_code(bias.dtype) if bias is not None else 0,
+        _hip.ptr(y), _hip.dtype_code(y.dtype) if y is not None else 0, y.stride(0) if y is not None else 0,
+        _hip.ptr(acc_out), acc_out.stride(1) if acc_out is not None else 0,
+        m, int(silu) | (2 * int(order)), split, tile,
+        _hip.ptr(workspace), need, _hip.stream_handle(device))
+    _hip.check(rc, "kea_lowbit_gemm")
+
+
+def round_up(v: int, multiple: int) -> int:
+    return -(-v // multiple) * multiple
+
+
+def quantize(x: Tensor, rows: tuple, m: int, k: int, parts: int, *, norm=None, input_activation: str = "",
+             qs_dtype: torch.dtype = torch.float32, ldq: int | None = None) -> tuple[Tensor, Tensor, int]:
+    """Residual int8 parts of x: row r at x + (r // T) * XB + (r % T) * XT + kk * XK with rows = (XB, XT, XK, T).
+
+    Returns q int8 [parts, m, ldq] (zero padded from k to ldq = round_up(k, 16)), qs [parts, m] and ldq."""
+    if x.dtype not in (torch.float32, torch.float16):
+        raise ValueError(f"expected FP32 or FP16 input, got {x.dtype}")
+    if input_activation not in ("", "silu"):
+        raise ValueError(f"unsupported input activation {input_activation!r}")
+    xb, xt, xk, t = rows
+    ldq = round_up(k, 16) if ldq is None else ldq
+    q = torch.empty(parts, m, ldq, device=x.device, dtype=torch.int8)
+    qs = torch.empty(parts, m, device=x.device, dtype=qs_dtype)
+    if m == 0:
+        return q, qs, ldq
+    nw = nb = None
+    eps = 0.0
+    if norm is not None:
+        nw = norm.weight.detach().to(device=x.device, dtype=torch.float32).contiguous()
+        nb = norm.bias.detach().to(device=x.device, dtype=torch.float32).contiguous()
+        eps = float(norm.eps)
+        if nw.numel() != k or nb.numel() != k:
+            raise ValueError("LayerNorm shape does not match the input features")
+    rc = _hip.lib().kea_quantize(x.data_ptr(), _hip.dtype_code(x.dtype), xb, xt, xk, max(t, 1), m, k, parts,
+                                 _hip.ptr(nw), _hip.ptr(nb), eps, int(input_activation == "silu"), q.data_ptr(), ldq,
+                                 qs.data_ptr(), _hip.dtype_code(qs_dtype), _hip.stream_handle(x.device))
+    _hip.check(rc, "kea_quantize")
+    return q, qs, ldq

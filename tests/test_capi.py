@@ -1,0 +1,141 @@
+"""CPU tests of the C ABI library: it loads, exports every function include/kea_lowbit.h declares, its host-side
+layout functions place every code where the header says, and its argument validation rejects bad calls before any
+GPU work (no compute call is made without a GPU)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from kea_kernels import _hip
+from oracle import oracle as O
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "kea_lowbit.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(kea_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    names = declared_functions()
+    assert len(names) >= 10
+    L = _hip.lib()
+    for name in names:
+        assert hasattr(L, name), name
+        assert name in _hip.SIGNATURES, f"{name} has no ctypes signature"
+    assert L.kea_version() >= 100
+    assert L.kea_config_count() >= 1 and L.kea_config_name(1)
+
+
+def _words(wbits, codes, n, k):
+    L = _hip.lib()
+    count = (L.kea_b1_native_words if wbits == 1 else L.kea_t2_native_words)(n, k)
+    words = np.zeros(count, np.uint32)
+    fn = L.kea_b1_relayout_host if wbits == 1 else L.kea_t2_relayout_host
+    rc = fn(codes.ctypes.data_as(ctypes.c_void_p), n, k, words.ctypes.data_as(ctypes.c_void_p))
+    return rc, words
+
+
+def _index(t, j, lane, J):
+    jq = j // 4
+    wq = min(4, J - 4 * jq)
+    return t * J * 64 + jq * 256 + lane * wq + (j - 4 * jq)
+
+
+@pytest.mark.parametrize("n,k", [(1, 1), (16, 128), (20, 300), (33, 640), (5, 1100)])
+def test_b1_native_layout_places_every_code(n, k):
+    rng = np.random.default_rng(n * 7 + k)
+    signs = np.where(rng.random((n, k)) < 0.5, -1, 1).astype(np.int8)
+    codes = O.pack_signs(signs)
+    rc, words = _words(1, codes, n, k)
+    assert rc == 0
+    J = -(-k // 128)
+    assert words.size == -(-n // 16) * J * 64
+    # the header's formula: word j of lane l of tile t, bit 8i + 4h + d = inverted sign of w[16t + l%16][128j + ...]
+    for row in range(n):
+        t, c = divmod(row, 16)
+        for kk in range(k):
+            j, r = divmod(kk, 128)
+            h, r = divmod(r, 64)
+            g, r = divmod(r, 16)
+            d, i = divmod(r, 4)
+            bit = (words[_index(t, j, c + 16 * g, J)] >> (8 * i + 4 * h + d)) & 1
+            assert bit == (signs[row, kk] == -1)
+    back = np.zeros_like(codes)
+    assert _hip.lib().kea_b1_unlayout_host(words.ctypes.data_as(ctypes.c_void_p), n, k,
+                                           back.ctypes.data_as(ctypes.c_void_p)) == 0
+    assert np.array_equal(back, codes)
+
+
+@pytest.mark.parametrize("n,k", [(1, 1), (16, 64), (20, 300), (33, 640)])
+def test_t2_native_layout_places_every_code(n, k):
+    rng = np.random.default_rng(n * 11 + k)
+    values = rng.integers(-1, 2, (n, k)).astype(np.int8)
+    codes = O.pack_ternary(values)
+    rc, words = _words(2, codes, n, k)
+    assert rc == 0
+    J = -(-k // 64)
+    for row in range(n):
+        t, c = divmod(row, 16)
+        for kk in range(k):
+            j, r = divmod(kk, 64)
+            g, r = divmod(r, 16)
+            d, i = divmod(r, 4)
+            code = (words[_index(t, j, c + 16 * g, J)] >> (8 * i + 2 * d)) & 3
+            assert code == {0: 0, 1: 1, -1: 2}[int(values[row, kk])]
+    back = np.zeros_like(codes)
+    assert _hip.lib().kea_t2_unlayout_host(words.ctypes.data_as(ctypes.c_void_p), n, k,
+                                           back.ctypes.data_as(ctypes.c_void_p)) == 0
+    assert np.array_equal(back, codes)
+
+
+def test_relayout_rejects_invalid_codes():
+    bad = np.array([[0, 0x80], [0, 0]], np.uint8)  # K = 12: bit 15 is tail padding
+    rc, _ = _words(1, bad, 2, 12)
+    assert rc == -3 and "tail" in _hip.last_error()
+    rc, _ = _words(2, np.array([[0b11]], np.uint8), 1, 4)
+    assert rc == -3
+    rc, _ = _words(2, np.array([[0b01_00_00_00]], np.uint8), 1, 3)
+    assert rc == -3
+
+
+def test_gemm_argument_validation_happens_before_any_launch():
+    L = _hip.lib()
+    args = dict(wbits=1, q=None, part_stride=0, ldq=1024, parts=1, qs=None, qs_dtype=0, qs_stride=0, w=None, n=4096,
+                k=1024, ws=None, ws_dtype=0, ws_group=0, bias=None, bias_dtype=0, y=None, y_dtype=0, ldy=4096,
+                acc=None, acc_ld=0, m=128, flags=0, split=1, config=0, workspace=None, wsb=0, stream=None)
+
+    def call(**over):
+        a = dict(args, **over)
+        return L.kea_lowbit_gemm(*a.values())
+
+    assert call(wbits=3) == -1 and "wbits" in _hip.last_error()
+    assert call(parts=4) == -1
+    assert call() == -1  # missing q / w / scales
+    fake = 4096  # never dereferenced: validation fails first
+    base = dict(q=fake, qs=fake, w=fake, ws=fake, y=fake)
+    assert call(**base, flags=8) == -1 and "flags" in _hip.last_error()
+    assert call(**base, ldq=1000) == -1  # ldq < k
+    assert call(**base, ldq=1032) == -2 and "aligned" in _hip.last_error()  # ldq % 16
+    assert call(**dict(base, q=fake + 4)) == -2
+    assert call(**base, y_dtype=7) == -1
+    assert call(**base, ldy=100) == -1
+    assert call(**base, config=999) == -1
+    assert call(**base, split=4) == -4 and "workspace" in _hip.last_error()
+    assert call(**base, ws_group=100) == -1
+
+
+def test_tile_and_split_tables_are_pure_functions():
+    L = _hip.lib()
+    for (m, n, k) in [(128, 4096, 1024), (1000, 3072, 1024), (1, 2560, 640), (16, 1024, 4096)]:
+        t1, t2 = L.kea_lowbit_gemm_tile(1, 1, m, n, k), L.kea_lowbit_gemm_tile(1, 1, m, n, k)
+        assert t1 == t2 and 1 <= t1 <= L.kea_config_count()
+        s = L.kea_lowbit_gemm_split(1, 1, m, n, k, 0, 0)
+        assert s >= 1
+        ws = L.kea_lowbit_gemm_workspace(1, 1, m, n, k, 0, 0, 0)
+        assert ws == (s * m * n * 4 if s > 1 else 0)
