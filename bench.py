@@ -152,7 +152,19 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB (5 times); the known byte count "
+                         "calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args(argv)
+    if args.copy_calibration:
+        import torch
+        src = torch.ones(args.copy_calibration << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel() * 4, "launches": 5}), flush=True)
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the GEMM shards by clip; see "
               "DESIGN.md). Run with --gpus 1.", file=sys.stderr)

@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdint>
 #include <cstdio>
 #include <string>
@@ -255,8 +256,8 @@ __device__ __forceinline__ void dma4(const void *g, void *lds_wave_base) {
 // flight per workgroup and no VGPR holds staging data. Each wavefront issues the same number of copies per stage
 // (out-of-range sources are clamped to a valid address and their bytes are never used), which keeps the vmcnt
 // arithmetic exact. Activation rows are stored as 16-byte units with an XOR swizzle so that the 16 rows read by one
-// MFMA operand fetch land in distinct LDS bank groups.
-template <int WBITS, int P, int RM, int RN, int WM, int WN, bool SLICED>
+// MFMA operand fetch land in distinct LDS bank groups. KTAIL kernels serve K % 16 != 0 (byte-precise K masking).
+template <int WBITS, int P, int RM, int RN, int WM, int WN, bool SLICED, bool KTAIL>
 __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     constexpr StageShape SHAPE = stage_shape(WBITS, P, RM, RN, WM, WN);
     constexpr int SW = SHAPE.sw, NS = SHAPE.ns;
@@ -281,7 +282,8 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     static_assert(NS >= 2, "at least double buffering");
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];  // NS * STAGE_BYTES
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // the wavefront index is uniform; readfirstlane tells the compiler so (wave-derived math then runs on SALU)
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
     const int nquads = (p.J + 3) >> 2;
@@ -292,31 +294,53 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
 
     auto swz = [](int r) { return (r / SWZ_DIV) & SWZ_MASK; };
 
+    // Per-lane copy sources, fixed for the whole K loop: q plus a 32-bit per-lane byte offset (the host guarantees
+    // that q spans < 2 GiB), so every copy is one global_load_lds with a uniform base. Activation rows past M are
+    // clamped to row M-1 (their outputs are never stored). Units at k >= kend (K, or the end of this split-K slice)
+    // only occur in a workgroup's last stage; they copy the start of their row (in bounds) and the last stage's
+    // compute zeroes the weights of those k.
+    const int kend = min(p.K, jb * KW);
+    uint32_t a_off[LA];
+    int a_koff[LA];
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+        const int u = (i * NW + wave) * 64 + lane;
+        const int row = u / CHS, chp = u - row * CHS;
+        const int c = row / BM, r = row - c * BM;
+        a_koff[i] = (chp ^ swz(r)) * 16;
+        const int m = min(m0 + r, p.M - 1);
+        a_off[i] = (uint32_t)(c * p.part_stride + (long long)m * p.ldq + a_koff[i]);
+    }
+    const int tile0 = n0 >> 4;
+    const int jtail = (p.J - 1) & ~3, wq_tail = p.J - jtail;       // the last (possibly short) quad
+    const uint32_t b_lane = (uint32_t)lane * 16u, b_lane_tail = (uint32_t)(lane * wq_tail) * 4u;
+
     // Issue the copies of stage s into ring buffer s % NS.
     auto issue = [&](int s) {
         int8_t *buf = lds + (s % NS) * STAGE_BYTES;
-        const int k0 = (ja + s * SW) * KW;
+        const int jstage = ja + s * SW;
+        const int k0 = jstage * KW;
+        if (k0 + SW * KW <= kend) {  // uniform: every unit of the stage is inside [0, kend)
+            const int8_t *abase = p.q + k0;
 #pragma unroll
-        for (int i = 0; i < LA; ++i) {
-            const int u0 = (i * NW + wave) * 64, u = u0 + lane;
-            const int row = u / CHS, chp = u - row * CHS;
-            const int c = row / BM, r = row - c * BM;
-            const int k = k0 + (chp ^ swz(r)) * 16;
-            const int m = m0 + r;
-            const int8_t *src = (m < p.M && k < p.K) ? p.q + c * p.part_stride + (long long)m * p.ldq + k : p.q;
-            dma16(src, buf + u0 * 16);
+            for (int i = 0; i < LA; ++i) dma16(abase + a_off[i], buf + (i * NW + wave) * 64 * 16);
+        } else {
+#pragma unroll
+            for (int i = 0; i < LA; ++i) {
+                const uint32_t off = k0 + a_koff[i] < kend ? a_off[i] + (uint32_t)k0 : a_off[i] - (uint32_t)a_koff[i];
+                dma16(p.q + off, buf + (i * NW + wave) * 64 * 16);
+            }
         }
 #pragma unroll
         for (int i = 0; i < LB; ++i) {
-            const int b = i * NW + wave;
+            const int b = i * NW + wave;             // wave-uniform
             const int tt = b / SW, w = b - tt * SW;
-            const int t = (n0 >> 4) + tt, j = ja + s * SW + w;
-            const uint32_t *src = p.w;
-            if (t < p.NT && j < jb) {
-                const int jq = j >> 2, wq = min(4, p.J - 4 * jq);
-                src = p.w + (long long)t * p.J * 64 + (long long)jq * 256 + lane * wq + (j & 3);
-            }
-            dma4(src, buf + A_BYTES + b * 256);
+            const int t = tile0 + tt, j = jstage + w;
+            // words past the slice or past N are never used (their k are masked, their columns never stored)
+            const int jj = j < jb ? j : ja, tc = t < p.NT ? t : p.NT - 1;
+            const int jq = jj & ~3;
+            const char *wbase = (const char *)(p.w + ((long long)tc * p.J + jq) * 64 + (jj & 3));
+            dma4(wbase + (jq == jtail ? b_lane_tail : b_lane), buf + A_BYTES + b * 256);
         }
     };
 
@@ -328,32 +352,42 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
 #pragma unroll
             for (int jn = 0; jn < RN; ++jn) acc[c][i][jn] = (v4i){0, 0, 0, 0};
 
-    auto compute = [&](int s) {
+    // One stage of MFMAs: straight-line code (no accumulator ever passes a control-flow merge; merges made the
+    // compiler emit AGPR copy chains). The LDS reads of word w + 1 are issued before the MFMAs of word w. MASKED (the
+    // last stage) zeroes the weights at k >= kend: per 16-byte group of a lane's operand, or per byte for KTAIL.
+    auto compute = [&](int s, auto masked_tag) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
         const int8_t *buf = lds + (s % NS) * STAGE_BYTES;
-#pragma unroll
-        for (int w = 0; w < SW; ++w) {
-            const int j = ja + s * SW + w;
-            if (j >= jb) break;  // uniform: the stage runs past the K range
-            uint32_t wv[RN];
+        v4i af[2][KS][P][RM];
+        uint32_t wv[2][RN];
+        auto fetch = [&](int w, int slot) {
 #pragma unroll
             for (int jn = 0; jn < RN; ++jn)
-                wv[jn] = *(const uint32_t *)(buf + A_BYTES + ((wn * RN + jn) * SW + w) * 256 + lane * 4);
+                wv[slot][jn] = *(const uint32_t *)(buf + A_BYTES + ((wn * RN + jn) * SW + w) * 256 + lane * 4);
 #pragma unroll
-            for (int h = 0; h < KS; ++h) {
-                v4i af[P][RM];
+            for (int h = 0; h < KS; ++h)
 #pragma unroll
                 for (int c = 0; c < P; ++c)
 #pragma unroll
                     for (int i = 0; i < RM; ++i) {
                         const int r = (wm * RM + i) * 16 + (lane & 15);
                         const int ch = w * (KW / 16) + h * 4 + (lane >> 4);
-                        af[c][i] = *(const v4i *)(buf + ((c * BM + r) * CHS + (ch ^ swz(r))) * 16);
+                        af[slot][h][c][i] = *(const v4i *)(buf + ((c * BM + r) * CHS + (ch ^ swz(r))) * 16);
                     }
+        };
+        fetch(0, 0);
+#pragma unroll
+        for (int w = 0; w < SW; ++w) {
+            const int j = ja + s * SW + w;
+            if (w + 1 < SW) fetch(w + 1, (w + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);  // keep the next word's LDS reads ahead of this word's MFMAs
+            const int slot = w & 1;
+#pragma unroll
+            for (int h = 0; h < KS; ++h) {
                 const int kstep = j * KW + h * 64;
-                const bool tail = WBITS == 1 && kstep + 64 > p.K;  // uniform; 2-bit padding codes are already 0
 #pragma unroll
                 for (int jn = 0; jn < RN; ++jn) {
-                    const uint32_t w32 = wv[jn];
+                    const uint32_t w32 = wv[slot][jn];
                     v4i bf;
                     if constexpr (WBITS == 1) {
                         if (h == 0) {
@@ -361,23 +395,28 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
                         } else {
                             bf[0] = b1_expand<4>(w32); bf[1] = b1_expand<5>(w32); bf[2] = b1_expand<6>(w32); bf[3] = b1_expand<7>(w32);
                         }
-                        if (tail) {  // weights past K act as 0
-#pragma unroll
-                            for (int d = 0; d < 4; ++d) {
-                                const int valid = p.K - (kstep + (lane >> 4) * 16 + 4 * d);
-                                const uint32_t keep = valid >= 4 ? 0xFFFFFFFFu : (valid <= 0 ? 0u : (1u << (8 * valid)) - 1u);
-                                bf[d] = (int)((uint32_t)bf[d] & keep);
-                            }
-                        }
                     } else {
                         const uint32_t w4 = w32 >> 4;
                         bf[0] = t2_lo(w32); bf[1] = t2_hi(w32); bf[2] = t2_lo(w4); bf[3] = t2_hi(w4);
+                    }
+                    if constexpr (MASKED && KTAIL) {
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) {
+                            const int valid = kend - (kstep + (lane >> 4) * 16 + 4 * d);
+                            const uint32_t keep = valid >= 4 ? 0xFFFFFFFFu : (valid <= 0 ? 0u : (1u << (8 * valid)) - 1u);
+                            bf[d] = (int)((uint32_t)bf[d] & keep);
+                        }
+                    } else if constexpr (MASKED) {  // kend is a multiple of 16 here
+                        const bool keep = kstep + (lane >> 4) * 16 < kend;
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) bf[d] = keep ? bf[d] : 0;
                     }
 #pragma unroll
                     for (int c = 0; c < P; ++c)
 #pragma unroll
                         for (int i = 0; i < RM; ++i)
-                            acc[c][i][jn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af[c][i], acc[c][i][jn], 0, 0, 0);
+                            acc[c][i][jn] =
+                                __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af[slot][h][c][i], acc[c][i][jn], 0, 0, 0);
                 }
             }
         }
@@ -411,13 +450,19 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s)
         if (s < nst) issue(s);
-    for (int s = 0; s < nst; ++s) {
+    using plain_t = std::integral_constant<bool, false>;
+    using masked_t = std::integral_constant<bool, true>;
+    for (int s = 0; s < nst - 1; ++s) {
         const int issued_after = min(NS - 2, nst - 1 - s);  // stages issued after s so far
         wait_stage(issued_after);
         stage_barrier();  // stage s is in LDS for every wavefront; stage s-1's buffer is free
         if (s + NS - 1 < nst) issue(s + NS - 1);
-        compute(s);
+        compute(s, plain_t{});
     }
+    // the last stage (the host never launches an empty K range, so nst >= 1)
+    wait_vmcnt<0>();
+    stage_barrier();
+    compute(nst - 1, masked_t{});
 
     // ---- epilogue: the MFMA result row is the weight row n, the column the activation row m ----
 #pragma unroll
@@ -506,7 +551,8 @@ using KernelFn = void (*)(Params);
 
 template <int WBITS, int P, int RM, int RN, int WM, int WN>
 KernelFn pick_sliced(bool sliced) {
-    return sliced ? gemm_kernel<WBITS, P, RM, RN, WM, WN, true> : gemm_kernel<WBITS, P, RM, RN, WM, WN, false>;
+    return sliced ? gemm_kernel<WBITS, P, RM, RN, WM, WN, true, false>
+                  : gemm_kernel<WBITS, P, RM, RN, WM, WN, false, false>;
 }
 
 template <int WBITS, int P>
@@ -525,7 +571,16 @@ KernelFn pick_tile(int id, bool sliced) {
     }
 }
 
-KernelFn pick_kernel(int wbits, int parts, int id, bool sliced) {
+// K % 16 != 0 runs the byte-precise variant of tile kTailTile, unsplit.
+constexpr int kTailTile = 4;
+template <int WBITS, int P>
+KernelFn pick_ktail() { return gemm_kernel<WBITS, P, 1, 1, 2, 2, false, true>; }
+
+KernelFn pick_kernel(int wbits, int parts, int id, bool sliced, bool ktail) {
+    if (ktail) {
+        if (wbits == 1) return parts == 1 ? pick_ktail<1, 1>() : parts == 2 ? pick_ktail<1, 2>() : pick_ktail<1, 3>();
+        return parts == 1 ? pick_ktail<2, 1>() : parts == 2 ? pick_ktail<2, 2>() : pick_ktail<2, 3>();
+    }
     if (wbits == 1) {
         if (parts == 1) return pick_tile<1, 1>(id, sliced);
         if (parts == 2) return pick_tile<1, 2>(id, sliced);
@@ -598,10 +653,14 @@ static int resolve(int wbits, int parts, int64_t m, int64_t n, int64_t k, int sp
         return kea::fail(KEA_EINVAL, "bad sizes");
     if (config < 0 || config > kNumTiles) return kea::fail(KEA_EINVAL, "unknown config id");
     if (split_k < 0) return kea::fail(KEA_EINVAL, "split_k must be >= 0");
-    const int id = config ? config : choose_tile(wbits, parts, m, n, k);
+    int id = config ? config : choose_tile(wbits, parts, m, n, k);
     const long long J = wbits == 1 ? cdivl(k, 128) : cdivl(k, 64);
     const long long quads = cdivl(J, 4);
     int s = split_k ? split_k : choose_split(wbits, parts, m, n, k, id);
+    if (k & 15) {  // byte-precise K masking exists for one unsplit tile only
+        id = kTailTile;
+        s = 1;
+    }
     if (s > quads) s = (int)quads;
     if (s < 1) s = 1;
     const int per = (int)cdivl(quads, s);
@@ -659,6 +718,8 @@ int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq
     if (((uintptr_t)q & 15) || (ldq & 15) || (parts > 1 && (part_stride & 15)))
         return kea::fail(KEA_EALIGN, "q needs 16-byte aligned rows: q % 16 == 0, ldq % 16 == 0, part_stride % 16 == 0");
     if ((uintptr_t)w & 15) return kea::fail(KEA_EALIGN, "weight words must be 16-byte aligned");
+    if ((int64_t)(parts - 1) * part_stride + m * ldq > (int64_t)INT32_MAX)
+        return kea::fail(KEA_EINVAL, "q spans more than 2 GiB: split the call along M");
 
     Params p = {};
     p.q = q; p.part_stride = part_stride; p.ldq = ldq;
@@ -695,7 +756,7 @@ int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq
         p.slices = (int32_t *)workspace;
         p.slice_vec = (n % 4 == 0);
     }
-    KernelFn fn = pick_kernel(wbits, parts, tile, s > 1);
+    KernelFn fn = pick_kernel(wbits, parts, tile, s > 1, (k & 15) != 0);
     if (lds_bytes > 65536) {
         hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
         if (e != hipSuccess) return kea::fail((int)e, std::string("LDS attribute refused: ") + hipGetErrorString(e));
