@@ -358,66 +358,64 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     auto compute = [&](int s, auto masked_tag) {
         constexpr bool MASKED = decltype(masked_tag)::value;
         const int8_t *buf = lds + (s % NS) * STAGE_BYTES;
-        v4i af[2][KS][P][RM];
+        constexpr int STEPS = SW * KS;  // MFMA k-steps per stage
+        v4i af[2][P][RM];
         uint32_t wv[2][RN];
-        auto fetch = [&](int w, int slot) {
+        auto fetch = [&](int t, int slot) {
+            const int w = t / KS, h = t % KS;
+            if (h == 0) {
 #pragma unroll
-            for (int jn = 0; jn < RN; ++jn)
-                wv[slot][jn] = *(const uint32_t *)(buf + A_BYTES + ((wn * RN + jn) * SW + w) * 256 + lane * 4);
+                for (int jn = 0; jn < RN; ++jn)
+                    wv[w & 1][jn] = *(const uint32_t *)(buf + A_BYTES + ((wn * RN + jn) * SW + w) * 256 + lane * 4);
+            }
 #pragma unroll
-            for (int h = 0; h < KS; ++h)
+            for (int c = 0; c < P; ++c)
 #pragma unroll
-                for (int c = 0; c < P; ++c)
-#pragma unroll
-                    for (int i = 0; i < RM; ++i) {
-                        const int r = (wm * RM + i) * 16 + (lane & 15);
-                        const int ch = w * (KW / 16) + h * 4 + (lane >> 4);
-                        af[slot][h][c][i] = *(const v4i *)(buf + ((c * BM + r) * CHS + (ch ^ swz(r))) * 16);
-                    }
+                for (int i = 0; i < RM; ++i) {
+                    const int r = (wm * RM + i) * 16 + (lane & 15);
+                    const int ch = w * (KW / 16) + h * 4 + (lane >> 4);
+                    af[slot][c][i] = *(const v4i *)(buf + ((c * BM + r) * CHS + (ch ^ swz(r))) * 16);
+                }
         };
         fetch(0, 0);
 #pragma unroll
-        for (int w = 0; w < SW; ++w) {
-            const int j = ja + s * SW + w;
-            if (w + 1 < SW) fetch(w + 1, (w + 1) & 1);
-            __builtin_amdgcn_sched_barrier(0);  // keep the next word's LDS reads ahead of this word's MFMAs
-            const int slot = w & 1;
+        for (int t = 0; t < STEPS; ++t) {
+            const int w = t / KS, h = t % KS;
+            if (t + 1 < STEPS) fetch(t + 1, (t + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);  // keep the next k-step's LDS reads ahead of this one's MFMAs
+            const int slot = t & 1;
+            const int kstep = (ja + s * SW + w) * KW + h * 64;
 #pragma unroll
-            for (int h = 0; h < KS; ++h) {
-                const int kstep = j * KW + h * 64;
-#pragma unroll
-                for (int jn = 0; jn < RN; ++jn) {
-                    const uint32_t w32 = wv[slot][jn];
-                    v4i bf;
-                    if constexpr (WBITS == 1) {
-                        if (h == 0) {
-                            bf[0] = b1_expand<0>(w32); bf[1] = b1_expand<1>(w32); bf[2] = b1_expand<2>(w32); bf[3] = b1_expand<3>(w32);
-                        } else {
-                            bf[0] = b1_expand<4>(w32); bf[1] = b1_expand<5>(w32); bf[2] = b1_expand<6>(w32); bf[3] = b1_expand<7>(w32);
-                        }
+            for (int jn = 0; jn < RN; ++jn) {
+                const uint32_t w32 = wv[w & 1][jn];
+                v4i bf;
+                if constexpr (WBITS == 1) {
+                    if (h == 0) {
+                        bf[0] = b1_expand<0>(w32); bf[1] = b1_expand<1>(w32); bf[2] = b1_expand<2>(w32); bf[3] = b1_expand<3>(w32);
                     } else {
-                        const uint32_t w4 = w32 >> 4;
-                        bf[0] = t2_lo(w32); bf[1] = t2_hi(w32); bf[2] = t2_lo(w4); bf[3] = t2_hi(w4);
+                        bf[0] = b1_expand<4>(w32); bf[1] = b1_expand<5>(w32); bf[2] = b1_expand<6>(w32); bf[3] = b1_expand<7>(w32);
                     }
-                    if constexpr (MASKED && KTAIL) {
-#pragma unroll
-                        for (int d = 0; d < 4; ++d) {
-                            const int valid = kend - (kstep + (lane >> 4) * 16 + 4 * d);
-                            const uint32_t keep = valid >= 4 ? 0xFFFFFFFFu : (valid <= 0 ? 0u : (1u << (8 * valid)) - 1u);
-                            bf[d] = (int)((uint32_t)bf[d] & keep);
-                        }
-                    } else if constexpr (MASKED) {  // kend is a multiple of 16 here
-                        const bool keep = kstep + (lane >> 4) * 16 < kend;
-#pragma unroll
-                        for (int d = 0; d < 4; ++d) bf[d] = keep ? bf[d] : 0;
-                    }
-#pragma unroll
-                    for (int c = 0; c < P; ++c)
-#pragma unroll
-                        for (int i = 0; i < RM; ++i)
-                            acc[c][i][jn] =
-                                __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af[slot][h][c][i], acc[c][i][jn], 0, 0, 0);
+                } else {
+                    const uint32_t w4 = w32 >> 4;
+                    bf[0] = t2_lo(w32); bf[1] = t2_hi(w32); bf[2] = t2_lo(w4); bf[3] = t2_hi(w4);
                 }
+                if constexpr (MASKED && KTAIL) {
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        const int valid = kend - (kstep + (lane >> 4) * 16 + 4 * d);
+                        const uint32_t keep = valid >= 4 ? 0xFFFFFFFFu : (valid <= 0 ? 0u : (1u << (8 * valid)) - 1u);
+                        bf[d] = (int)((uint32_t)bf[d] & keep);
+                    }
+                } else if constexpr (MASKED) {  // kend is a multiple of 16 here
+                    const bool keep = kstep + (lane >> 4) * 16 < kend;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) bf[d] = keep ? bf[d] : 0;
+                }
+#pragma unroll
+                for (int c = 0; c < P; ++c)
+#pragma unroll
+                    for (int i = 0; i < RM; ++i)
+                        acc[c][i][jn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af[slot][c][i], acc[c][i][jn], 0, 0, 0);
             }
         }
     };
@@ -537,13 +535,16 @@ constexpr Tile kTiles[] = {
     {2, 1, 1, 4, "32x64 w1x4 r2x1"},   // 2
     {1, 2, 2, 2, "32x64 w2x2 r1x2"},   // 3
     {1, 1, 2, 2, "32x32 w2x2 r1x1"},   // 4
-    {2, 2, 2, 2, "64x64 w2x2 r2x2"},   // 5
-    {1, 2, 4, 1, "64x32 w4x1 r1x2"},   // 6
+    {4, 1, 1, 4, "64x64 w1x4 r4x1"},   // 5
+    {8, 1, 1, 4, "128x64 w1x4 r8x1"},  // 6
     {2, 4, 2, 2, "64x128 w2x2 r2x4"},  // 7
-    {4, 2, 2, 2, "128x64 w2x2 r4x2"},  // 8
-    {4, 4, 2, 2, "128x128 w2x2 r4x4"}, // 9
+    {4, 2, 1, 4, "64x128 w1x4 r4x2"},  // 8
+    {2, 2, 1, 4, "32x128 w1x4 r2x2"},  // 9
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
+
+// Register budget of a tile: accumulators plus double-buffered activation fragments (in 32-bit registers).
+constexpr bool tile_fits(int parts, int rm, int rn) { return parts * rm * rn * 4 + 2 * parts * rm * 4 <= 256; }
 
 inline long long cdivl(long long a, long long b) { return (a + b - 1) / b; }
 
@@ -555,18 +556,24 @@ KernelFn pick_sliced(bool sliced) {
                   : gemm_kernel<WBITS, P, RM, RN, WM, WN, false, false>;
 }
 
+template <int WBITS, int P, int RM, int RN, int WM, int WN>
+KernelFn pick_fit(bool sliced) {
+    if constexpr (tile_fits(P, RM, RN)) return pick_sliced<WBITS, P, RM, RN, WM, WN>(sliced);
+    else return nullptr;
+}
+
 template <int WBITS, int P>
 KernelFn pick_tile(int id, bool sliced) {
     switch (id) {
-        case 1: return pick_sliced<WBITS, P, 1, 1, 1, 4>(sliced);
-        case 2: return pick_sliced<WBITS, P, 2, 1, 1, 4>(sliced);
-        case 3: return pick_sliced<WBITS, P, 1, 2, 2, 2>(sliced);
-        case 4: return pick_sliced<WBITS, P, 1, 1, 2, 2>(sliced);
-        case 5: return pick_sliced<WBITS, P, 2, 2, 2, 2>(sliced);
-        case 6: return pick_sliced<WBITS, P, 1, 2, 4, 1>(sliced);
-        case 7: return pick_sliced<WBITS, P, 2, 4, 2, 2>(sliced);
-        case 8: return pick_sliced<WBITS, P, 4, 2, 2, 2>(sliced);
-        case 9: return pick_sliced<WBITS, P, 4, 4, 2, 2>(sliced);
+        case 1: return pick_fit<WBITS, P, 1, 1, 1, 4>(sliced);
+        case 2: return pick_fit<WBITS, P, 2, 1, 1, 4>(sliced);
+        case 3: return pick_fit<WBITS, P, 1, 2, 2, 2>(sliced);
+        case 4: return pick_fit<WBITS, P, 1, 1, 2, 2>(sliced);
+        case 5: return pick_fit<WBITS, P, 4, 1, 1, 4>(sliced);
+        case 6: return pick_fit<WBITS, P, 8, 1, 1, 4>(sliced);
+        case 7: return pick_fit<WBITS, P, 2, 4, 2, 2>(sliced);
+        case 8: return pick_fit<WBITS, P, 4, 2, 1, 4>(sliced);
+        case 9: return pick_fit<WBITS, P, 2, 2, 1, 4>(sliced);
         default: return nullptr;
     }
 }
@@ -598,17 +605,23 @@ FinishFn pick_finish(int parts) {
     return finish_kernel<3>;
 }
 
-// Tile choice: a pure function of (wbits, parts, m, n, k). Prefers the largest tile that still gives every CU a
-// workgroup (256 CUs on MI355X), else the one with the most workgroups.
+// Tile choice: a pure function of (wbits, parts, m, n, k), from MI355X sweeps over the BASELINE shapes. Large M
+// favours wide-N tiles with two activation tiles per wavefront; small and medium M favour 32x32 / 16x64 tiles with
+// many workgroups. Among the candidates for the M range, the first that gives every CU a workgroup wins, else the
+// one with the most workgroups.
 int choose_tile(int wbits, int parts, long long m, long long n, long long k) {
-    (void)wbits; (void)parts; (void)k;
-    static const int order[] = {9, 8, 7, 5, 2, 3, 6, 4, 1};
+    (void)wbits; (void)k;
+    static const int large_m[] = {9, 8, 2, 4};
+    static const int small_m[] = {4, 1, 2};
+    const int *order = m >= 512 ? large_m : small_m;
+    const int count = m >= 512 ? 4 : 3;
     int best = 1;
     long long best_wg = -1;
-    for (int id : order) {
+    for (int i = 0; i < count; ++i) {
+        const int id = order[i];
         const Tile &t = kTiles[id - 1];
+        if (!tile_fits(parts, t.rm, t.rn)) continue;
         const long long bm = t.wm * t.rm * 16, bn = t.wn * t.rn * 16;
-        if (bm > 16 && bm >= 2 * m) continue;  // mostly padding rows
         const long long wgs = cdivl(m, bm) * cdivl(n, bn);
         if (wgs >= 256) return id;
         if (wgs > best_wg) { best_wg = wgs; best = id; }
@@ -654,6 +667,9 @@ static int resolve(int wbits, int parts, int64_t m, int64_t n, int64_t k, int sp
     if (config < 0 || config > kNumTiles) return kea::fail(KEA_EINVAL, "unknown config id");
     if (split_k < 0) return kea::fail(KEA_EINVAL, "split_k must be >= 0");
     int id = config ? config : choose_tile(wbits, parts, m, n, k);
+    if (!tile_fits(parts, kTiles[id - 1].rm, kTiles[id - 1].rn))
+        return kea::fail(KEA_EINVAL, std::string("tile ") + kTiles[id - 1].name + " does not fit " +
+                                         std::to_string(parts) + " activation parts");
     const long long J = wbits == 1 ? cdivl(k, 128) : cdivl(k, 64);
     const long long quads = cdivl(J, 4);
     int s = split_k ? split_k : choose_split(wbits, parts, m, n, k, id);
