@@ -123,6 +123,24 @@ int kea_lowbit_gemm(int wbits,
                     int64_t m, int flags, int split_k, int config,
                     void *workspace_dev, int64_t workspace_bytes, void *stream);
 
+/* Exact deferred split-K: the K range is cut into `split` slices (split >= 1, at most ceil(J/4) where J is the number
+ * of native words per lane) and slice z writes its exact int32 partial accumulators to
+ * slices_dev[((z * parts + c) * m + row) * n + col] (int32 [split][parts][m][n], 16-byte aligned). No scale is read.
+ * Replaces the XCHG 5 slice kernels (kk/binary/kernels_exact.py:24-54) driven by hybrid_exact.dot_slices
+ * (kk/binary/hybrid_exact.py:53-72), whose slices are packed int64 words instead. */
+int kea_lowbit_gemm_slices(int wbits, const int8_t *q_dev, int64_t part_stride, int64_t ldq, int parts,
+                           const uint32_t *w_dev, int64_t n, int64_t k, int64_t m, int split, int config,
+                           int32_t *slices_dev, void *stream);
+
+/* Sums slices int32 [split][parts][m][n] in slice order (exact) and applies the epilogue of kea_lowbit_gemm (same
+ * scale, bias, flag and output arguments); bitwise the unsplit kea_lowbit_gemm result. Replaces the integer finish
+ * of the reference's exact row epilogue (kk/binary/row_exact.py:69-96) for the projection value. */
+int kea_lowbit_slices_finish(const int32_t *slices_dev, int split, int parts, int64_t m, int64_t n,
+                             const void *qs_dev, int qs_dtype, int64_t qs_stride,
+                             const void *wscale_dev, int ws_dtype, const void *bias_dev, int bias_dtype,
+                             void *y_dev, int y_dtype, int64_t ldy, int32_t *acc_out_dev, int64_t acc_ld,
+                             int flags, void *stream);
+
 /* Workspace bytes kea_lowbit_gemm needs for these arguments (0 when split_k resolves to 1). */
 int64_t kea_lowbit_gemm_workspace(int wbits, int parts, int64_t m, int64_t n, int64_t k, int64_t ws_group,
                                   int split_k, int config);

@@ -789,4 +789,88 @@ int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq
     return KEA_OK;
 }
 
+int kea_lowbit_gemm_slices(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts,
+                           const uint32_t *w, int64_t n, int64_t k, int64_t m, int split, int config,
+                           int32_t *slices, void *stream) {
+    if (split < 1) return kea::fail(KEA_EINVAL, "split must be >= 1");
+    int tile, s, qps;
+    int rc = resolve(wbits, parts, m, n, k, split, config, &tile, &s, &qps);
+    if (rc != KEA_OK) return rc;
+    if (k & 15) return kea::fail(KEA_EINVAL, "deferred slices need k % 16 == 0");
+    if (s != split)
+        return kea::fail(KEA_EINVAL, "split does not cut the K range into that many non-empty slices (at most " +
+                                         std::to_string(s) + ")");
+    if (m == 0) return KEA_OK;
+    if (!q || !w || !slices) return kea::fail(KEA_EINVAL, "q, w and slices are required");
+    if (ldq < k) return kea::fail(KEA_EINVAL, "ldq < k");
+    if (parts > 1 && part_stride < m * ldq) return kea::fail(KEA_EINVAL, "part_stride < m * ldq (parts overlap)");
+    if (((uintptr_t)q & 15) || (ldq & 15) || (parts > 1 && (part_stride & 15)))
+        return kea::fail(KEA_EALIGN, "q needs 16-byte aligned rows");
+    if (((uintptr_t)w & 15) || ((uintptr_t)slices & 15)) return kea::fail(KEA_EALIGN, "w and slices must be 16-byte aligned");
+    if ((int64_t)(parts - 1) * part_stride + m * ldq > (int64_t)INT32_MAX)
+        return kea::fail(KEA_EINVAL, "q spans more than 2 GiB: split the call along M");
+    Params p = {};
+    p.q = q; p.part_stride = part_stride; p.ldq = ldq;
+    p.w = w;
+    p.M = (int)m; p.N = (int)n; p.K = (int)k;
+    p.J = (int)(wbits == 1 ? cdivl(k, 128) : cdivl(k, 64));
+    p.NT = (int)cdivl(n, 16);
+    p.quads_per_slice = qps;
+    p.slices = slices;
+    p.slice_vec = (n % 4 == 0);
+    const Tile &t = kTiles[tile - 1];
+    const int bm = t.wm * t.rm * 16, bn = t.wn * t.rn * 16;
+    const StageShape shape = stage_shape(wbits, parts, t.rm, t.rn, t.wm, t.wn);
+    const long long words_per_wg = std::min<long long>(4LL * qps, (long long)p.J);
+    const int lds_bytes = std::min(shape.ns, (int)cdivl(words_per_wg, shape.sw)) * shape.stage_bytes;
+    KernelFn fn = pick_kernel(wbits, parts, tile, true, false);
+    if (lds_bytes > 65536) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
+        if (e != hipSuccess) return kea::fail((int)e, std::string("LDS attribute refused: ") + hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(fn, dim3((unsigned)cdivl(n, bn), (unsigned)cdivl(m, bm), (unsigned)s), dim3(t.wm * t.wn * 64),
+                       lds_bytes, (hipStream_t)stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("slice launch failed: ") + hipGetErrorString(e));
+    return KEA_OK;
+}
+
+int kea_lowbit_slices_finish(const int32_t *slices, int split, int parts, int64_t m, int64_t n, const void *qs,
+                             int qs_dtype, int64_t qs_stride, const void *wscale, int ws_dtype, const void *bias,
+                             int bias_dtype, void *y, int y_dtype, int64_t ldy, int32_t *acc_out, int64_t acc_ld,
+                             int flags, void *stream) {
+    if (split < 1 || parts < 1 || parts > 3 || m < 0 || n < 1 || m > INT32_MAX || n > INT32_MAX)
+        return kea::fail(KEA_EINVAL, "bad sizes");
+    if (flags & ~(KEA_FLAG_SILU | KEA_FLAG_ORDER)) return kea::fail(KEA_EINVAL, "unknown flags");
+    if (qs_dtype != KEA_F32 && qs_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "qs dtype must be f32 or f16");
+    if (ws_dtype != KEA_F32 && ws_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "wscale dtype must be f32 or f16");
+    if (bias && bias_dtype != KEA_F32 && bias_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "bias dtype must be f32 or f16");
+    if (y && y_dtype != KEA_F32 && y_dtype != KEA_F16 && y_dtype != KEA_BF16)
+        return kea::fail(KEA_EINVAL, "y dtype must be f32, f16 or bf16");
+    if (y && ldy < n) return kea::fail(KEA_EINVAL, "ldy < n");
+    if (acc_out && acc_ld < n) return kea::fail(KEA_EINVAL, "acc_ld < n");
+    if (m == 0) return KEA_OK;
+    if (!slices || !qs || !wscale) return kea::fail(KEA_EINVAL, "slices, qs and wscale are required");
+    if (!y && !acc_out) return kea::fail(KEA_EINVAL, "nothing to write: y and acc_out are both NULL");
+    if ((uintptr_t)slices & 15) return kea::fail(KEA_EALIGN, "slices must be 16-byte aligned");
+    Params p = {};
+    p.qs = qs; p.qs_stride = qs_stride; p.qs_dtype = qs_dtype;
+    p.ws = wscale; p.ws_dtype = ws_dtype;
+    p.bias = bias; p.bias_dtype = bias_dtype;
+    p.y = y; p.ldy = ldy; p.y_dtype = y_dtype;
+    p.acc = acc_out; p.acc_ld = acc_ld;
+    p.M = (int)m; p.N = (int)n;
+    p.flags = flags;
+    p.slices = const_cast<int32_t *>(slices);
+    p.slice_vec = (n % 4 == 0);
+    const int esz = (y_dtype == KEA_F32) ? 4 : 2;
+    p.y_vec = y && (ldy % 4 == 0) && ((uintptr_t)y % (4 * esz) == 0);
+    p.acc_vec = acc_out && (acc_ld % 4 == 0) && ((uintptr_t)acc_out % 16 == 0);
+    const long long work = m * cdivl(n, 4);
+    hipLaunchKernelGGL(pick_finish(parts), dim3((unsigned)cdivl(work, 256)), dim3(256), 0, (hipStream_t)stream, p, split);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("finish launch failed: ") + hipGetErrorString(e));
+    return KEA_OK;
+}
+
 }  // extern "C"

@@ -53,6 +53,8 @@ def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscal
     device = q.device
     _on(device, qs, words, wscale, bias, y, acc_out)
     L = _hip.lib()
+    if config is not None and not hasattr(config, "tile"):
+        config = None  # a reference tile tuple (its RTX 5090 tiling): accepted, results never depend on tiles
     tile = 0 if config is None else int(config.tile)
     split = 0 if config is None else int(config.split)
     need = L.kea_lowbit_gemm_workspace(wbits, parts, max(m, 1), n, k, ws_group, split, tile)
@@ -70,6 +72,57 @@ def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscal
         m, int(silu) | (2 * int(order)), split, tile,
         _hip.ptr(workspace), need, _hip.stream_handle(device))
     _hip.check(rc, "kea_lowbit_gemm")
+
+
+def gemm_slices(wbits: int, q: Tensor, words: Tensor, n: int, k: int, slices: Tensor, *, m: int | None = None,
+                config=None) -> None:
+    """Exact deferred split-K: slices int32 [S, P, m, N] <- the int32 K-slice sums (S = slices.shape[0])."""
+    if q.dtype != torch.int8 or q.dim() != 3 or q.stride(2) != 1 or q.stride(1) != q.shape[2]:
+        raise ValueError("q must be int8 [P, M, ldq] with contiguous rows")
+    parts, rows, ldq = q.shape
+    m = rows if m is None else m
+    if m > rows:
+        raise ValueError(f"m = {m} exceeds the {rows} rows of q")
+    if (slices.dtype != torch.int32 or slices.dim() != 4 or tuple(slices.shape[1:]) != (parts, m, n)
+            or not slices.is_contiguous()):
+        raise ValueError(f"slices must be contiguous int32 [S, {parts}, {m}, {n}]")
+    _on(q.device, words, slices)
+    tile = 0 if config is None or not hasattr(config, "tile") else int(config.tile)
+    rc = _hip.lib().kea_lowbit_gemm_slices(wbits, q.data_ptr(), q.stride(0), ldq, parts, words.data_ptr(), n, k, m,
+                                           slices.shape[0], tile, slices.data_ptr(), _hip.stream_handle(q.device))
+    _hip.check(rc, "kea_lowbit_gemm_slices")
+
+
+def slices_finish(slices: Tensor, qs: Tensor, wscale: Tensor, bias: Tensor | None, y: Tensor | None = None,
+                  acc_out: Tensor | None = None, *, silu: bool = False, order: int = 0) -> None:
+    """y[:m] and/or acc_out from exact int32 slices [S, P, m, N]: slice sums in slice order, then the GEMM epilogue
+    (bitwise the unsplit GEMM's result)."""
+    if slices.dtype != torch.int32 or slices.dim() != 4 or not slices.is_contiguous():
+        raise ValueError("slices must be contiguous int32 [S, P, M, N]")
+    split, parts, m, n = slices.shape
+    if qs.dim() != 2 or qs.shape[0] != parts or qs.shape[1] < m or qs.stride(1) != 1 or qs.dtype not in _SCALE_DTYPES:
+        raise ValueError(f"qs must be f32/f16 [{parts}, >= {m}] with unit column stride")
+    if wscale.dtype not in _SCALE_DTYPES or not wscale.is_contiguous() or wscale.numel() != n:
+        raise ValueError("weight scales must be contiguous f32 or f16 [N]")
+    if bias is not None and (bias.dtype not in _SCALE_DTYPES or not bias.is_contiguous() or bias.numel() != n):
+        raise ValueError("bias must be contiguous f32 or f16 [N]")
+    if y is None and acc_out is None:
+        raise ValueError("nothing to compute: y and acc_out are both None")
+    if y is not None and (y.dim() != 2 or y.shape[0] < m or y.shape[1] < n or y.stride(1) != 1):
+        raise ValueError(f"y must be a row-major [>= {m}, >= {n}] view")
+    if acc_out is not None and (acc_out.dtype != torch.int32 or tuple(acc_out.shape[:2]) != (parts, m)
+                                or acc_out.shape[2] < n or acc_out.stride(2) != 1
+                                or acc_out.stride(0) != m * acc_out.stride(1)):
+        raise ValueError(f"acc_out must be int32 [{parts}, {m}, >= {n}] with dense part planes")
+    _on(slices.device, qs, wscale, bias, y, acc_out)
+    rc = _hip.lib().kea_lowbit_slices_finish(
+        slices.data_ptr(), split, parts, m, n, qs.data_ptr(), _hip.dtype_code(qs.dtype), qs.stride(0),
+        wscale.data_ptr(), _hip.dtype_code(wscale.dtype), _hip.ptr(bias),
+        _hip.dtype_code(bias.dtype) if bias is not None else 0,
+        _hip.ptr(y), _hip.dtype_code(y.dtype) if y is not None else 0, y.stride(0) if y is not None else 0,
+        _hip.ptr(acc_out), acc_out.stride(1) if acc_out is not None else 0,
+        int(silu) | (2 * int(order)), _hip.stream_handle(slices.device))
+    _hip.check(rc, "kea_lowbit_slices_finish")
 
 
 def round_up(v: int, multiple: int) -> int:

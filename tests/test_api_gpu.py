@@ -1,0 +1,239 @@
+"""GPU tests of the operator and provider API: the reference's GPU contract tests (tests/test_kernels_gpu.py:30-105)
+restated for this build, plus the provider seam, the ternary modules and the exact deferred split-K slices.
+
+Bars: the P-part dot against FP64 sum_c acc_c * s_c * alpha from exact integer accumulators, rtol 2e-6 / atol 1e-6;
+linear against dense FP64 relative Frobenius error < 2e-2 / 1e-4 / 1e-6 for P = 1 / 2 / 3; PackedLinear < 1e-5;
+exact split-K slices + finish bitwise equal to the unsplit GEMM; provider calls bitwise equal to the layer's own.
+Integer accumulators come from the pinned CPU oracle (exact int32 sums, the reference test's int64 formula).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from kea_kernels import formats, lowbit
+from kea_kernels.binary import bits, configs, hybrid_exact, layer as L, layer_parts, provider
+from kea_kernels.binary.kernels import GemmConfig
+from kea_kernels.ternary import encoder4, fused_kernels, runtime
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1024, 1024), (4096, 1024), (1024, 4096), (3072, 1024)]
+
+
+def _weights(n, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    signs = torch.where(torch.rand(n, k, generator=g) < 0.5, -1, 1).to(torch.int8)
+    scale = torch.rand(n, generator=g) * 0.02 + 0.001
+    return bits.pack_signs(signs), scale.float(), signs
+
+
+def _exact_epilogue(q, qs, codes, k, scale, parts):
+    """FP64 sum_c acc_c * s_c * alpha, acc from the oracle's exact int32 GEMM."""
+    acc = O.b1_gemm(q[:parts, :, :].cpu().numpy(), codes.numpy(), k).astype(np.float64)
+    s = qs[:parts].cpu().double().numpy()
+    y = sum(acc[c] * s[c][:, None] for c in range(parts))
+    return torch.from_numpy(y * scale.double().numpy()[None, :])
+
+
+@pytest.mark.parametrize("parts", [1, 2, 3])
+@pytest.mark.parametrize("n,k", SHAPES)
+@pytest.mark.parametrize("m", [38, 126, 300])
+@torch.inference_mode()
+def test_b1_dot_equals_exact_integer_reference(parts, n, k, m):
+    codes, scale, _ = _weights(n, k, seed=n + k + m)
+    layer = layer_parts.LAYERS[parts].prepare(codes, scale, None, k, "cuda")
+    assert layer.fast
+    x = torch.randn(m, k, device="cuda")
+    q, qs, ldq = L.quantize(x, (0, x.stride(0), x.stride(1), m), m, k)
+    y = torch.empty(m, n, device="cuda")
+    layer.dot(q[:parts], qs[:parts], ldq, m, y, parts=parts)
+    torch.cuda.synchronize()
+    ref = _exact_epilogue(q, qs, codes, k, scale, parts)
+    torch.testing.assert_close(y.cpu().double(), ref, rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("parts,tol", [(1, 2e-2), (2, 1e-4), (3, 1e-6)])
+@torch.inference_mode()
+def test_linear_matches_dense_fp64_within_activation_precision(parts, tol):
+    n, k, m = 1024, 4096, 126
+    codes, scale, _ = _weights(n, k, seed=7)
+    layer = layer_parts.LAYERS[parts].prepare(codes, scale, None, k, "cuda")
+    x = torch.randn(2, m // 2, k, device="cuda")
+    y = layer.linear(x).cpu().double()
+    ref = x.cpu().double() @ bits.dense_weight(codes, scale, k).t()
+    err = (y - ref).norm() / ref.norm()
+    assert err < tol
+
+
+@torch.inference_mode()
+def test_conv_is_the_transposed_linear():
+    n, k, b, t = 256, 512, 2, 37
+    codes, scale, _ = _weights(n, k, seed=11)
+    bias = torch.randn(n)
+    layer = L.Int8MmaLayer.prepare(codes, scale, bias, k, "cuda")
+    x = torch.randn(b, k, t, device="cuda")
+    yc = layer.conv(x)
+    assert yc.shape == (b, n, t)
+    yl = layer.linear(x.transpose(1, 2).contiguous())
+    assert torch.equal(yc, yl.transpose(1, 2))
+    ref = x.transpose(1, 2).cpu().double() @ bits.dense_weight(codes, scale, k).t() + bias.double()
+    assert (yc.transpose(1, 2).cpu().double() - ref).norm() / ref.norm() < 1e-6
+
+
+@pytest.mark.parametrize("parts", [2, 3])
+@pytest.mark.parametrize("m,n,k", [(38, 1024, 1024), (38, 1024, 4096), (126, 1024, 4096)])
+@torch.inference_mode()
+def test_exact_split_k_finish_equals_in_kernel_finish(parts, m, n, k):
+    """Deferred integer slices finished by finish_slices are bitwise the unsplit in-kernel epilogue."""
+    codes, scale, _ = _weights(n, k, seed=m * n + k)
+    bias = torch.randn(n) * 0.1
+    layer = layer_parts.LAYERS[parts].prepare(codes, scale, bias, k, "cuda")
+    xx = torch.randn(1, m, k, device="cuda")
+    q, qs = layer_parts.m1_quantize_parts(xx, parts)
+    y = torch.empty(1, m, n, device="cuda")
+    layer.dot(q, qs, k, m, y.view(m, n), config=GemmConfig(configs.choose(m, n, k, parts).tile, 1), parts=parts)
+    auto = hybrid_exact.choose_exact_deferred(m, n, k, parts)
+    quads = -(-(-(-k // 128)) // 4)  # groups of four native words along K: the most slices a call can have
+    for cfg in [c for c in (auto, GemmConfig(4, 2), GemmConfig(1, 4), GemmConfig(4, 8)) if c and c.split <= quads]:
+        slices = torch.empty(cfg.split, parts, m, n, device="cuda", dtype=torch.int32)
+        hybrid_exact.dot_slices(layer, q, qs, k, m, slices, cfg)
+        value = hybrid_exact.ExactDeferredProjection(slices, layer.scale, layer.bias, cfg.split, (1, m, n), qs)
+        exact = value.finish()
+        acc = torch.empty(parts, m, n, device="cuda", dtype=torch.int32)
+        hybrid_exact.finish_slices(value, None, acc)
+        torch.cuda.synchronize()
+        assert torch.equal(exact, y), cfg
+        ref_acc = O.b1_gemm(q.cpu().numpy(), codes.numpy(), k)
+        assert np.array_equal(acc.cpu().numpy(), ref_acc), cfg
+    with pytest.raises(RuntimeError, match="integer slices"):
+        value.partial
+
+
+@torch.inference_mode()
+def test_project_deferred_matches_project():
+    n, k, m = 1024, 4096, 38
+    codes, scale, _ = _weights(n, k, seed=5)
+    layer = L.Int8MmaLayer.prepare(codes, scale, None, k, "cuda")
+    x = torch.randn(1, m, k, device="cuda")
+    value = hybrid_exact.project_deferred(layer, x, config=GemmConfig(4, 4))
+    assert isinstance(value, hybrid_exact.ExactDeferredProjection)
+    assert torch.equal(value.finish(), layer.project(x))
+
+
+@torch.inference_mode()
+def test_slices_entry_points_reject_bad_arguments():
+    codes, scale, _ = _weights(64, 256, seed=1)
+    layer = L.Int8MmaLayer.prepare(codes, scale, None, 256, "cuda")
+    q = torch.zeros(3, 8, 256, device="cuda", dtype=torch.int8)
+    qs = torch.ones(3, 8, device="cuda")
+    with pytest.raises(ValueError, match="slices"):
+        hybrid_exact.dot_slices(layer, q, qs, 256, 8, torch.empty(2, 3, 8, 32, device="cuda", dtype=torch.int32))
+    with pytest.raises(ValueError, match="split"):  # 256 = one group of four words: no second slice exists
+        hybrid_exact.dot_slices(layer, q, qs, 256, 8, torch.empty(2, 3, 8, 64, device="cuda", dtype=torch.int32))
+
+
+@pytest.mark.parametrize("mode,parts", [("bf16x3", 3), ("x2", 2), ("x1", 1)])
+@torch.inference_mode()
+def test_ternary_packed_linear_matches_dense_fp64(mode, parts):
+    n, k, m = 1024, 1024, 64
+    g = torch.Generator().manual_seed(3)
+    codes = torch.randint(-1, 2, (n, k), generator=g, dtype=torch.int8)
+    scale = torch.rand(n, generator=g) * 0.02 + 0.001
+    module = runtime.PackedLinear(formats.pack_ternary(codes), scale.float(), k, mode=mode).cuda()
+    x = torch.randn(m, k, device="cuda")
+    y = module(x).cpu().double()
+    ref = x.cpu().double() @ (codes.double() * scale.double()[:, None]).t()
+    tol = {3: 1e-5, 2: 1e-4, 1: 2e-2}[parts]
+    assert (y - ref).norm() / ref.norm() < tol
+
+
+@torch.inference_mode()
+def test_ternary_provider_fused_norm_silu_and_conv():
+    n, k, b, t = 512, 1024, 2, 40
+    g = torch.Generator().manual_seed(9)
+    codes = torch.randint(-1, 2, (n, k), generator=g, dtype=torch.int8)
+    scale = torch.rand(n, generator=g) * 0.02 + 0.001
+    bias = torch.randn(n, generator=g)
+    mod = runtime.PackedPointwiseConv1d(formats.pack_ternary(codes), scale, k, bias).cuda()
+    norm = torch.nn.LayerNorm(k)
+    with torch.no_grad():
+        norm.weight.copy_(torch.rand(k, generator=g) + 0.5)
+        norm.bias.copy_(torch.randn(k, generator=g) * 0.1)
+    dnorm = torch.nn.LayerNorm(k).cuda()
+    dnorm.load_state_dict(norm.state_dict())
+    proj = encoder4.ExpandedProjection()
+    assert proj.bytes == 0
+    x = torch.randn(b, k, t, device="cuda")
+    y = proj(x, mod, conv=True, components=3, activation="silu", norm=dnorm, input_activation="silu")
+    assert y.shape == (b, n, t)
+    z = torch.nn.functional.silu(norm(x.cpu().transpose(1, 2)).double())
+    ref = torch.nn.functional.silu(z @ (codes.double() * scale.double()[:, None]).t() + bias.double())
+    assert (y.transpose(1, 2).cpu().double() - ref).norm() / ref.norm() < 1e-5
+    same = fused_kernels.int8_matmul(x, mod, True, 3, "silu", dnorm, None, "silu")
+    assert torch.equal(y, same)
+
+
+@torch.inference_mode()
+def test_binary_provider_table_and_part_count_on_gpu():
+    n, k = 256, 1024
+    layers = {}
+    for i, name in enumerate(["b.0.self_attn.linear_q", "b.0.self_attn.linear_k", "b.0.self_attn.linear_v",
+                              "b.0.feed_forward1.linear1"]):
+        codes, scale, _ = _weights(n * (1 + 3 * ("linear1" in name)), k, seed=20 + i)
+        layers[name] = (codes, scale, torch.randn(codes.shape[0]) if "linear1" in name else None, "linear", k)
+    table, modules = provider.prepare_table(layers, layer_parts.Int8MmaPartsLayer, "cuda")
+    proj = provider.BinaryProjection(table)
+    x = torch.randn(2, 19, k, device="cuda")
+    q, kk, v = (modules[f"b.0.self_attn.{s}"] for s in provider.QKV)
+    fused = torch.cat([q.packed_t, kk.packed_t, v.packed_t], 1)
+    handle = type("H", (), {"packed_t": fused})()
+    y = proj(x, handle)
+    assert y.shape == (2, 19, 3 * n)
+    assert torch.equal(proj(x, kk), y[..., n:2 * n])
+    qkv_layer = table.entries[0].layer
+    assert torch.equal(y, qkv_layer.project(x))
+    ff = modules["b.0.feed_forward1.linear1"]
+    ff_codes, ff_scale, ff_bias = layers["b.0.feed_forward1.linear1"][:3]
+    ref = x.cpu().double() @ bits.dense_weight(ff_codes, ff_scale, k).t() + ff_bias.double()
+    for parts, tol in [(1, 2e-2), (2, 1e-4), (3, 1e-6)]:
+        yp = provider.PartCount(proj, parts)(x, ff, components=3)
+        assert (yp.cpu().double() - ref).norm() / ref.norm() < tol
+    assert table.weight_bytes() == sum(e.layer.weight_bytes() for e in table.entries)
+
+
+def test_layer_errors_match_the_reference_contract():
+    codes, scale, _ = _weights(64, 128, seed=2)
+    with pytest.raises(ValueError, match="GPU"):
+        L.Int8MmaLayer.prepare(codes, scale, None, 128, "cpu")
+    layer = L.Int8MmaLayer.prepare(codes, scale, None, 128, "cuda")
+    with pytest.raises(ValueError, match="input"):
+        layer.linear(torch.randn(4, 100, device="cuda"))
+    with pytest.raises(ValueError, match="FP32"):
+        layer.linear(torch.randn(4, 128, device="cuda", dtype=torch.float64))
+    q = torch.zeros(3, 4, 136, device="cuda", dtype=torch.int8)[:, :, 8:]
+    with pytest.raises(ValueError, match="aligned"):
+        layer.dot(q, torch.ones(3, 4, device="cuda"), 128, 4, torch.empty(4, 64, device="cuda"))
+    with pytest.raises(RuntimeError, match="inference only"):
+        layer.linear(torch.randn(4, 128, device="cuda", requires_grad=True))
+
+
+@torch.inference_mode()
+def test_output_dtypes_through_the_layer():
+    n, k, m = 512, 1024, 64
+    codes, scale, _ = _weights(n, k, seed=4)
+    layer = L.Int8MmaLayer.prepare(codes, scale, None, k, "cuda")
+    x = torch.randn(m, k, device="cuda")
+    y32 = layer.linear(x)
+    for dt in (torch.float16, torch.bfloat16):
+        y = layer.linear(x, out_dtype=dt)
+        assert y.dtype == dt and torch.equal(y, y32.to(dt))
+
+
+@torch.inference_mode()
+def test_quantize_zero_rows_and_lowbit_zero_m():
+    x = torch.empty(0, 64, device="cuda")
+    q, qs, ldq = lowbit.quantize(x, (0, 64, 1, 1), 0, 64, 3)
+    assert q.shape == (3, 0, 64) and qs.shape == (3, 0)
