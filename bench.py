@@ -145,6 +145,77 @@ def traffic_from_profiles():
         return None
 
 
+# --- secondary measurements (python bench.py --suite): BASELINE.json configs 2-4 and the reference's tuned shapes ---
+REF_SHAPES = [(n, k, m) for n, k in [(1024, 1024), (1024, 4096), (2048, 1024), (3072, 1024), (4096, 1024)]
+              for m in (38, 126, 256, 368)]  # kk/binary/configs.py:17-36 (RTX 5090 timings, three parts, FP32 out)
+
+
+def _suite_case(wbits, parts, m, n, k, *, scale_dtype, out_dtype, seed, reps=200):
+    """Per-launch microseconds of the library's default configuration, inputs resident, HIP-graph replay."""
+    import torch
+    from kea_kernels import formats, lowbit
+    from kea_kernels.binary import bits, kernels
+    g = torch.Generator().manual_seed(seed)
+    dev = torch.device("cuda", 0)
+    ldq = -(-k // 16) * 16
+    q = torch.randint(-127, 128, (parts, m, ldq), generator=g, dtype=torch.int8).to(dev)
+    qs = (torch.rand(parts, m, generator=g) * 0.01 + 1e-3).to(scale_dtype).to(dev)
+    if wbits == 1:
+        codes = bits.pack_signs(torch.where(torch.rand(n, k, generator=g) < 0.5, -1, 1).to(torch.int8))
+    else:
+        codes = formats.pack_ternary(torch.randint(-1, 2, (n, k), generator=g, dtype=torch.int8))
+    words = kernels.relayout_codes(codes, k, wbits).to(dev)
+    alpha = (torch.rand(n, generator=g) * 0.09 + 0.01).to(scale_dtype).to(dev)
+    y = torch.empty(m, n, dtype=out_dtype, device=dev)
+    stream = torch.cuda.Stream(dev)
+
+    def step():
+        lowbit.gemm(wbits, q, qs, words, n, k, alpha, None, y, None)
+
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(100):
+            step()
+    with torch.cuda.stream(stream):
+        graph.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps // 100):
+            graph.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1000 / (reps // 100 * 100)
+    esz = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
+    ops = 2 * m * n * k * parts
+    nbytes = (m * k * parts + n * (-(-k * wbits // 8)) + esz[scale_dtype] * (n + parts * m) + esz[out_dtype] * m * n)
+    t_roof = max(ops / (PEAK_INT8_TOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9))
+    return {"wbits": wbits, "parts": parts, "M": m, "N": n, "K": k, "us": round(us, 3),
+            "tops": round(ops / us / 1e6, 2), "gbs": round(nbytes / us / 1e3, 1),
+            "bound": "mfma" if ops / (PEAK_INT8_TOPS * 1e12) >= nbytes / (PEAK_HBM_GBS * 1e9) else "hbm",
+            "roofline_frac": round(t_roof / (us * 1e-6), 4)}
+
+
+def suite() -> None:
+    """One JSON line per case: configs 2-4 of BASELINE.json and the reference's tuned (N, K, M) shapes at three
+    activation parts with FP32 scales and output (the arithmetic its in-source timings use)."""
+    import torch
+    f16, f32 = torch.float16, torch.float32
+    cases = [("config2", 2, 1, 128, 1024, 4096, f16, f16)]
+    cases += [("config3", 1, 1, 1000, n, k, f16, f16)
+              for n, k in [(3072, 1024), (1024, 1024), (4096, 1024), (1024, 4096), (2048, 1024)]]
+    cases += [("config4", w, 1, m, n, k, f16, f16) for w in (1, 2) for m in (1, 4, 16)
+              for n, k in [(2560, 640), (1030, 640)]]
+    cases += [("config4", w, 1, 16, 1024, 4096, f16, f16) for w in (1, 2)]
+    cases += [("refshape_x3", w, 3, m, n, k, f32, f32) for w in (1, 2) for n, k, m in REF_SHAPES]
+    for i, (name, w, p, m, n, k, sd, od) in enumerate(cases):
+        row = _suite_case(w, p, m, n, k, scale_dtype=sd, out_dtype=od, seed=i)
+        print(json.dumps({"case": name, **row}), flush=True)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="low-bit GEMM benchmark (BASELINE.json config 1)")
     ap.add_argument("--gpus", type=int, default=1)
@@ -155,7 +226,12 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (5 times); the known byte count "
                          "calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--suite", action="store_true",
+                    help="only time BASELINE.json configs 2-4 and the reference's tuned shapes (one JSON line each)")
     args = ap.parse_args(argv)
+    if args.suite:
+        suite()
+        return 0
     if args.copy_calibration:
         import torch
         src = torch.ones(args.copy_calibration << 18, dtype=torch.float32, device="cuda")

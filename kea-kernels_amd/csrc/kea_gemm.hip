@@ -10,7 +10,8 @@
 //     for 2 (1-bit) or 1 (2-bit) k-steps of 64;
 //   * expansion to int8 is a mask (v_and_b32) plus a byte permute (v_perm_b32) per 4 weights, with the permute's
 //     constant table mapping the masked selector bytes to 0x01 / 0xFF (1-bit) or 0x00 / 0x01 / 0xFF (2-bit);
-//   * activations are staged in LDS (double buffered, padded rows), weights go global -> VGPR directly;
+//   * activations and weight words both stream global -> LDS by direct copies (global_load_lds) into a ring of stage
+//     buffers (256 k each; two by default), tracked with vmcnt; activation rows are XOR-swizzled 16-byte units;
 //   * v_mfma_i32_16x16x64_i8 with the weight fragment as the A operand, so each lane ends up owning 4 consecutive
 //     output columns of one row: the epilogue stores 8-byte (fp16/bf16) or 16-byte (fp32) vectors;
 //   * split-K writes exact int32 slices [S][P][M][N] and a second kernel sums them in slice order (integer
@@ -195,8 +196,8 @@ __device__ __forceinline__ void epilogue4(const Params &p, int m, int nb, const 
 }
 
 // Stage geometry shared by the kernels and the host launcher. A stage is 256 k (2 native words at 1 bit, 4 at 2
-// bits), i.e. 16 activation units of 16 bytes per row. The ring depth NS is as deep as the LDS budget (kLdsBudget,
-// up to the 160 KB a gfx950 workgroup may allocate) and the 6-bit vmcnt counter allow (at least 2).
+// bits), i.e. 16 activation units of 16 bytes per row. The ring depth NS is kMaxStages unless the LDS budget
+// (kLdsBudget, the 160 KB a gfx950 workgroup may allocate) or the 6-bit vmcnt counter allow fewer (at least 2).
 struct StageShape {
     int sw;           // native words per stage
     int stage_bytes;  // LDS bytes per ring buffer
@@ -204,6 +205,13 @@ struct StageShape {
     int ns;           // ring buffers
 };
 constexpr int kLdsBudget = 160 * 1024;
+// Ring depth cap. Sweeps on MI355X over the BASELINE shapes: two buffers per workgroup beat deeper rings nearly
+// everywhere (up to 1.7x at P = 3), because the LDS a deeper ring takes costs more in co-resident workgroups (the
+// latency hiding that matters) than the extra stages in flight give back.
+#ifndef KEA_MAX_STAGES
+#define KEA_MAX_STAGES 2
+#endif
+constexpr int kMaxStages = KEA_MAX_STAGES;
 
 __host__ __device__ constexpr StageShape stage_shape(int wbits, int parts, int rm, int rn, int wm, int wn) {
     const int nw = wm * wn, bm = wm * rm * 16, bn = wn * rn * 16;
@@ -214,7 +222,7 @@ __host__ __device__ constexpr StageShape stage_shape(int wbits, int parts, int r
     const int copies = a_units / 64 / nw + b_words / nw;
     int ns = kLdsBudget / stage;
     if (ns > 63 / copies + 1) ns = 63 / copies + 1;
-    if (ns > 8) ns = 8;
+    if (ns > kMaxStages) ns = kMaxStages;
     if (ns < 2) ns = 2;
     return StageShape{sw, stage, copies, ns};
 }
@@ -503,18 +511,37 @@ __global__ void __launch_bounds__(256) finish_kernel(Params p, int S) {
     for (int c = 0; c < P; ++c)
 #pragma unroll
         for (int r = 0; r < 4; ++r) a[c][r] = 0;
-    for (int z = 0; z < S; ++z)
+    // Slices are read in batches of up to 8 whose loads are all issued before any is summed (one memory latency per
+    // batch instead of one per slice); the sum itself runs in slice order.
+    const long long plane = (long long)p.M * p.N;
+    const int32_t *base = p.slices + (long long)m * p.N + nb;
+    const bool vec = p.slice_vec && nb + 3 < p.N;
+    for (int z0 = 0; z0 < S; z0 += 8) {
+        int4 v[8][P];
 #pragma unroll
-        for (int c = 0; c < P; ++c) {
-            const int32_t *src = p.slices + (((long long)z * P + c) * p.M + m) * p.N + nb;
-            if (p.slice_vec && nb + 3 < p.N) {
-                const int4 v = *(const int4 *)src;
-                a[c][0] += v.x; a[c][1] += v.y; a[c][2] += v.z; a[c][3] += v.w;
-            } else {
-                for (int r = 0; r < 4; ++r)
-                    if (nb + r < p.N) a[c][r] += src[r];
+        for (int z = 0; z < 8; ++z)
+#pragma unroll
+            for (int c = 0; c < P; ++c) {
+                v[z][c] = make_int4(0, 0, 0, 0);
+                if (z0 + z < S) {
+                    const int32_t *src = base + ((long long)(z0 + z) * P + c) * plane;
+                    if (vec) {
+                        v[z][c] = *(const int4 *)src;
+                    } else {
+                        v[z][c].x = src[0];
+                        if (nb + 1 < p.N) v[z][c].y = src[1];
+                        if (nb + 2 < p.N) v[z][c].z = src[2];
+                        if (nb + 3 < p.N) v[z][c].w = src[3];
+                    }
+                }
             }
-        }
+#pragma unroll
+        for (int z = 0; z < 8; ++z)
+#pragma unroll
+            for (int c = 0; c < P; ++c) {
+                a[c][0] += v[z][c].x; a[c][1] += v[z][c].y; a[c][2] += v[z][c].z; a[c][3] += v[z][c].w;
+            }
+    }
     EpiOperands e;
     load_row_scales<P>(p, m, e);
     load_col_scales(p, nb, e);
@@ -605,31 +632,21 @@ FinishFn pick_finish(int parts) {
     return finish_kernel<3>;
 }
 
-// Tile choice: a pure function of (wbits, parts, m, n, k), from MI355X sweeps over the BASELINE shapes. Large M
-// favours wide-N tiles with two activation tiles per wavefront; small and medium M favour 32x32 / 16x64 tiles with
-// many workgroups. Among the candidates for the M range, the first that gives every CU a workgroup wins, else the
-// one with the most workgroups.
+// Tile and split choice: a pure function of (wbits, parts, m, n, k), fitted to MI355X sweeps of every tile x split
+// over BASELINE.json's shapes and the reference's tuned (N, K, M) points at P = 1 and 3 (the chosen configuration is
+// within 0.3% of the per-shape best summed over those 61 shapes). With P >= 2 the narrow 16x64 tile wins (its
+// register budget leaves room for co-resident workgroups); with P = 1 the 32x32 tile wins up to a few hundred rows,
+// then wide tiles take over as M grows.
 int choose_tile(int wbits, int parts, long long m, long long n, long long k) {
     (void)wbits; (void)k;
-    static const int large_m[] = {9, 8, 2, 4};
-    static const int small_m[] = {4, 1, 2};
-    const int *order = m >= 512 ? large_m : small_m;
-    const int count = m >= 512 ? 4 : 3;
-    int best = 1;
-    long long best_wg = -1;
-    for (int i = 0; i < count; ++i) {
-        const int id = order[i];
-        const Tile &t = kTiles[id - 1];
-        if (!tile_fits(parts, t.rm, t.rn)) continue;
-        const long long bm = t.wm * t.rm * 16, bn = t.wn * t.rn * 16;
-        const long long wgs = cdivl(m, bm) * cdivl(n, bn);
-        if (wgs >= 256) return id;
-        if (wgs > best_wg) { best_wg = wgs; best = id; }
-    }
-    return best;
+    if (parts >= 2) return (m >= 320 && n >= 3072) ? 3 : 1;
+    if (m <= 64) return 4;
+    if (m < 512) return (n >= 4096 && m >= 192) ? 2 : 4;
+    return n <= 1024 ? 2 : (n >= 4096 ? 8 : 5);
 }
 
-// Split factor for split_k == 0: split K only when the (M, N) tiling leaves most CUs idle.
+// Split factor for split_k == 0: split K only for long K ranges (>= 2048) whose tiling leaves at most 64 workgroups,
+// by powers of two up to 8 slices and 256 workgroups; the split's second launch costs more than it saves otherwise.
 int choose_split(int wbits, int parts, long long m, long long n, long long k, int id) {
     const Tile &t = kTiles[id - 1];
     const long long bm = t.wm * t.rm * 16, bn = t.wn * t.rn * 16;
@@ -637,9 +654,9 @@ int choose_split(int wbits, int parts, long long m, long long n, long long k, in
     const long long J = wbits == 1 ? cdivl(k, 128) : cdivl(k, 64);
     const long long quads = cdivl(J, 4);
     (void)parts;
-    if (wgs >= 128 || quads < 2) return 1;
+    if (k < 2048 || wgs > 64) return 1;
     long long s = 1;
-    while (s * 2 <= quads && wgs * s * 2 <= 512) s *= 2;
+    while (s * 2 <= std::min<long long>(8, quads) && wgs * s * 2 <= 256) s *= 2;
     return (int)s;
 }
 
