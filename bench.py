@@ -150,7 +150,7 @@ REF_SHAPES = [(n, k, m) for n, k in [(1024, 1024), (1024, 4096), (2048, 1024), (
               for m in (38, 126, 256, 368)]  # kk/binary/configs.py:17-36 (RTX 5090 timings, three parts, FP32 out)
 
 
-def _suite_case(wbits, parts, m, n, k, *, scale_dtype, out_dtype, seed, reps=200):
+def _suite_case(wbits, parts, m, n, k, *, scale_dtype, out_dtype, seed, reps=200, ws_group=0):
     """Per-launch microseconds of the library's default configuration, inputs resident, HIP-graph replay."""
     import torch
     from kea_kernels import formats, lowbit
@@ -165,12 +165,14 @@ def _suite_case(wbits, parts, m, n, k, *, scale_dtype, out_dtype, seed, reps=200
     else:
         codes = formats.pack_ternary(torch.randint(-1, 2, (n, k), generator=g, dtype=torch.int8))
     words = kernels.relayout_codes(codes, k, wbits).to(dev)
-    alpha = (torch.rand(n, generator=g) * 0.09 + 0.01).to(scale_dtype).to(dev)
+    groups = -(-k // ws_group) if ws_group else 0
+    shape = (n, groups) if ws_group else (n,)
+    alpha = (torch.rand(*shape, generator=g) * 0.09 + 0.01).to(scale_dtype).to(dev)
     y = torch.empty(m, n, dtype=out_dtype, device=dev)
     stream = torch.cuda.Stream(dev)
 
     def step():
-        lowbit.gemm(wbits, q, qs, words, n, k, alpha, None, y, None)
+        lowbit.gemm(wbits, q, qs, words, n, k, alpha, None, y, None, ws_group=ws_group)
 
     with torch.cuda.stream(stream):
         step()
@@ -191,9 +193,10 @@ def _suite_case(wbits, parts, m, n, k, *, scale_dtype, out_dtype, seed, reps=200
     us = a.elapsed_time(b) * 1000 / (reps // 100 * 100)
     esz = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
     ops = 2 * m * n * k * parts
-    nbytes = (m * k * parts + n * (-(-k * wbits // 8)) + esz[scale_dtype] * (n + parts * m) + esz[out_dtype] * m * n)
+    nbytes = (m * k * parts + n * (-(-k * wbits // 8)) + esz[scale_dtype] * (alpha.numel() + parts * m)
+              + esz[out_dtype] * m * n)
     t_roof = max(ops / (PEAK_INT8_TOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9))
-    return {"wbits": wbits, "parts": parts, "M": m, "N": n, "K": k, "us": round(us, 3),
+    return {"wbits": wbits, "parts": parts, "M": m, "N": n, "K": k, "ws_group": ws_group, "us": round(us, 3),
             "tops": round(ops / us / 1e6, 2), "gbs": round(nbytes / us / 1e3, 1),
             "bound": "mfma" if ops / (PEAK_INT8_TOPS * 1e12) >= nbytes / (PEAK_HBM_GBS * 1e9) else "hbm",
             "roofline_frac": round(t_roof / (us * 1e-6), 4)}
@@ -204,7 +207,7 @@ def suite() -> None:
     activation parts with FP32 scales and output (the arithmetic its in-source timings use)."""
     import torch
     f16, f32 = torch.float16, torch.float32
-    cases = [("config2", 2, 1, 128, 1024, 4096, f16, f16)]
+    cases = [("config2", 2, 1, 128, 1024, 4096, f16, f16), ("config2_group128", 2, 1, 128, 1024, 4096, f16, f16)]
     cases += [("config3", 1, 1, 1000, n, k, f16, f16)
               for n, k in [(3072, 1024), (1024, 1024), (4096, 1024), (1024, 4096), (2048, 1024)]]
     cases += [("config4", w, 1, m, n, k, f16, f16) for w in (1, 2) for m in (1, 4, 16)
@@ -212,7 +215,8 @@ def suite() -> None:
     cases += [("config4", w, 1, 16, 1024, 4096, f16, f16) for w in (1, 2)]
     cases += [("refshape_x3", w, 3, m, n, k, f32, f32) for w in (1, 2) for n, k, m in REF_SHAPES]
     for i, (name, w, p, m, n, k, sd, od) in enumerate(cases):
-        row = _suite_case(w, p, m, n, k, scale_dtype=sd, out_dtype=od, seed=i)
+        row = _suite_case(w, p, m, n, k, scale_dtype=sd, out_dtype=od, seed=i,
+                          ws_group=128 if name.endswith("group128") else 0)
         print(json.dumps({"case": name, **row}), flush=True)
 
 

@@ -93,7 +93,8 @@ int kea_t2_unlayout_host(const uint32_t *words_host, int64_t n, int64_t k, uint8
  *                                                P = 2: fma(f(a0), s0, f(a1)*s1)   (ORDER: fma(f(a1), s1, f(a0)*s0))
  *                                                P = 3: fma(f(a2), s2, <P = 2 form>)
  *     r = bias ? fma(r, alpha[n], bias[n]) : r * alpha[n]
- *   per-group scales (ws_group > 0, a multiple of 64; alpha is [N][ceil(K/ws_group)]):
+ *   per-group scales (ws_group = 64, 128 or 256; alpha is [N][ceil(K/ws_group)] row-major, group g covering
+ *   k in [g*ws_group, (g+1)*ws_group); tile configs 0, 1 and 4 only, unsplit: split_k 0 or 1):
  *     r = 0; for g in groups: r = fma(comb_P(acc_g, s), alpha[n][g], r);  r = bias ? r + bias[n] : r
  *   SiLU (flags & KEA_FLAG_SILU): r = r / (1 + exp(-r)); then y[m*ldy + n] = RN(r) in y_dtype.
  *   f() is int32 -> fp32 round-to-nearest; every FP32 operation is IEEE round-to-nearest-even, unfused

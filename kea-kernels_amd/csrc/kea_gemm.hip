@@ -62,6 +62,8 @@ struct Params {
     int y_vec;      // 1: y rows allow aligned 4-element vector stores
     int acc_vec;    // 1: acc_out rows allow aligned int4 stores
     int slice_vec;  // 1: the dense [S][P][M][N] slices allow aligned int4 access (N % 4 == 0)
+    int groups;     // per-group scales: G = ceil(K / ws_group) groups, alpha [N][G]
+    int gp_shift;   // log2 of the padded group count held in LDS (a power of two >= the groups the stages span)
 };
 
 __device__ __forceinline__ float load_scalar(const void *p, int dtype, long long i) {
@@ -167,11 +169,11 @@ __device__ __forceinline__ void load_row_scales(const Params &p, int m, EpiOpera
     for (int c = 0; c < 3; ++c) e.s[c] = c < P ? load_scalar(p.qs, p.qs_dtype, c * p.qs_stride + mm) : 0.f;
 }
 
-__device__ __forceinline__ void load_col_scales(const Params &p, int nb, EpiOperands &e) {
+__device__ __forceinline__ void load_col_scales(const Params &p, int nb, EpiOperands &e, bool with_alpha = true) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int n = nb + r < p.N ? nb + r : p.N - 1;
-        e.alpha[r] = load_scalar(p.ws, p.ws_dtype, n);
+        e.alpha[r] = with_alpha ? load_scalar(p.ws, p.ws_dtype, n) : 0.f;
         e.bias[r] = p.bias ? load_scalar(p.bias, p.bias_dtype, n) : 0.f;
     }
 }
@@ -185,6 +187,29 @@ __device__ __forceinline__ void epilogue4(const Params &p, int m, int nb, const 
         for (int r = 0; r < 4; ++r) {
             int ar[3] = {a[0][r], P > 1 ? a[1][r] : 0, P > 2 ? a[2][r] : 0};
             v[r] = finish(combine<P>(ar, e.s, p.flags), e.alpha[r], p.bias != nullptr, e.bias[r], p.flags);
+        }
+        store4(p, (long long)m * p.ldy + nb, nb, v);
+    }
+    if (p.acc) {
+#pragma unroll
+        for (int c = 0; c < P; ++c)
+            store_int4(p.acc + ((long long)c * p.M + m) * p.acc_ld + nb, p.acc_vec, nb, p.N, a[c]);
+    }
+}
+
+// The per-group epilogue of 4 consecutive columns: r holds sum_g fma(comb_P(acc_g), alpha[n][g], .) from the main
+// loop; then r = bias ? r + bias : r, optional SiLU, store. a[c][r] are the full-K accumulators (for acc_out).
+template <int P>
+__device__ __forceinline__ void epilogue4_groups(const Params &p, int m, int nb, const int (*a)[4], const float *racc,
+                                                 const EpiOperands &e) {
+    if (p.y) {
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float x = racc[r];
+            if (p.bias) x = x + e.bias[r];
+            if (p.flags & KEA_FLAG_SILU) x = x / (1.0f + expf(-x));
+            v[r] = x;
         }
         store4(p, (long long)m * p.ldy + nb, nb, v);
     }
@@ -265,8 +290,16 @@ __device__ __forceinline__ void dma4(const void *g, void *lds_wave_base) {
 // (out-of-range sources are clamped to a valid address and their bytes are never used), which keeps the vmcnt
 // arithmetic exact. Activation rows are stored as 16-byte units with an XOR swizzle so that the 16 rows read by one
 // MFMA operand fetch land in distinct LDS bank groups. KTAIL kernels serve K % 16 != 0 (byte-precise K masking).
-template <int WBITS, int P, int RM, int RN, int WM, int WN, bool SLICED, bool KTAIL>
+//
+// GQ > 0: per-group weight scales, one group per GQ k-steps of 64 (ws_group = 64 * GQ). The tile's block of alpha
+// ([N][G] in memory) is staged once into LDS as f32 [group][column] (zero rows past the last group), and after the
+// last k-step of each group every lane folds that group's exact int32 sums into an FP32 running value:
+// r = fma(comb_P(acc - acc_at_previous_group_end), alpha[n][g], r). Group ends are fixed positions of the unrolled
+// stage, so the folding is straight-line code; accumulators are only read there.
+template <int WBITS, int P, int RM, int RN, int WM, int WN, bool SLICED, bool KTAIL, int GQ = 0>
 __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
+    static_assert(GQ == 0 || GQ == 1 || GQ == 2 || GQ == 4, "groups of 64, 128 or 256 k");
+    static_assert(GQ == 0 || !SLICED, "per-group scales run unsplit");
     constexpr StageShape SHAPE = stage_shape(WBITS, P, RM, RN, WM, WN);
     constexpr int SW = SHAPE.sw, NS = SHAPE.ns;
     constexpr int NW = WM * WN;                 // wavefronts
@@ -360,6 +393,53 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
 #pragma unroll
             for (int jn = 0; jn < RN; ++jn) acc[c][i][jn] = (v4i){0, 0, 0, 0};
 
+    // Epilogue operands (per-token scales also feed the per-group folding inside the K loop).
+    EpiOperands rows[RM], cols[RN];
+
+    // Per-group scales: FP32 running values, the accumulators at the previous group end, and the alpha block in LDS
+    // (f32 [group][column], row stride ALD floats: 16-byte rows whose starts spread over the banks), placed after the
+    // ring buffers this workgroup uses.
+    constexpr int ALD = BN + 4;
+    float racc[RM][RN][4];
+    int prev[GQ > 0 ? P : 1][RM][RN][4];
+    float *alds = (float *)(lds + min(NS, nst) * STAGE_BYTES);
+    if constexpr (GQ > 0) {
+#pragma unroll
+        for (int i = 0; i < RM; ++i)
+#pragma unroll
+            for (int jn = 0; jn < RN; ++jn)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    racc[i][jn][r] = 0.f;
+#pragma unroll
+                    for (int c = 0; c < P; ++c) prev[c][i][jn][r] = 0;
+                }
+    }
+
+    // Folds the group that ends with the k-step starting at kstep into racc (per-group scales only).
+    auto fold = [&](int kstep) {
+        if constexpr (GQ > 0) {
+        const int g = kstep / (64 * GQ);
+#pragma unroll
+        for (int jn = 0; jn < RN; ++jn) {
+            const float4 al = *(const float4 *)(alds + g * ALD + (wn * RN + jn) * 16 + (lane >> 4) * 4);
+            const float alv[4] = {al.x, al.y, al.z, al.w};
+#pragma unroll
+            for (int i = 0; i < RM; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    int d[3] = {0, 0, 0};
+#pragma unroll
+                    for (int c = 0; c < P; ++c) {
+                        d[c] = acc[c][i][jn][r] - prev[c][i][jn][r];
+                        prev[c][i][jn][r] = acc[c][i][jn][r];
+                    }
+                    racc[i][jn][r] = __builtin_fmaf(combine<P>(d, rows[i].s, p.flags), alv[r], racc[i][jn][r]);
+                }
+        }
+        }
+    };
+
     // One stage of MFMAs: straight-line code (no accumulator ever passes a control-flow merge; merges made the
     // compiler emit AGPR copy chains). The LDS reads of word w + 1 are issued before the MFMAs of word w. MASKED (the
     // last stage) zeroes the weights at k >= kend: per 16-byte group of a lane's operand, or per byte for KTAIL.
@@ -425,6 +505,10 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
                     for (int i = 0; i < RM; ++i)
                         acc[c][i][jn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af[slot][c][i], acc[c][i][jn], 0, 0, 0);
             }
+            // t is a fully unrolled step index, so group ends are compile-time positions (no branch)
+            if constexpr (GQ > 0) {
+                if ((t + 1) % GQ == 0) fold(kstep);
+            }
         }
     };
 
@@ -445,17 +529,53 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
 
     // Epilogue operands are fetched before the ring so their latency overlaps the main loads (the copies below are
     // issued after these loads, so the stage waits never depend on them).
-    EpiOperands rows[RM], cols[RN];
     if constexpr (!SLICED) {
 #pragma unroll
         for (int i = 0; i < RM; ++i) load_row_scales<P>(p, m0 + (wm * RM + i) * 16 + (lane & 15), rows[i]);
 #pragma unroll
-        for (int jn = 0; jn < RN; ++jn) load_col_scales(p, n0 + (wn * RN + jn) * 16 + (lane >> 4) * 4, cols[jn]);
+        for (int jn = 0; jn < RN; ++jn)
+            load_col_scales(p, n0 + (wn * RN + jn) * 16 + (lane >> 4) * 4, cols[jn], GQ == 0);
     }
+
+    // Per-group scales: the tile's alpha rows [n0, n0 + BN) x groups [0, 2^gp_shift) go to LDS as f32 in chunks of
+    // ACH values per lane (zero past the last group; rows past N clamped, never stored). The first chunk's loads are
+    // issued before the ring's and stored after, so their latency overlaps the first stage's.
+    constexpr int ACH = 8;
+    float av[ACH];
+    const int atotal = BN << p.gp_shift, gmask = (1 << p.gp_shift) - 1;
+    auto alpha_load = [&](int base) {
+#pragma unroll
+        for (int u = 0; u < ACH; ++u) {
+            const int idx = base + (u * NW + wave) * 64 + lane;
+            const int g = idx & gmask, c = idx >> p.gp_shift;
+            av[u] = 0.f;
+            if (c < BN && g < p.groups)
+                av[u] = load_scalar(p.ws, p.ws_dtype, (long long)min(n0 + c, p.N - 1) * p.groups + g);
+        }
+    };
+    auto alpha_store = [&](int base) {
+#pragma unroll
+        for (int u = 0; u < ACH; ++u) {
+            const int idx = base + (u * NW + wave) * 64 + lane;
+            const int g = idx & gmask, c = idx >> p.gp_shift;
+            if (c < BN) alds[g * ALD + c] = av[u];
+        }
+    };
+    if constexpr (GQ > 0) alpha_load(0);
 
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s)
         if (s < nst) issue(s);
+
+    if constexpr (GQ > 0) {
+        alpha_store(0);
+        for (int base = ACH * 64 * NW; base < atotal; base += ACH * 64 * NW) {
+            alpha_load(base);
+            alpha_store(base);
+        }
+        // LDS writes complete before the first stage barrier publishes them (lgkmcnt(0); vmcnt, expcnt untouched)
+        __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | (7 << 4));
+    }
     using plain_t = std::integral_constant<bool, false>;
     using masked_t = std::integral_constant<bool, true>;
     for (int s = 0; s < nst - 1; ++s) {
@@ -489,6 +609,8 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
                 for (int c = 0; c < P; ++c)
                     store_int4(p.slices + (((long long)blockIdx.z * P + c) * p.M + m) * p.N + nb, p.slice_vec, nb,
                                p.N, a[c]);
+            } else if constexpr (GQ > 0) {
+                epilogue4_groups<P>(p, m, nb, a, racc[i][jn], cols[jn]);
             } else {
                 EpiOperands e = cols[jn];
 #pragma unroll
@@ -610,6 +732,26 @@ constexpr int kTailTile = 4;
 template <int WBITS, int P>
 KernelFn pick_ktail() { return gemm_kernel<WBITS, P, 1, 1, 2, 2, false, true>; }
 
+// Per-group scales: tile 1 (16x64, P >= 2) or tile 4 (32x32, P = 1, and the byte-precise K tail), unsplit.
+template <int WBITS, int P, int GQ>
+KernelFn pick_group_gq(int id, bool ktail) {
+    if (ktail) return gemm_kernel<WBITS, P, 1, 1, 2, 2, false, true, GQ>;
+    return id == 1 ? gemm_kernel<WBITS, P, 1, 1, 1, 4, false, false, GQ> : gemm_kernel<WBITS, P, 1, 1, 2, 2, false, false, GQ>;
+}
+template <int WBITS, int P>
+KernelFn pick_group_p(int gq, int id, bool ktail) {
+    if (gq == 1) return pick_group_gq<WBITS, P, 1>(id, ktail);
+    if (gq == 2) return pick_group_gq<WBITS, P, 2>(id, ktail);
+    return pick_group_gq<WBITS, P, 4>(id, ktail);
+}
+KernelFn pick_group(int wbits, int parts, int gq, int id, bool ktail) {
+    if (wbits == 1)
+        return parts == 1 ? pick_group_p<1, 1>(gq, id, ktail)
+             : parts == 2 ? pick_group_p<1, 2>(gq, id, ktail) : pick_group_p<1, 3>(gq, id, ktail);
+    return parts == 1 ? pick_group_p<2, 1>(gq, id, ktail)
+         : parts == 2 ? pick_group_p<2, 2>(gq, id, ktail) : pick_group_p<2, 3>(gq, id, ktail);
+}
+
 KernelFn pick_kernel(int wbits, int parts, int id, bool sliced, bool ktail) {
     if (ktail) {
         if (wbits == 1) return parts == 1 ? pick_ktail<1, 1>() : parts == 2 ? pick_ktail<1, 2>() : pick_ktail<1, 3>();
@@ -730,10 +872,19 @@ int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq
                     int ws_dtype, int64_t ws_group, const void *bias, int bias_dtype, void *y, int y_dtype,
                     int64_t ldy, int32_t *acc_out, int64_t acc_ld, int64_t m, int flags, int split_k, int config,
                     void *workspace, int64_t workspace_bytes, void *stream) {
-    int tile, s, qps;
-    int rc = resolve(wbits, parts, m, n, k, ws_group ? 1 : split_k, config, &tile, &s, &qps);
+    int tile, s, qps, gq = 0;
+    if (ws_group != 0) {
+        if (ws_group != 64 && ws_group != 128 && ws_group != 256)
+            return kea::fail(KEA_EINVAL, "ws_group must be 0 (per-channel scales), 64, 128 or 256");
+        if (config != 0 && config != 1 && config != 4)
+            return kea::fail(KEA_EINVAL, "per-group weight scales run tile configs 1 and 4 only");
+        if (split_k > 1) return kea::fail(KEA_EINVAL, "per-group weight scales run unsplit (split_k 0 or 1)");
+        gq = (int)(ws_group / 64);
+        if (!config) config = parts >= 2 ? 1 : 4;
+        split_k = 1;
+    }
+    int rc = resolve(wbits, parts, m, n, k, split_k, config, &tile, &s, &qps);
     if (rc != KEA_OK) return rc;
-    if (ws_group != 0) return kea::fail(KEA_EINVAL, "per-group weight scales are not supported by this build");
     if (flags & ~(KEA_FLAG_SILU | KEA_FLAG_ORDER)) return kea::fail(KEA_EINVAL, "unknown flags");
     if (m > 0 && (!w || !qs || !wscale)) return kea::fail(KEA_EINVAL, "q, qs, w and wscale are required");
     if (m > 0 && !y && !acc_out) return kea::fail(KEA_EINVAL, "nothing to write: y and acc_out are both NULL");
@@ -777,7 +928,18 @@ int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq
     // the first nst buffers need LDS.
     const long long words_per_wg = std::min<long long>(4LL * qps, (long long)p.J);
     const int nst = (int)cdivl(words_per_wg, shape.sw);
-    const int lds_bytes = std::min(shape.ns, nst) * shape.stage_bytes;
+    int lds_bytes = std::min(shape.ns, nst) * shape.stage_bytes;
+    if (gq) {
+        // alpha block: the groups the stages span (4 k-steps of 64 per stage), padded to a power of two
+        const int spanned = nst * 4 / gq;
+        int shift = 0;
+        while ((1 << shift) < spanned) ++shift;
+        p.groups = (int)cdivl(k, ws_group);
+        p.gp_shift = shift;
+        lds_bytes += (1 << shift) * (bn + 4) * 4;
+        if (lds_bytes > kLdsBudget)
+            return kea::fail(KEA_EINVAL, "too many weight-scale groups for one workgroup's LDS: use a larger ws_group");
+    }
     dim3 grid((unsigned)cdivl(n, bn), (unsigned)cdivl(m, bm), (unsigned)s);
     dim3 block(t.wm * t.wn * 64);
     hipStream_t st = (hipStream_t)stream;
@@ -789,7 +951,8 @@ int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq
         p.slices = (int32_t *)workspace;
         p.slice_vec = (n % 4 == 0);
     }
-    KernelFn fn = pick_kernel(wbits, parts, tile, s > 1, (k & 15) != 0);
+    KernelFn fn = gq ? pick_group(wbits, parts, gq, tile, (k & 15) != 0)
+                     : pick_kernel(wbits, parts, tile, s > 1, (k & 15) != 0);
     if (lds_bytes > 65536) {
         hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
         if (e != hipSuccess) return kea::fail((int)e, std::string("LDS attribute refused: ") + hipGetErrorString(e));

@@ -266,3 +266,82 @@ def test_graph_replays_match_eager():
         torch.cuda.synchronize()
         assert torch.equal(y.cpu().view(torch.int16), y_eager.view(torch.int16)), f"replay {i}"
         case.run()  # eager work between replays
+
+
+# --- per-group weight scales ---------------------------------------------------------------------------------------
+
+def _group_run(case, ws_group, alpha_g, *, out_dtype, silu=False, order=0, config=None):
+    """Runs the GEMM with alpha_g [N, G] group scales (dtype of case.qs)."""
+    y = torch.full((case.m, case.n), float("nan"), device=DEV, dtype=out_dtype)
+    a = torch.full((case.p, case.m, case.n), -7, device=DEV, dtype=torch.int32)
+    lowbit.gemm(case.wbits, case.dq, case.dqs, case.words, case.n, case.k, alpha_g.to(DEV), case.dbias, y, a,
+                silu=silu, order=order, config=config, ws_group=ws_group)
+    torch.cuda.synchronize()
+    return y.cpu(), a.cpu().numpy()
+
+
+def _group_ref(case, ws_group, alpha_g, *, silu=False, order=0):
+    fn = O.b1_gemm if case.wbits == 1 else O.t2_gemm
+    acc_g = fn(case.q.numpy(), case.codes, case.k, group=ws_group)
+    bias = None if case.bias is None else case.bias.float().numpy()
+    y = O.epilogue(acc_g, case.qs.float().numpy(), alpha_g.float().numpy(), bias, silu=silu, order=order)
+    return y, acc_g.sum(axis=0, dtype=np.int64).astype(np.int32)
+
+
+@pytest.mark.parametrize("wbits", [1, 2])
+@pytest.mark.parametrize("ws_group", [64, 128, 256])
+@pytest.mark.parametrize("p", [1, 3])
+@torch.inference_mode()
+def test_group_scales_bitwise(wbits, ws_group, p):
+    case = Case(wbits, p, 70, 300, 1000, seed=ws_group + p + wbits, bias=True)
+    groups = -(-case.k // ws_group)
+    g = torch.Generator().manual_seed(ws_group * 7 + p)
+    alpha_g = (torch.rand(case.n, groups, generator=g) * 0.09 + 0.01).to(case.qs.dtype)
+    y, acc = _group_run(case, ws_group, alpha_g, out_dtype=torch.float32, order=p % 2)
+    ref_y, ref_acc = _group_ref(case, ws_group, alpha_g, order=p % 2)
+    assert np.array_equal(acc, ref_acc)
+    bad = np.argwhere(y.numpy().view(np.uint32) != ref_y.view(np.uint32))
+    assert bad.size == 0, f"{bad.shape[0]} mismatches, first {bad[:5].tolist()}"
+
+
+@torch.inference_mode()
+def test_config2_ternary_group128_fp16():
+    """BASELINE config 2 with group-128 fp16 scales [1024, 32], fp16 output."""
+    case = Case(2, 1, 128, 1024, 4096, seed=22)
+    g = torch.Generator().manual_seed(23)
+    alpha_g = (torch.rand(case.n, 32, generator=g) * 0.09 + 0.01).to(torch.float16)
+    y, acc = _group_run(case, 128, alpha_g, out_dtype=torch.float16)
+    ref_y, ref_acc = _group_ref(case, 128, alpha_g)
+    assert np.array_equal(acc, ref_acc)
+    assert np.array_equal(_gpu_bits(y, torch.float16), O.to_f16_bits(ref_y))
+    # tile 1 and tile 4 give the same bits
+    y1, _ = _group_run(case, 128, alpha_g, out_dtype=torch.float16, config=kernels.GemmConfig(tile=1, split=1))
+    assert torch.equal(y1.view(torch.int16), y.view(torch.int16))
+
+
+@pytest.mark.parametrize("k", [17, 300, 4096 + 64])
+@torch.inference_mode()
+def test_group_scales_ragged_k_and_silu(k):
+    case = Case(1, 2, 33, 45, k, seed=k, bias=True, pad_garbage=True)
+    groups = -(-k // 64)
+    g = torch.Generator().manual_seed(k)
+    alpha_g = (torch.rand(case.n, groups, generator=g) * 0.09 + 0.01).to(case.qs.dtype)
+    y, acc = _group_run(case, 64, alpha_g, out_dtype=torch.float32)
+    ref_y, ref_acc = _group_ref(case, 64, alpha_g)
+    assert np.array_equal(acc, ref_acc)
+    assert np.array_equal(y.numpy().view(np.uint32), ref_y.view(np.uint32))
+    ys, _ = _group_run(case, 64, alpha_g, out_dtype=torch.float32, silu=True)
+    ref_s, _ = _group_ref(case, 64, alpha_g, silu=True)
+    np.testing.assert_allclose(ys.numpy(), ref_s, rtol=2e-6, atol=2e-6)
+
+
+@torch.inference_mode()
+def test_group_scales_reject_unsupported_arguments():
+    case = Case(1, 1, 8, 64, 256, seed=3)
+    alpha_g = torch.ones(64, 4, dtype=case.qs.dtype)
+    with pytest.raises(ValueError, match="ws_group"):
+        _group_run(case, 96, alpha_g, out_dtype=torch.float32)
+    with pytest.raises(ValueError, match="tile configs"):
+        _group_run(case, 64, alpha_g, out_dtype=torch.float32, config=kernels.GemmConfig(tile=2, split=1))
+    with pytest.raises(ValueError, match="unsplit"):
+        _group_run(case, 64, alpha_g, out_dtype=torch.float32, config=kernels.GemmConfig(tile=4, split=2))
