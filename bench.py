@@ -220,6 +220,48 @@ def suite() -> None:
         print(json.dumps({"case": name, **row}), flush=True)
 
 
+def encoder_bench(batch: int, parts: int, reps: int = 20, seed: int = 5) -> dict:
+    """the 24-layer synthetic encoder (1-bit linears at `parts` int8 parts) on `batch` clips
+    of 10 s of seeded Gaussian noise, preprocessing + encoder captured in one HIP graph; ms per clip = replay / batch.
+    Accuracy: relative Frobenius error against the same model with FP32 dense linears."""
+    import torch
+    from kea_kernels import encoder as E
+    cfg = E.EncoderConfig()
+    weights = E.synthetic_weights(cfg, seed=seed)
+    enc = E.FastConformerEncoder(weights, cfg, "cuda", parts=parts)
+    g = torch.Generator().manual_seed(seed + batch)
+    audio = torch.randn(batch, 160000, generator=g).cuda()
+    t0 = time.perf_counter()
+    enc(audio)
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3
+    out = enc(audio)  # a second eager call: library autotuning (convolutions, FFT plans) settled
+    graph = E.EncoderGraph(enc, batch, 160000)
+    got = graph(audio).clone()
+    torch.cuda.synchronize()
+    graph_diff = float((got - out).abs().max())
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(3):
+        graph.replay()
+    a.record(graph.stream)
+    for _ in range(reps):
+        graph.replay()
+    b.record(graph.stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    dense = E.FastConformerEncoder(weights, cfg, "cuda", dense=True)
+    ref = dense(audio)
+    rel = float((out.double() - ref.double()).norm() / ref.double().norm())
+    t = out.shape[1]
+    # linear ops per forward: the 10 per-token linears of each layer (W_pos runs once per length, outside the graph)
+    per_layer = sum(n * k for name, (n, k, _) in E.quantized_shapes(cfg).items() if name != "self_attn.linear_pos")
+    lin_ops = 2 * t * batch * cfg.layers * per_layer
+    return {"case": "config5_encoder", "batch": batch, "parts": parts, "frames": t, "ms_per_forward": round(ms, 4),
+            "ms_per_clip": round(ms / batch, 4), "eager_ms_first_call": round(eager_ms, 1),
+            "graph_vs_eager_max_abs_diff": graph_diff, "rel_err_vs_dense_fp32": rel,
+            "quantized_linear_ops_per_clip": lin_ops // batch, "weight_bytes": enc.weight_bytes()}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="low-bit GEMM benchmark (BASELINE.json config 1)")
     ap.add_argument("--gpus", type=int, default=1)
@@ -230,11 +272,20 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (5 times); the known byte count "
                          "calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--encoder", action="store_true",
+                    help="only run BASELINE.json config 5 (24-layer encoder, batch 1 and 8; one JSON line each)")
+    ap.add_argument("--encoder-cases", default="1x1,8x1,1x3,8x3", metavar="BxP,...",
+                    help="batch x parts cases of --encoder")
     ap.add_argument("--suite", action="store_true",
                     help="only time BASELINE.json configs 2-4 and the reference's tuned shapes (one JSON line each)")
     args = ap.parse_args(argv)
     if args.suite:
         suite()
+        return 0
+    if args.encoder:
+        for case in args.encoder_cases.split(","):
+            batch, parts = (int(v) for v in case.split("x"))
+            print(json.dumps(encoder_bench(batch, parts)), flush=True)
         return 0
     if args.copy_calibration:
         import torch

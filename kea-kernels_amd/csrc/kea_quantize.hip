@@ -1,14 +1,19 @@
-// Residual int8 activation quantizer with optional fused LayerNorm and input SiLU (one wavefront per token row).
+// Residual int8 activation quantizer with optional fused LayerNorm and input SiLU.
 //
 // Semantics follow the reference's quantizers (kk/binary/kernels.py:567-616 and the Triton `_quantize`,
 // kk/ternary/fused_kernels.py:31-50):
 //     z = x ; z = LayerNorm(z) * w + b (optional) ; z = z * sigmoid(z) (optional)
 //     for c < P:  s_c = max(max|z| / 127, 1e-30) ; q_c = rint(z / s_c) ; z = z - q_c * s_c
 // with IEEE division and round-half-even (the reference's `div.full` / `ex2.approx` NVIDIA approximations are not
-// reproduced). Reductions that are not exact (the LayerNorm sums) use one fixed order that the CPU oracle restates:
-// each lane sums its elements k = lane, lane + 64, ... in increasing k, then a xor butterfly over 64 lanes with
-// offsets 32, 16, ..., 1. The max reductions are exact in any order. With fp16 scales the scale is rounded to fp16
-// (kept >= the smallest fp16 subnormal, <= the largest finite fp16) before use and q is clamped to [-127, 127].
+// reproduced). With fp16 scales the scale is rounded to fp16 (kept >= the smallest fp16 subnormal, <= the largest
+// finite fp16) before use and q is clamped to [-127, 127].
+//
+// Layout: a row is handled by WPR wave64s (1 for K <= 1024, 4 above), thread th of the row holding the 4-element
+// chunks k = 4 * (th + 64 * WPR * i) + j: consecutive threads read consecutive 16-byte chunks (one float4 load each
+// when the row is contiguous and aligned) and store the 4 quantized bytes as one dword. The LayerNorm sums, the only
+// reductions that are not exact, use one fixed order that the CPU oracle restates: each thread sums its elements in
+// increasing k, a xor butterfly over the 64 lanes of each wave (offsets 32, 16, ..., 1), then the wave totals in wave
+// order. The max reductions are exact in any order.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -17,8 +22,6 @@
 #include "kea_internal.h"
 
 namespace {
-
-constexpr int kRowsPerBlock = 4;
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -36,53 +39,98 @@ __device__ __forceinline__ float load_x(const void *x, int dtype, long long i) {
     return ((const float *)x)[i];
 }
 
-// CPL: elements per lane held in registers (K <= 64 * CPL).
-template <int CPL>
-__global__ void __launch_bounds__(64 * kRowsPerBlock)
+// Row-wide reduction over the WPR waves of a row: wave butterfly, then the wave totals in wave order through LDS.
+// slot: a distinct LDS slot per reduction of the kernel (no barrier is needed before a slot's reuse).
+template <int WPR, bool MAX>
+__device__ __forceinline__ float row_reduce(float v, float (*red)[WPR], int slot, int wave) {
+    v = MAX ? wave_max(v) : wave_sum(v);
+    if constexpr (WPR == 1) {
+        return v;
+    } else {
+        if ((threadIdx.x & 63) == 0) red[slot][wave] = v;
+        __syncthreads();
+        float r = red[slot][0];
+#pragma unroll
+        for (int w = 1; w < WPR; ++w) r = MAX ? fmaxf(r, red[slot][w]) : r + red[slot][w];
+        return r;
+    }
+}
+
+// VPT: 4-element chunks per thread (K <= 256 * WPR * VPT). VEC: contiguous, 16-byte aligned rows (float4 loads) and
+// ldq % 4 == 0 (dword stores); otherwise element-wise access with any strides.
+template <int VPT, int WPR, bool VEC>
+__global__ void __launch_bounds__(256)
 quantize_kernel(const void *x, int x_dtype, long long xb, long long xt, long long xk, long long t, int M, int K,
                 int parts, const float *nw, const float *nb, float eps, int input_silu, int8_t *q, long long ldq,
                 void *qs, int qs_dtype) {
-    const int lane = threadIdx.x & 63;
-    const int m = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-    if (m >= M) return;
+    constexpr int RPB = 4 / WPR;     // rows per block
+    constexpr int TPR = 64 * WPR;    // threads per row
+    __shared__ float red[RPB][5][WPR];
+    const int th = threadIdx.x % TPR, rl = threadIdx.x / TPR, wave = th >> 6;
+    const int m = blockIdx.x * RPB + rl;
+    if (m >= M) return;  // whole rows leave together: the row's barriers stay matched
     const long long base = (long long)(m / t) * xb + (long long)(m % t) * xt;
-    float z[CPL];
+    float z[VPT][4];
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-        const int k = lane + 64 * i;
-        z[i] = k < K ? load_x(x, x_dtype, base + (long long)k * xk) : 0.f;
+    for (int i = 0; i < VPT; ++i) {
+        const int k0 = 4 * (th + TPR * i);
+        if constexpr (VEC) {
+            if (k0 < K) {
+                if (x_dtype == KEA_F16) {
+                    const uint2 h = *(const uint2 *)((const _Float16 *)x + base + k0);
+                    const _Float16 *hv = (const _Float16 *)&h;
+                    z[i][0] = (float)hv[0]; z[i][1] = (float)hv[1]; z[i][2] = (float)hv[2]; z[i][3] = (float)hv[3];
+                } else {
+                    const float4 v = *(const float4 *)((const float *)x + base + k0);
+                    z[i][0] = v.x; z[i][1] = v.y; z[i][2] = v.z; z[i][3] = v.w;
+                }
+            } else {
+                z[i][0] = z[i][1] = z[i][2] = z[i][3] = 0.f;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) z[i][j] = k0 + j < K ? load_x(x, x_dtype, base + (long long)(k0 + j) * xk) : 0.f;
+        }
     }
     if (nw) {
         float sum = 0.f;
 #pragma unroll
-        for (int i = 0; i < CPL; ++i)
-            if (lane + 64 * i < K) sum = sum + z[i];
-        const float mean = wave_sum(sum) / (float)K;
+        for (int i = 0; i < VPT; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sum = sum + z[i][j];
+        const float mean = row_reduce<WPR, false>(sum, red[rl], 0, wave) / (float)K;
         float sq = 0.f;
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-            const int k = lane + 64 * i;
-            z[i] = k < K ? z[i] - mean : 0.f;
-            sq = sq + z[i] * z[i];
-        }
-        const float var = wave_sum(sq) / (float)K;
+        for (int i = 0; i < VPT; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = 4 * (th + TPR * i) + j;
+                z[i][j] = k < K ? z[i][j] - mean : 0.f;
+                sq = sq + z[i][j] * z[i][j];
+            }
+        const float var = row_reduce<WPR, false>(sq, red[rl], 1, wave) / (float)K;
         const float inv = 1.0f / sqrtf(var + eps);
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-            const int k = lane + 64 * i;
-            if (k < K) z[i] = z[i] * inv * nw[k] + nb[k];
-        }
+        for (int i = 0; i < VPT; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = 4 * (th + TPR * i) + j;
+                if (k < K) z[i][j] = z[i][j] * inv * nw[k] + nb[k];
+            }
     }
     if (input_silu) {
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) z[i] = z[i] * (1.0f / (1.0f + expf(-z[i])));
+        for (int i = 0; i < VPT; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) z[i][j] = z[i][j] * (1.0f / (1.0f + expf(-z[i][j])));
     }
     for (int c = 0; c < parts; ++c) {
         float amax = 0.f;
 #pragma unroll
-        for (int i = 0; i < CPL; ++i)
-            if (lane + 64 * i < K) amax = fmaxf(amax, fabsf(z[i]));
-        amax = wave_max(amax);
+        for (int i = 0; i < VPT; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(z[i][j]));
+        amax = row_reduce<WPR, true>(amax, red[rl], 2 + c, wave);
         float s = fmaxf(amax / 127.0f, 1.0e-30f);
         if (qs_dtype == KEA_F16) {
             _Float16 h = (_Float16)s;
@@ -90,22 +138,32 @@ quantize_kernel(const void *x, int x_dtype, long long xb, long long xt, long lon
             hs = fmaxf(hs, 5.9604644775390625e-08f);  // 2^-24, the smallest fp16 subnormal
             hs = fminf(hs, 65504.0f);
             s = hs;
-            if (lane == 0) ((_Float16 *)qs)[(long long)c * M + m] = (_Float16)s;
-        } else if (lane == 0) {
+            if (th == 0) ((_Float16 *)qs)[(long long)c * M + m] = (_Float16)s;
+        } else if (th == 0) {
             ((float *)qs)[(long long)c * M + m] = s;
         }
         int8_t *row = q + ((long long)c * M + m) * ldq;
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-            const int k = lane + 64 * i;
-            if (k < K) {
-                float v = rintf(z[i] / s);
+        for (int i = 0; i < VPT; ++i) {
+            const int k0 = 4 * (th + TPR * i);
+            uint32_t packed = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float v = rintf(z[i][j] / s);
                 v = fminf(fmaxf(v, -127.0f), 127.0f);
-                row[k] = (int8_t)(int)v;
-                z[i] = z[i] - v * s;
+                packed |= (uint32_t)(uint8_t)(int8_t)(int)v << (8 * j);
+                z[i][j] = z[i][j] - v * s;
+            }
+            if constexpr (VEC) {
+                if (k0 < K) *(uint32_t *)(row + k0) = packed;  // k0 + 3 < ldq: ldq >= K and ldq % 4 == 0
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (k0 + j < K) row[k0 + j] = (int8_t)(packed >> (8 * j));
             }
         }
-        for (long long k = K + lane; k < ldq; k += 64) row[k] = 0;
+        const long long kpad = VEC ? (long long)((K + 3) & ~3) : (long long)K;
+        for (long long k = kpad + th; k < ldq; k += TPR) row[k] = 0;
     }
 }
 
@@ -123,16 +181,31 @@ extern "C" int kea_quantize(const void *x, int x_dtype, int64_t xb, int64_t xt, 
     if ((norm_w == nullptr) != (norm_b == nullptr)) return kea::fail(KEA_EINVAL, "norm weight and bias go together");
     if (m == 0) return KEA_OK;
     if (!x || !q || !qs) return kea::fail(KEA_EINVAL, "x, q and qs are required");
-    const dim3 grid((unsigned)((m + kRowsPerBlock - 1) / kRowsPerBlock)), block(64 * kRowsPerBlock);
     hipStream_t st = (hipStream_t)stream;
-    const int cpl = (int)((k + 63) / 64);
-#define KEA_Q(N)                                                                                                  \
-    hipLaunchKernelGGL(quantize_kernel<N>, grid, block, 0, st, x, x_dtype, xb, xt, xk, t, (int)m, (int)k, parts, \
-                       norm_w, norm_b, eps, input_silu, q, ldq, qs, qs_dtype)
-    if (cpl <= 4) KEA_Q(4);
-    else if (cpl <= 16) KEA_Q(16);
-    else if (cpl <= 64) KEA_Q(64);
-    else KEA_Q(128);
+    const int esz = x_dtype == KEA_F16 ? 2 : 4;
+    const int wpr = k > 1024 ? 4 : 1;              // waves per row (the oracle restates this rule)
+    const int vpt = (int)((k + 256 * wpr - 1) / (256 * wpr));
+    const bool vec = xk == 1 && k % 4 == 0 && ldq % 4 == 0 && xb % 4 == 0 && xt % 4 == 0 &&
+                     ((uintptr_t)x % (4 * esz)) == 0 && ((uintptr_t)q % 4) == 0;
+    const dim3 grid((unsigned)((m + 4 / wpr - 1) / (4 / wpr))), block(256);
+#define KEA_Q(V, W)                                                                                                \
+    do {                                                                                                           \
+        if (vec)                                                                                                   \
+            hipLaunchKernelGGL((quantize_kernel<V, W, true>), grid, block, 0, st, x, x_dtype, xb, xt, xk, t,       \
+                               (int)m, (int)k, parts, norm_w, norm_b, eps, input_silu, q, ldq, qs, qs_dtype);       \
+        else                                                                                                       \
+            hipLaunchKernelGGL((quantize_kernel<V, W, false>), grid, block, 0, st, x, x_dtype, xb, xt, xk, t,      \
+                               (int)m, (int)k, parts, norm_w, norm_b, eps, input_silu, q, ldq, qs, qs_dtype);       \
+    } while (0)
+    if (wpr == 1) {
+        if (vpt <= 1) KEA_Q(1, 1);
+        else if (vpt <= 2) KEA_Q(2, 1);
+        else KEA_Q(4, 1);
+    } else {
+        if (vpt <= 2) KEA_Q(2, 4);
+        else if (vpt <= 4) KEA_Q(4, 4);
+        else KEA_Q(8, 4);
+    }
 #undef KEA_Q
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return kea::fail((int)e, std::string("quantize launch failed: ") + hipGetErrorString(e));

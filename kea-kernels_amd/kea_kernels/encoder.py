@@ -1,0 +1,395 @@
+"""A Parakeet-TDT-0.6B-shaped FastConformer encoder on the 1-bit layers (the workload of BASELINE.json config 5).
+
+The reference runs NeMo's encoder with its 264 quantized linears swapped for provider-backed modules
+(kk/binary/provider.py:212-262) and a set of offline fusions (kk/ternary/layer_fusions4.py,
+kk/ternary/transforms.py). NeMo is not part of this build, so this module is the build's own encoder with the same
+layer arithmetic (NeMo ConformerLayer with relative-position attention, as patched by
+kk/ternary/layer_fusions4.py:60-80):
+
+    x   = audio -> log-mel (128 bins) -> dw-striding subsampling x8 (Conv2d 3x3/2 + 2 x [depthwise 3x3/2 +
+          pointwise 1x1], ReLU) -> Linear(256 * 16 -> d) -> x * sqrt(d)
+    per layer (24):
+      r = x + 0.5 * FF1(LN(x))                      FF(z) = W2 silu(W1 z)
+      r = r + W_out RelPosMHSA(LN(r))               q, k, v = W_qkv z (fused), p = W_pos pos_emb (frozen per T)
+      r = r + W_pw2 silu(BN(dwconv9(GLU(W_pw1 LN(r)))))
+      r = r + 0.5 * FF2(LN(r))
+      x = LN_out(r)
+
+All 11 linears of a layer (W1, W2 of both FFs, W_q, W_k, W_v, W_out, W_pos, W_pw1, W_pw2; formats.PER_LAYER) are
+1-bit x int8 GEMMs through the provider seam (binary.provider.BinaryProjection over Int8MmaPartsLayer), with the
+LayerNorms in front of W1 / W_qkv / W_pw1 fused into the quantizer, SiLU after W1 fused into the GEMM epilogue and
+the SiLU in front of W_pw2 fused into the quantizer (the reference's norm_quant / silu transforms). Everything else
+(subsampling convolutions, attention core, GLU, depthwise convolution with BatchNorm folded into it, residual adds,
+the output LayerNorm) is PyTorch on the GPU. The quantized linears have no bias (Q/K/V must be bias-free to fuse,
+kk/binary/provider.py:230-244).
+
+`EncoderGraph` captures preprocessing + encoder for a fixed (batch, samples) into one HIP graph, as the reference
+captures its encoder (kk/ternary/graphs.py). `dense=True` builds the same model with the quantized linears replaced by
+FP32 matmuls on the dense weights (signs * alpha): the parity reference for the quantized encoder.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from kea_kernels import formats
+from kea_kernels.binary import bits, layer_parts, provider
+
+
+@dataclass(frozen=True)
+class EncoderConfig:
+    layers: int = 24
+    d_model: int = 1024
+    heads: int = 8
+    ff_mult: int = 4
+    conv_kernel: int = 9
+    feat_in: int = 128
+    sub_channels: int = 256
+    xscaling: bool = True
+    sample_rate: int = 16000
+    n_fft: int = 512
+    win_length: int = 400
+    hop_length: int = 160
+    preemph: float = 0.97
+    eps: float = 1e-5
+
+    @property
+    def d_ff(self) -> int:
+        return self.ff_mult * self.d_model
+
+
+def quantized_shapes(cfg: EncoderConfig) -> dict:
+    """{suffix: (N, K, kind)} of the 11 quantized linears of one layer."""
+    d, f = cfg.d_model, cfg.d_ff
+    return {"feed_forward1.linear1": (f, d, "linear"), "feed_forward1.linear2": (d, f, "linear"),
+            "feed_forward2.linear1": (f, d, "linear"), "feed_forward2.linear2": (d, f, "linear"),
+            "self_attn.linear_q": (d, d, "linear"), "self_attn.linear_k": (d, d, "linear"),
+            "self_attn.linear_v": (d, d, "linear"), "self_attn.linear_out": (d, d, "linear"),
+            "self_attn.linear_pos": (d, d, "linear"), "conv.pointwise_conv1": (2 * d, d, "conv"),
+            "conv.pointwise_conv2": (d, d, "conv")}
+
+
+def synthetic_weights(cfg: EncoderConfig, seed: int = 0) -> dict:
+    """Random-init parameters on the CPU (seeded torch.Generator). Quantized linears as export codes + FP32 scales
+    (alpha ~ U(0.5, 1.5) / sqrt(K), which keeps activations O(1) through the stack)."""
+    g = torch.Generator().manual_seed(seed)
+    d, c, h = cfg.d_model, cfg.sub_channels, cfg.heads
+
+    def randn(*shape, std=1.0):
+        return torch.randn(*shape, generator=g) * std
+
+    w = {}
+    shapes = quantized_shapes(cfg)
+    assert tuple(shapes) == tuple(sorted(shapes, key=formats.PER_LAYER.index))
+    for layer in range(cfg.layers):
+        pre = f"encoder.layers.{layer}."
+        for suffix, (n, k, _) in shapes.items():
+            signs = torch.where(torch.rand(n, k, generator=g) < 0.5, -1, 1).to(torch.int8)
+            w[pre + suffix + ".codes"] = bits.pack_signs(signs)
+            w[pre + suffix + ".scale"] = (torch.rand(n, generator=g) + 0.5) / math.sqrt(k)
+        for norm in ("norm_feed_forward1", "norm_self_att", "norm_conv", "norm_feed_forward2", "norm_out"):
+            w[pre + norm + ".weight"] = 1.0 + randn(d, std=0.05)
+            w[pre + norm + ".bias"] = randn(d, std=0.02)
+        w[pre + "self_attn.pos_bias_u"] = randn(h, d // h, std=0.02)
+        w[pre + "self_attn.pos_bias_v"] = randn(h, d // h, std=0.02)
+        w[pre + "conv.depthwise_conv.weight"] = randn(d, 1, cfg.conv_kernel, std=1.0 / 3.0)
+        w[pre + "conv.batch_norm.weight"] = 1.0 + randn(d, std=0.05)
+        w[pre + "conv.batch_norm.bias"] = randn(d, std=0.02)
+        w[pre + "conv.batch_norm.running_mean"] = randn(d, std=0.1)
+        w[pre + "conv.batch_norm.running_var"] = 1.0 + torch.rand(d, generator=g)
+    pre = "encoder.pre_encode."
+    w[pre + "conv.0.weight"] = randn(c, 1, 3, 3, std=1.0 / 3.0)
+    w[pre + "conv.0.bias"] = randn(c, std=0.02)
+    for i in (2, 5):
+        w[pre + f"conv.{i}.weight"] = randn(c, 1, 3, 3, std=1.0 / 3.0)
+        w[pre + f"conv.{i}.bias"] = randn(c, std=0.02)
+        w[pre + f"conv.{i + 1}.weight"] = randn(c, c, 1, 1, std=1.0 / math.sqrt(c))
+        w[pre + f"conv.{i + 1}.bias"] = randn(c, std=0.02)
+    sub_out = c * (cfg.feat_in // 8)
+    w[pre + "out.weight"] = randn(d, sub_out, std=1.0 / math.sqrt(sub_out))
+    w[pre + "out.bias"] = randn(d, std=0.02)
+    return w
+
+
+# --- preprocessing ---------------------------------------------------------------------------------------------------
+
+def mel_filterbank(cfg: EncoderConfig) -> np.ndarray:
+    """[n_mels, n_fft // 2 + 1] triangular filters on the Slaney mel scale with Slaney area normalisation (the
+    librosa default NeMo's preprocessor uses), FP64."""
+    def hz_to_mel(f):
+        f = np.asarray(f, np.float64)
+        lin = f / (200.0 / 3)
+        logstep = math.log(6.4) / 27.0
+        return np.where(f >= 1000.0, 15.0 + np.log(np.maximum(f, 1e-10) / 1000.0) / logstep, lin)
+
+    def mel_to_hz(m):
+        m = np.asarray(m, np.float64)
+        logstep = math.log(6.4) / 27.0
+        return np.where(m >= 15.0, 1000.0 * np.exp(logstep * (m - 15.0)), m * (200.0 / 3))
+
+    n_bins = cfg.n_fft // 2 + 1
+    fft_freqs = np.linspace(0, cfg.sample_rate / 2, n_bins)
+    mel_pts = mel_to_hz(np.linspace(hz_to_mel(0.0), hz_to_mel(cfg.sample_rate / 2), cfg.feat_in + 2))
+    fdiff = np.diff(mel_pts)
+    ramps = mel_pts[:, None] - fft_freqs[None, :]
+    lower = -ramps[:-2] / fdiff[:-1, None]
+    upper = ramps[2:] / fdiff[1:, None]
+    fb = np.maximum(0.0, np.minimum(lower, upper))
+    fb *= (2.0 / (mel_pts[2:cfg.feat_in + 2] - mel_pts[:cfg.feat_in]))[:, None]
+    return fb
+
+
+def frames_for(cfg: EncoderConfig, samples: int) -> int:
+    """Feature frames of a clip: samples / hop (the centred STFT's final frame is dropped: 160,000 -> 1000)."""
+    return samples // cfg.hop_length
+
+
+def encoded_length(frames: int) -> int:
+    for _ in range(3):
+        frames = (frames + 2 - 3) // 2 + 1
+    return frames
+
+
+class Preprocessor:
+    """audio [B, S] FP32 -> normalised log-mel [B, n_mels, frames]: pre-emphasis, |STFT|^2 (Hann 400 / hop 160 /
+    n_fft 512, centred), mel projection, log(x + 2^-24), per-feature mean / std normalisation over time."""
+
+    def __init__(self, cfg: EncoderConfig, device):
+        self.cfg = cfg
+        self.window = torch.hann_window(cfg.win_length, periodic=False, dtype=torch.float32, device=device)
+        self.fb = torch.from_numpy(mel_filterbank(cfg)).float().to(device)
+
+    def __call__(self, audio: Tensor) -> Tensor:
+        cfg = self.cfg
+        x = torch.cat([audio[:, :1], audio[:, 1:] - cfg.preemph * audio[:, :-1]], dim=1)
+        spec = torch.stft(x, n_fft=cfg.n_fft, hop_length=cfg.hop_length, win_length=cfg.win_length,
+                          window=self.window, center=True, pad_mode="constant", return_complex=True)
+        frames = frames_for(cfg, audio.shape[1])
+        power = torch.view_as_real(spec[:, :, :frames]).pow(2).sum(-1)          # [B, bins, frames]
+        mel = torch.matmul(self.fb, power)                                     # [B, mels, frames]
+        logmel = torch.log(mel + 2.0 ** -24)
+        mean = logmel.mean(dim=2, keepdim=True)
+        std = logmel.std(dim=2, keepdim=True) + 1e-5
+        return (logmel - mean) / std
+
+
+def relative_positions(cfg: EncoderConfig, t: int, device) -> Tensor:
+    """Sinusoidal encodings of relative positions t-1 .. -(t-1): [2t-1, d] (NeMo RelPositionalEncoding)."""
+    pos = torch.arange(t - 1, -t, -1, dtype=torch.float32, device=device)[:, None]
+    div = torch.exp(torch.arange(0, cfg.d_model, 2, dtype=torch.float32, device=device)
+                    * (-math.log(10000.0) / cfg.d_model))
+    pe = torch.zeros(2 * t - 1, cfg.d_model, device=device)
+    pe[:, 0::2] = torch.sin(pos * div)
+    pe[:, 1::2] = torch.cos(pos * div)
+    return pe
+
+
+def rel_shift(x: Tensor) -> Tensor:
+    """[B, H, T, 2T-1] scores against relative positions -> [B, H, T, T] (Transformer-XL shift, NeMo rel_shift)."""
+    b, h, t, p = x.shape
+    x = F.pad(x, (1, 0)).view(b, h, p + 1, t)[:, :, 1:].reshape(b, h, t, p)
+    return x[..., :t]
+
+
+# --- the encoder -----------------------------------------------------------------------------------------------------
+
+class _DenseLinear:
+    """FP32 dense stand-in for a quantized linear: signs * alpha (exact in FP32), y = z W^T."""
+
+    def __init__(self, codes: Tensor, scale: Tensor, k: int, device):
+        self.w = bits.dense_weight(codes, scale, k, dtype=torch.float32).to(device)
+        self.out_features, self.in_features = self.w.shape
+
+    def __call__(self, x, *, activation="", norm=None, input_activation=""):
+        z = x
+        if norm is not None:
+            z = F.layer_norm(z, norm[0].shape, norm[0], norm[1], norm[2])
+        if input_activation == "silu":
+            z = F.silu(z)
+        y = torch.matmul(z, self.w.t())
+        return F.silu(y) if activation == "silu" else y
+
+
+class _Norm:
+    """LayerNorm parameters in the shape the quantizer's fused LayerNorm reads (weight, bias, eps)."""
+
+    def __init__(self, weight: Tensor, bias: Tensor, eps: float):
+        self.weight, self.bias, self.eps = weight, bias, eps
+        self.normalized_shape = (weight.numel(),)
+
+
+class FastConformerEncoder:
+    """audio [B, S] -> encoder output [B, T', d]. parts = int8 activation parts of every quantized linear (1 = the
+    Kea-B x1 mode); dense=True swaps the quantized linears for FP32 dense matmuls (the parity reference)."""
+
+    def __init__(self, weights: dict, cfg: EncoderConfig = EncoderConfig(), device="cuda", *, parts: int = 1,
+                 dense: bool = False):
+        self.cfg, self.parts, self.dense = cfg, parts, dense
+        self.device = device = torch.device(device)
+        if device.type == "cuda" and device.index is None:
+            self.device = device = torch.device("cuda", torch.cuda.current_device())
+        self.pre = Preprocessor(cfg, device)
+        dev = lambda t: t.to(device=device, dtype=torch.float32)  # noqa: E731
+        p = "encoder.pre_encode."
+        self.sub = {k[len(p):]: dev(v) for k, v in weights.items() if k.startswith(p)}
+        self.layers = []
+        self._pos_cache: dict = {}
+        shapes = quantized_shapes(cfg)
+        quantized = {}
+        for layer in range(cfg.layers):
+            pre = f"encoder.layers.{layer}."
+            fp = {}
+            for norm in ("norm_feed_forward1", "norm_self_att", "norm_conv", "norm_feed_forward2", "norm_out"):
+                fp[norm] = _Norm(dev(weights[pre + norm + ".weight"]), dev(weights[pre + norm + ".bias"]), cfg.eps)
+            fp["u"] = dev(weights[pre + "self_attn.pos_bias_u"])
+            fp["v"] = dev(weights[pre + "self_attn.pos_bias_v"])
+            # BatchNorm (inference) folded into the depthwise convolution: w' = w * g / sqrt(var + eps),
+            # b' = beta - mean * g / sqrt(var + eps)
+            gain = weights[pre + "conv.batch_norm.weight"] / torch.sqrt(weights[pre + "conv.batch_norm.running_var"]
+                                                                         + cfg.eps)
+            fp["dw_w"] = dev(weights[pre + "conv.depthwise_conv.weight"] * gain[:, None, None])
+            fp["dw_b"] = dev(weights[pre + "conv.batch_norm.bias"] - weights[pre + "conv.batch_norm.running_mean"] * gain)
+            self.layers.append(fp)
+            for suffix, (n, k, kind) in shapes.items():
+                quantized[pre + suffix] = (weights[pre + suffix + ".codes"], weights[pre + suffix + ".scale"], None,
+                                           kind, k)
+        if dense:
+            self.linears = {name: _DenseLinear(codes, scale, k, device)
+                            for name, (codes, scale, _, _, k) in quantized.items()}
+            for layer in range(cfg.layers):
+                pre = f"encoder.layers.{layer}.self_attn."
+                parts = [self.linears[pre + x] for x in provider.QKV]
+                fused = _DenseLinear.__new__(_DenseLinear)
+                fused.w = torch.cat([x.w for x in parts])
+                fused.out_features, fused.in_features = fused.w.shape
+                self.linears[pre + "qkv"] = fused
+            self.table = None
+        else:
+            self.table, modules = provider.prepare_table(quantized, layer_parts.LAYERS[parts], device)
+            self.project = provider.PartCount(provider.BinaryProjection(self.table), parts)
+            self.modules = modules
+            self._fused = {}
+            for layer in range(cfg.layers):
+                pre = f"encoder.layers.{layer}.self_attn."
+                handle = torch.cat([modules[pre + x].packed_t for x in provider.QKV], 1)
+                self._fused[pre + "qkv"] = type("FusedQKV", (), {"packed_t": handle})()
+
+    # one quantized linear through the provider seam (or its dense stand-in)
+    def _linear(self, name: str, x: Tensor, *, activation="", norm=None, input_activation="") -> Tensor:
+        if self.dense:
+            nt = None if norm is None else (norm.weight, norm.bias, norm.eps)
+            return self.linears[name](x, activation=activation, norm=nt, input_activation=input_activation)
+        mod = self._fused.get(name) or self.modules[name]
+        return self.project(x, mod, False, self.parts, activation, norm, None, input_activation)
+
+    def weight_bytes(self) -> int:
+        return 0 if self.table is None else self.table.weight_bytes()
+
+    def subsample(self, feats: Tensor) -> Tensor:
+        """[B, mels, frames] -> [B, T', d] (dw-striding x8, then the output linear)."""
+        s = self.sub
+        c = self.cfg.sub_channels
+        x = feats.transpose(1, 2).unsqueeze(1)                                        # [B, 1, frames, mels]
+        x = F.relu(F.conv2d(x, s["conv.0.weight"], s["conv.0.bias"], stride=2, padding=1))
+        for i in (2, 5):
+            x = F.conv2d(x, s[f"conv.{i}.weight"], s[f"conv.{i}.bias"], stride=2, padding=1, groups=c)
+            x = F.relu(F.conv2d(x, s[f"conv.{i + 1}.weight"], s[f"conv.{i + 1}.bias"]))
+        b, _, t, f = x.shape
+        x = x.transpose(1, 2).reshape(b, t, c * f)
+        return F.linear(x, s["out.weight"], s["out.bias"])
+
+    def positions(self, t: int) -> list:
+        """W_pos applied to the relative encodings, per layer, for length t: [H, 2t-1, dk] each. Frozen per length
+        (the reference freezes them for graph capture too, kk/ternary/transforms.py:18-21); computed with the same
+        quantized GEMM as every other call."""
+        hit = self._pos_cache.get(t)
+        if hit is None:
+            cfg = self.cfg
+            pe = relative_positions(cfg, t, self.device).unsqueeze(0)
+            hit = []
+            for layer in range(cfg.layers):
+                p = self._linear(f"encoder.layers.{layer}.self_attn.linear_pos", pe)[0]
+                hit.append(p.view(2 * t - 1, cfg.heads, -1).permute(1, 2, 0).contiguous())  # [H, dk, 2t-1]
+            self._pos_cache[t] = hit
+        return hit
+
+    def attention(self, qkv: Tensor, pos_t: Tensor, u: Tensor, v_bias: Tensor) -> Tensor:
+        b, t, _ = qkv.shape
+        h = self.cfg.heads
+        dk = self.cfg.d_model // h
+        q, k, v = qkv.view(b, t, 3, h, dk).unbind(2)
+        qu = (q + u).transpose(1, 2).contiguous()                                   # [B, H, T, dk]
+        qv = (q + v_bias).transpose(1, 2).contiguous()
+        kt = k.permute(0, 2, 3, 1).contiguous()                                     # [B, H, dk, T]
+        ac = torch.matmul(qu, kt)
+        bd = rel_shift(torch.matmul(qv, pos_t))                                     # [B, H, T, T]
+        attn = torch.softmax((ac + bd) * (1.0 / math.sqrt(dk)), dim=-1)
+        out = torch.matmul(attn, v.transpose(1, 2).contiguous())                    # [B, H, T, dk]
+        return out.transpose(1, 2).reshape(b, t, h * dk)
+
+    def layer(self, i: int, x: Tensor, pos_t: Tensor) -> Tensor:
+        fp = self.layers[i]
+        pre = f"encoder.layers.{i}."
+        y = self._linear(pre + "feed_forward1.linear1", x, norm=fp["norm_feed_forward1"], activation="silu")
+        r = torch.add(x, self._linear(pre + "feed_forward1.linear2", y), alpha=0.5)
+        qkv = self._linear(pre + "self_attn.qkv", r, norm=fp["norm_self_att"])
+        r = r + self._linear(pre + "self_attn.linear_out", self.attention(qkv, pos_t, fp["u"], fp["v"]))
+        z = self._linear(pre + "conv.pointwise_conv1", r, norm=fp["norm_conv"])
+        z = F.glu(z, dim=-1)                                                        # a * sigmoid(g)
+        z = F.conv1d(z.transpose(1, 2), fp["dw_w"], fp["dw_b"], padding=self.cfg.conv_kernel // 2,
+                     groups=self.cfg.d_model).transpose(1, 2)
+        r = r + self._linear(pre + "conv.pointwise_conv2", z, input_activation="silu")
+        y = self._linear(pre + "feed_forward2.linear1", r, norm=fp["norm_feed_forward2"], activation="silu")
+        r = torch.add(r, self._linear(pre + "feed_forward2.linear2", y), alpha=0.5)
+        n = fp["norm_out"]
+        return F.layer_norm(r, n.normalized_shape, n.weight, n.bias, n.eps)
+
+    def encode(self, feats: Tensor) -> Tensor:
+        x = self.subsample(feats)
+        if self.cfg.xscaling:
+            x = x * math.sqrt(self.cfg.d_model)
+        pos = self.positions(x.shape[1])
+        for i in range(self.cfg.layers):
+            x = self.layer(i, x, pos[i])
+        return x
+
+    @torch.inference_mode()
+    def __call__(self, audio: Tensor) -> Tensor:
+        return self.encode(self.pre(audio))
+
+
+class EncoderGraph:
+    """One HIP graph of preprocessing + encoder for a fixed (batch, samples); __call__ copies the audio into the
+    graph's input buffer, replays and returns the graph's output buffer (overwritten by the next call)."""
+
+    def __init__(self, encoder: FastConformerEncoder, batch: int, samples: int, *, warmup: int = 2):
+        self.encoder = encoder
+        dev = encoder.device
+        self.audio = torch.zeros(batch, samples, device=dev)
+        self.stream = torch.cuda.Stream(dev)
+        with torch.inference_mode():
+            encoder.positions(encoded_length(frames_for(encoder.cfg, samples)))
+            with torch.cuda.stream(self.stream):
+                for _ in range(warmup):
+                    encoder(self.audio)
+            torch.cuda.synchronize(dev)
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph, stream=self.stream):
+                self.out = encoder(self.audio)
+        torch.cuda.synchronize(dev)
+
+    def replay(self) -> Tensor:
+        with torch.cuda.stream(self.stream):
+            self.graph.replay()
+        return self.out
+
+    def __call__(self, audio: Tensor) -> Tensor:
+        with torch.cuda.stream(self.stream):
+            self.audio.copy_(audio)
+            self.graph.replay()
+        return self.out

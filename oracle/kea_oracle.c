@@ -214,19 +214,31 @@ static float f16_to_f32(uint16_t h) {
 
 /* Sum of z[0..k) in the library's fixed order: 64 lane partials (lane l sums k = l, l + 64, ... in increasing k),
  * then a xor butterfly with offsets 32, 16, 8, 4, 2, 1 (lane 0's value). */
-static float lane_sum(const float *z, int64_t k) {
-    float p[64];
-    for (int l = 0; l < 64; ++l) {
+/*
+ * The library's fixed LayerNorm summation order: a row is split over WPR wave64s (1 for k <= 1024, else 4); thread th
+ * of the row sums, in increasing k, its 4-element chunks k = 4 * (th + 64 * WPR * i) + j; each wave combines its 64
+ * partial sums with a xor butterfly (offsets 32, 16, ..., 1); the wave totals are then added in wave order.
+ */
+static float row_sum(const float *z, int64_t k) {
+    const int wpr = k > 1024 ? 4 : 1, tpr = 64 * wpr;
+    float p[256];
+    for (int th = 0; th < tpr; ++th) {
         float s = 0.f;
-        for (int64_t i = l; i < k; i += 64) s = s + z[i];
-        p[l] = s;
+        for (int64_t c = 4 * (int64_t)th; c < k; c += 4 * (int64_t)tpr)
+            for (int64_t kk = c; kk < c + 4 && kk < k; ++kk) s = s + z[kk];
+        p[th] = s;
     }
-    for (int off = 32; off >= 1; off >>= 1) {
-        float nxt[64];
-        for (int l = 0; l < 64; ++l) nxt[l] = p[l] + p[l ^ off];
-        memcpy(p, nxt, sizeof(p));
+    float total = 0.f;
+    for (int w = 0; w < wpr; ++w) {
+        float *v = p + 64 * w;
+        for (int off = 32; off >= 1; off >>= 1) {
+            float nxt[64];
+            for (int l = 0; l < 64; ++l) nxt[l] = v[l] + v[l ^ off];
+            memcpy(v, nxt, sizeof(nxt));
+        }
+        total = w == 0 ? v[0] : total + v[0];
     }
-    return p[0];
+    return total;
 }
 
 /*
@@ -249,10 +261,10 @@ EXPORT int oracle_quantize(const void *x, int x_f16, int64_t xb, int64_t xt, int
                 z[kk] = x_f16 ? f16_to_f32(((const uint16_t *)x)[i]) : ((const float *)x)[i];
             }
             if (nw) {
-                const float mean = lane_sum(z, k) / (float)k;
+                const float mean = row_sum(z, k) / (float)k;
                 for (int64_t kk = 0; kk < k; ++kk) z[kk] = z[kk] - mean;
                 for (int64_t kk = 0; kk < k; ++kk) sq[kk] = z[kk] * z[kk];
-                const float var = lane_sum(sq, k) / (float)k;
+                const float var = row_sum(sq, k) / (float)k;
                 const float inv = 1.0f / sqrtf(var + eps);
                 for (int64_t kk = 0; kk < k; ++kk) z[kk] = z[kk] * inv * nw[kk] + nb[kk];
             }

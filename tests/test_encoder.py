@@ -1,0 +1,100 @@
+"""The synthetic FastConformer encoder: host-side pieces on the CPU, the quantized encoder
+against its FP32 dense twin on the GPU (relative Frobenius error bars per part count), and graph replay = eager."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from kea_kernels import encoder as E
+
+
+def test_rel_shift_matches_the_relative_index():
+    """rel_shift(bd)[i, j] must be the score of query i against relative position i - j, i.e. column (T-1) - (i-j)
+    of the [2T-1] relative axis (positions T-1 .. -(T-1))."""
+    t = 7
+    x = torch.arange(t * (2 * t - 1), dtype=torch.float32).view(1, 1, t, 2 * t - 1)
+    y = E.rel_shift(x)
+    for i in range(t):
+        for j in range(t):
+            assert y[0, 0, i, j] == x[0, 0, i, (t - 1) - (i - j)]
+
+
+def test_relative_positions_closed_form():
+    cfg = E.EncoderConfig(d_model=8)
+    pe = E.relative_positions(cfg, 3, "cpu")
+    assert pe.shape == (5, 8)
+    for row, pos in enumerate([2, 1, 0, -1, -2]):
+        for i in range(4):
+            w = math.exp(-(2 * i) * math.log(10000.0) / 8)
+            assert abs(float(pe[row, 2 * i]) - math.sin(pos * w)) < 1e-6
+            assert abs(float(pe[row, 2 * i + 1]) - math.cos(pos * w)) < 1e-6
+
+
+def test_mel_filterbank_is_triangular_and_area_normalised():
+    cfg = E.EncoderConfig()
+    fb = E.mel_filterbank(cfg)
+    assert fb.shape == (128, 257) and (fb >= 0).all()
+    peaks = fb.argmax(axis=1)
+    assert (np.diff(peaks) >= 0).all()
+    # Slaney normalisation: height 2 / bandwidth gives every triangle unit area in Hz (sampled at FFT bins)
+    hz = np.linspace(0, cfg.sample_rate / 2, 257)
+    area = (fb * (hz[1] - hz[0])).sum(axis=1)
+    assert ((area[48:] > 0.9) & (area[48:] < 1.12)).all()  # wide filters: sampled area close to 1
+
+
+def test_lengths_and_batchnorm_fold():
+    cfg = E.EncoderConfig(layers=1)
+    assert E.frames_for(cfg, 160000) == 1000 and E.encoded_length(1000) == 125
+    w = E.synthetic_weights(cfg, seed=3)
+    enc = E.FastConformerEncoder(w, cfg, "cpu", dense=True)
+    pre = "encoder.layers.0.conv."
+    x = torch.randn(2, cfg.d_model, 20)
+    bn = torch.nn.BatchNorm1d(cfg.d_model, eps=cfg.eps).eval()
+    bn.weight.data, bn.bias.data = w[pre + "batch_norm.weight"], w[pre + "batch_norm.bias"]
+    bn.running_mean, bn.running_var = w[pre + "batch_norm.running_mean"], w[pre + "batch_norm.running_var"]
+    ref = bn(F.conv1d(x, w[pre + "depthwise_conv.weight"], padding=4, groups=cfg.d_model))
+    got = F.conv1d(x, enc.layers[0]["dw_w"], enc.layers[0]["dw_b"], padding=4, groups=cfg.d_model)
+    torch.testing.assert_close(got, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_dense_encoder_runs_on_cpu():
+    cfg = E.EncoderConfig(layers=2)
+    enc = E.FastConformerEncoder(E.synthetic_weights(cfg, seed=1), cfg, "cpu", dense=True)
+    out = enc(torch.randn(2, 160000, generator=torch.Generator().manual_seed(0)))
+    assert out.shape == (2, 125, 1024) and torch.isfinite(out).all()
+    assert 0.5 < float(out.std()) < 2.0  # LayerNorm output
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("parts,tol", [(1, 5e-2), (2, 5e-4), (3, 5e-6)])
+@torch.inference_mode()
+def test_quantized_encoder_matches_dense_fp32(parts, tol):
+    """4 layers, batch 2: the int8-activation encoder against the same weights as FP32 dense matmuls. The bars are
+    the per-layer precision of P int8 parts (the reference's P-dependent linear bars 2e-2 / 1e-4 / 1e-6,
+    tests/test_kernels_gpu.py:47-57) widened for four layers of error propagation."""
+    cfg = E.EncoderConfig(layers=4)
+    w = E.synthetic_weights(cfg, seed=11)
+    audio = torch.randn(2, 160000, generator=torch.Generator().manual_seed(12)).cuda()
+    quant = E.FastConformerEncoder(w, cfg, "cuda", parts=parts)(audio)
+    dense = E.FastConformerEncoder(w, cfg, "cuda", dense=True)(audio)
+    rel = float((quant.double() - dense.double()).norm() / dense.double().norm())
+    assert rel < tol, rel
+
+
+@pytest.mark.gpu
+@torch.inference_mode()
+def test_encoder_graph_replays_equal_eager():
+    cfg = E.EncoderConfig(layers=3)
+    enc = E.FastConformerEncoder(E.synthetic_weights(cfg, seed=4), cfg, "cuda", parts=1)
+    audio = torch.randn(1, 48000, generator=torch.Generator().manual_seed(5)).cuda()
+    eager = enc(audio)
+    graph = E.EncoderGraph(enc, 1, 48000)
+    for _ in range(3):
+        got = graph(audio)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(got, eager, rtol=0, atol=0)
+        _ = enc(audio)  # eager work between replays

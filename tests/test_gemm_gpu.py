@@ -207,7 +207,7 @@ def test_zero_rows_is_a_no_op():
 
 # --- the quantizer ------------------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("k", [300, 1024, 4096])
+@pytest.mark.parametrize("k", [17, 256, 300, 1024, 1500, 2050, 4096, 8192])
 @pytest.mark.parametrize("with_norm", [False, True])
 @torch.inference_mode()
 def test_quantizer_bitwise_against_oracle(k, with_norm):
@@ -229,6 +229,27 @@ def test_quantizer_bitwise_against_oracle(k, with_norm):
     rq, rqs = O.quantize(x.numpy(), 3, ldq=ldq,
                          norm=None if norm is None else (norm.weight.detach().numpy(), norm.bias.detach().numpy()),
                          eps=1e-5)
+    assert np.array_equal(q.cpu().numpy(), rq)
+    assert np.array_equal(qs.cpu().numpy(), rqs)
+
+
+@pytest.mark.parametrize("k", [64, 1024, 2048])
+@torch.inference_mode()
+def test_quantizer_strided_rows_bitwise(k):
+    """x [B, K, T] read as rows (b, t) with element stride T (the pointwise-convolution layout)."""
+    g = torch.Generator().manual_seed(k)
+    x = torch.randn(3, k, 41, generator=g)
+    norm = torch.nn.LayerNorm(k)
+    with torch.no_grad():
+        norm.weight.copy_(torch.rand(k, generator=g) + 0.5)
+        norm.bias.copy_(torch.randn(k, generator=g) * 0.1)
+    dnorm = torch.nn.LayerNorm(k).to(DEV)
+    dnorm.load_state_dict(norm.state_dict())
+    xd = x.to(DEV)
+    q, qs, ldq = lowbit.quantize(xd, (xd.stride(0), xd.stride(2), xd.stride(1), 41), 3 * 41, k, 2, norm=dnorm)
+    torch.cuda.synchronize()
+    rows = x.transpose(1, 2).reshape(3 * 41, k).contiguous().numpy()
+    rq, rqs = O.quantize(rows, 2, ldq=ldq, norm=(norm.weight.detach().numpy(), norm.bias.detach().numpy()), eps=1e-5)
     assert np.array_equal(q.cpu().numpy(), rq)
     assert np.array_equal(qs.cpu().numpy(), rqs)
 
