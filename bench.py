@@ -241,12 +241,13 @@ def encoder_bench(batch: int, parts: int, reps: int = 20, seed: int = 5) -> dict
     torch.cuda.synchronize()
     graph_diff = float((got - out).abs().max())
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for _ in range(3):
-        graph.replay()
-    a.record(graph.stream)
-    for _ in range(reps):
-        graph.replay()
-    b.record(graph.stream)
+    with torch.cuda.stream(graph.stream):  # replays back to back on the graph's own stream
+        for _ in range(3):
+            graph.graph.replay()
+        a.record(graph.stream)
+        for _ in range(reps):
+            graph.graph.replay()
+        b.record(graph.stream)
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / reps
     dense = E.FastConformerEncoder(weights, cfg, "cuda", dense=True)

@@ -1,0 +1,44 @@
+/*
+ * kea_encoder.h - fused FastConformer encoder kernels of libkea_hip.so (MI355X / gfx950), FP32.
+ *
+ * Conventions as in kea_lowbit.h: device pointers, int64 sizes and strides (in elements), a hipStream_t as void*,
+ * KEA_OK / negative KEA_E* (nothing launched) / positive hipError_t, message in kea_last_error(). No allocation, no
+ * host synchronisation: both entry points are HIP-graph capturable.
+ */
+#ifndef KEA_ENCODER_H
+#define KEA_ENCODER_H
+
+#include <stdint.h>
+
+#include "kea_lowbit.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Relative-position multi-head self-attention (Transformer-XL form of NeMo's RelPositionMultiHeadAttention):
+ *   for batch b, head h, query i, key j (T tokens, heads x head_dim = d):
+ *     s[i][j] = ((q_i + u_h) . k_j + (q_i + v_h) . p_{T-1-i+j}) * scale,  out_i = sum_j softmax_j(s)[i][j] v_j
+ *   q, k, v of token t: qkv[(b*T + t)*ld + {0, d, 2d} + h*head_dim + 0 .. head_dim-1]   (the fused QKV projection)
+ *   p_r (relative position T-1-r, r = 0 .. 2T-2): pos[r*ldp + h*head_dim + ...]        (W_pos applied, [2T-1][>= d])
+ *   bias_u, bias_v: [heads][head_dim];  out: out[(b*T + t)*ldo + h*head_dim + ...].
+ * head_dim must be 128 and T <= 256; qkv, pos and out 16-byte aligned with ld, ldp, ldo multiples of 4.
+ * Replaces the reference's relative_attention + Triton _attention / _position_scores
+ * (kk/ternary/fused_kernels.py:163-240). */
+int kea_relpos_attention(const float *qkv_dev, int64_t ld, const float *pos_dev, int64_t ldp,
+                         const float *bias_u_dev, const float *bias_v_dev, float *out_dev, int64_t ldo,
+                         int64_t batch, int64_t t, int heads, int head_dim, float scale, void *stream);
+
+/* GLU + depthwise convolution (BatchNorm folded into w and bias by the caller):
+ *   y[(b*T + t)*ldy + c] = bias[c] + sum_{j<kernel} w[c*kernel + j] * glu(b, t + j - kernel/2, c)
+ *   glu(b, t, c) = x[(b*T + t)*ldx + c] * sigmoid(x[(b*T + t)*ldx + channels + c]), 0 outside [0, T).
+ * kernel odd; bias may be NULL. Replaces the reference's _glu_pad + depthwise Conv1d + batch_norm of the patched
+ * convolution module (kk/ternary/layer_fusions4.py:10-30, :62-72). */
+int kea_glu_dwconv(const float *x_dev, int64_t ldx, const float *w_dev, const float *bias_dev, float *y_dev,
+                   int64_t ldy, int64_t batch, int64_t t, int64_t channels, int kernel, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KEA_ENCODER_H */

@@ -124,6 +124,22 @@ int kea_lowbit_gemm(int wbits,
                     int64_t m, int flags, int split_k, int config,
                     void *workspace_dev, int64_t workspace_bytes, void *stream);
 
+/* kea_lowbit_gemm plus a residual stream: y[m*ldy + n] = residual[m*ldr + n] + r * factor (an IEEE multiply, then an
+ * IEEE add), with r the epilogue value above (after bias and SiLU). residual is FP32 [m][ldr], ldr >= n; y may be
+ * the residual itself (in place, with ldy == ldr and y_dtype KEA_F32). Replaces the residual step of the reference's
+ * row epilogue, x = R + value * FACTOR (kk/ternary/row_fusion.py:28-39, :90-113). */
+int kea_lowbit_gemm_residual(int wbits,
+                             const int8_t *q_dev, int64_t part_stride, int64_t ldq, int parts,
+                             const void *qs_dev, int qs_dtype, int64_t qs_stride,
+                             const uint32_t *w_dev, int64_t n, int64_t k,
+                             const void *wscale_dev, int ws_dtype, int64_t ws_group,
+                             const void *bias_dev, int bias_dtype,
+                             void *y_dev, int y_dtype, int64_t ldy,
+                             int32_t *acc_out_dev, int64_t acc_ld,
+                             int64_t m, int flags, int split_k, int config,
+                             void *workspace_dev, int64_t workspace_bytes,
+                             const float *residual_dev, int64_t ldr, float factor, void *stream);
+
 /* Exact deferred split-K: the K range is cut into `split` slices (split >= 1, at most ceil(J/4) where J is the number
  * of native words per lane) and slice z writes its exact int32 partial accumulators to
  * slices_dev[((z * parts + c) * m + row) * n + col] (int32 [split][parts][m][n], 16-byte aligned). No scale is read.

@@ -20,7 +20,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "kea_kernels" / "lib" / "libkea_hip.so"
-SOURCES = ["kea_gemm.hip", "kea_quantize.hip", "kea_layout.cpp"]
+SOURCES = ["kea_gemm.hip", "kea_quantize.hip", "kea_encoder.hip", "kea_layout.cpp"]
 ARCH = "gfx950"
 
 

@@ -62,6 +62,9 @@ struct Params {
     int y_vec;      // 1: y rows allow aligned 4-element vector stores
     int acc_vec;    // 1: acc_out rows allow aligned int4 stores
     int slice_vec;  // 1: the dense [S][P][M][N] slices allow aligned int4 access (N % 4 == 0)
+    const float *res;   // optional residual: y = res[m * ldr + n] + value * res_factor (two roundings)
+    long long ldr;
+    float res_factor;
     int groups;     // per-group scales: G = ceil(K / ws_group) groups, alpha [N][G]
     int gp_shift;   // log2 of the padded group count held in LDS (a power of two >= the groups the stages span)
 };
@@ -160,7 +163,22 @@ struct EpiOperands {
     float s[3];      // per-token scales of the P parts
     float alpha[4];  // per-channel scales
     float bias[4];
+    float res[4];    // residual values (when Params::res is set)
 };
+
+// Residual values of row m, columns nb..nb+3 (clamped indices; the clamped values are never stored).
+__device__ __forceinline__ void load_residual(const Params &p, int m, int nb, float *r) {
+    if (!p.res) return;
+    const int mm = m < p.M ? m : p.M - 1;
+    const float *src = p.res + (long long)mm * p.ldr;
+    if ((p.ldr & 3) == 0 && ((uintptr_t)p.res & 15) == 0 && nb + 3 < p.N) {
+        const float4 v = *(const float4 *)(src + nb);
+        r[0] = v.x; r[1] = v.y; r[2] = v.z; r[3] = v.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = src[nb + i < p.N ? nb + i : p.N - 1];
+    }
+}
 
 template <int P>
 __device__ __forceinline__ void load_row_scales(const Params &p, int m, EpiOperands &e) {
@@ -187,6 +205,7 @@ __device__ __forceinline__ void epilogue4(const Params &p, int m, int nb, const 
         for (int r = 0; r < 4; ++r) {
             int ar[3] = {a[0][r], P > 1 ? a[1][r] : 0, P > 2 ? a[2][r] : 0};
             v[r] = finish(combine<P>(ar, e.s, p.flags), e.alpha[r], p.bias != nullptr, e.bias[r], p.flags);
+            if (p.res) v[r] = e.res[r] + v[r] * p.res_factor;
         }
         store4(p, (long long)m * p.ldy + nb, nb, v);
     }
@@ -209,6 +228,7 @@ __device__ __forceinline__ void epilogue4_groups(const Params &p, int m, int nb,
             float x = racc[r];
             if (p.bias) x = x + e.bias[r];
             if (p.flags & KEA_FLAG_SILU) x = x / (1.0f + expf(-x));
+            if (p.res) x = e.res[r] + x * p.res_factor;
             v[r] = x;
         }
         store4(p, (long long)m * p.ldy + nb, nb, v);
@@ -536,6 +556,20 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
         for (int jn = 0; jn < RN; ++jn)
             load_col_scales(p, n0 + (wn * RN + jn) * 16 + (lane >> 4) * 4, cols[jn], GQ == 0);
     }
+    // Residual values: prefetched with the other epilogue operands on small tiles, loaded in the epilogue otherwise
+    // (keeps the register budget of the wide tiles).
+    constexpr bool RES_PREFETCH = !SLICED && RM * RN <= 2;
+    float resv[RES_PREFETCH ? RM : 1][RES_PREFETCH ? RN : 1][4];
+    if constexpr (RES_PREFETCH) {
+        if (p.res) {
+#pragma unroll
+            for (int i = 0; i < RM; ++i)
+#pragma unroll
+                for (int jn = 0; jn < RN; ++jn)
+                    load_residual(p, m0 + (wm * RM + i) * 16 + (lane & 15), n0 + (wn * RN + jn) * 16 + (lane >> 4) * 4,
+                                  resv[i][jn]);
+        }
+    }
 
     // Per-group scales: the tile's alpha rows [n0, n0 + BN) x groups [0, 2^gp_shift) go to LDS as f32 in chunks of
     // ACH values per lane (zero past the last group; rows past N clamped, never stored). The first chunk's loads are
@@ -609,13 +643,18 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
                 for (int c = 0; c < P; ++c)
                     store_int4(p.slices + (((long long)blockIdx.z * P + c) * p.M + m) * p.N + nb, p.slice_vec, nb,
                                p.N, a[c]);
-            } else if constexpr (GQ > 0) {
-                epilogue4_groups<P>(p, m, nb, a, racc[i][jn], cols[jn]);
             } else {
                 EpiOperands e = cols[jn];
 #pragma unroll
                 for (int c = 0; c < 3; ++c) e.s[c] = rows[i].s[c];
-                epilogue4<P>(p, m, nb, a, e);
+                if constexpr (RES_PREFETCH) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) e.res[r] = resv[i][jn][r];
+                } else {
+                    load_residual(p, m, nb, e.res);
+                }
+                if constexpr (GQ > 0) epilogue4_groups<P>(p, m, nb, a, racc[i][jn], e);
+                else epilogue4<P>(p, m, nb, a, e);
             }
         }
     }
@@ -667,6 +706,7 @@ __global__ void __launch_bounds__(256) finish_kernel(Params p, int S) {
     EpiOperands e;
     load_row_scales<P>(p, m, e);
     load_col_scales(p, nb, e);
+    load_residual(p, m, nb, e.res);
     epilogue4<P>(p, m, nb, a, e);
 }
 
@@ -867,11 +907,12 @@ int kea_lowbit_gemm_split(int wbits, int parts, int64_t m, int64_t n, int64_t k,
     return s;
 }
 
-int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts, const void *qs,
-                    int qs_dtype, int64_t qs_stride, const uint32_t *w, int64_t n, int64_t k, const void *wscale,
-                    int ws_dtype, int64_t ws_group, const void *bias, int bias_dtype, void *y, int y_dtype,
-                    int64_t ldy, int32_t *acc_out, int64_t acc_ld, int64_t m, int flags, int split_k, int config,
-                    void *workspace, int64_t workspace_bytes, void *stream) {
+static int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts, const void *qs,
+                     int qs_dtype, int64_t qs_stride, const uint32_t *w, int64_t n, int64_t k, const void *wscale,
+                     int ws_dtype, int64_t ws_group, const void *bias, int bias_dtype, void *y, int y_dtype,
+                     int64_t ldy, int32_t *acc_out, int64_t acc_ld, int64_t m, int flags, int split_k, int config,
+                     void *workspace, int64_t workspace_bytes, const float *residual, int64_t ldr, float factor,
+                     void *stream) {
     int tile, s, qps, gq = 0;
     if (ws_group != 0) {
         if (ws_group != 64 && ws_group != 128 && ws_group != 256)
@@ -895,6 +936,8 @@ int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq
         return kea::fail(KEA_EINVAL, "y dtype must be f32, f16 or bf16");
     if (y && ldy < n) return kea::fail(KEA_EINVAL, "ldy < n");
     if (acc_out && acc_ld < n) return kea::fail(KEA_EINVAL, "acc_ld < n");
+    if (residual && !y) return kea::fail(KEA_EINVAL, "a residual needs y");
+    if (residual && ldr < n) return kea::fail(KEA_EINVAL, "ldr < n");
     if (m == 0) return KEA_OK;
     if (!q) return kea::fail(KEA_EINVAL, "q is required");
     if (ldq < k) return kea::fail(KEA_EINVAL, "ldq < k");
@@ -912,6 +955,7 @@ int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq
     p.bias = bias; p.bias_dtype = bias_dtype;
     p.y = y; p.ldy = ldy; p.y_dtype = y_dtype;
     p.acc = acc_out; p.acc_ld = acc_ld;
+    p.res = residual; p.ldr = ldr; p.res_factor = factor;
     p.M = (int)m; p.N = (int)n; p.K = (int)k;
     p.J = (int)(wbits == 1 ? cdivl(k, 128) : cdivl(k, 64));
     p.NT = (int)cdivl(n, 16);
@@ -967,6 +1011,28 @@ int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq
         if (e != hipSuccess) return kea::fail((int)e, std::string("finish launch failed: ") + hipGetErrorString(e));
     }
     return KEA_OK;
+}
+
+int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts, const void *qs,
+                    int qs_dtype, int64_t qs_stride, const uint32_t *w, int64_t n, int64_t k, const void *wscale,
+                    int ws_dtype, int64_t ws_group, const void *bias, int bias_dtype, void *y, int y_dtype,
+                    int64_t ldy, int32_t *acc_out, int64_t acc_ld, int64_t m, int flags, int split_k, int config,
+                    void *workspace, int64_t workspace_bytes, void *stream) {
+    return gemm_impl(wbits, q, part_stride, ldq, parts, qs, qs_dtype, qs_stride, w, n, k, wscale, ws_dtype, ws_group,
+                     bias, bias_dtype, y, y_dtype, ldy, acc_out, acc_ld, m, flags, split_k, config, workspace,
+                     workspace_bytes, nullptr, 0, 0.f, stream);
+}
+
+int kea_lowbit_gemm_residual(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts, const void *qs,
+                             int qs_dtype, int64_t qs_stride, const uint32_t *w, int64_t n, int64_t k,
+                             const void *wscale, int ws_dtype, int64_t ws_group, const void *bias, int bias_dtype,
+                             void *y, int y_dtype, int64_t ldy, int32_t *acc_out, int64_t acc_ld, int64_t m, int flags,
+                             int split_k, int config, void *workspace, int64_t workspace_bytes, const float *residual,
+                             int64_t ldr, float factor, void *stream) {
+    if (!residual) return kea::fail(KEA_EINVAL, "residual is required");
+    return gemm_impl(wbits, q, part_stride, ldq, parts, qs, qs_dtype, qs_stride, w, n, k, wscale, ws_dtype, ws_group,
+                     bias, bias_dtype, y, y_dtype, ldy, acc_out, acc_ld, m, flags, split_k, config, workspace,
+                     workspace_bytes, residual, ldr, factor, stream);
 }
 
 int kea_lowbit_gemm_slices(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts,

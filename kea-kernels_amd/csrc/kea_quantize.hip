@@ -70,6 +70,18 @@ quantize_kernel(const void *x, int x_dtype, long long xb, long long xt, long lon
     const int m = blockIdx.x * RPB + rl;
     if (m >= M) return;  // whole rows leave together: the row's barriers stay matched
     const long long base = (long long)(m / t) * xb + (long long)(m % t) * xt;
+    // LayerNorm weights are loaded with the row (their latency overlaps the row's and the reductions')
+    float lw[VPT][4], lb[VPT][4];
+    if (nw) {
+#pragma unroll
+        for (int i = 0; i < VPT; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = 4 * (th + TPR * i) + j;
+                lw[i][j] = k < K ? nw[k] : 0.f;
+                lb[i][j] = k < K ? nb[k] : 0.f;
+            }
+    }
     float z[VPT][4];
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
@@ -115,7 +127,7 @@ quantize_kernel(const void *x, int x_dtype, long long xb, long long xt, long lon
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int k = 4 * (th + TPR * i) + j;
-                if (k < K) z[i][j] = z[i][j] * inv * nw[k] + nb[k];
+                if (k < K) z[i][j] = z[i][j] * inv * lw[i][j] + lb[i][j];
             }
     }
     if (input_silu) {

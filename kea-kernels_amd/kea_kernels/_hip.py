@@ -34,6 +34,9 @@ SIGNATURES = {
     "kea_t2_unlayout_host": (_i32, [_vp, _i64, _i64, _vp]),
     "kea_lowbit_gemm": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _vp, _i32, _i64,
                                _vp, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _i64, _vp]),
+    "kea_lowbit_gemm_residual": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _vp, _i32,
+                                        _i64, _vp, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _i32, _i32, _i32, _vp,
+                                        _i64, _vp, _i64, _f32, _vp]),
     "kea_lowbit_gemm_slices": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _vp]),
     "kea_lowbit_slices_finish": (_i32, [_vp, _i32, _i32, _i64, _i64, _vp, _i32, _i64, _vp, _i32, _vp, _i32, _vp,
                                         _i32, _i64, _vp, _i64, _i32, _vp]),
@@ -44,6 +47,8 @@ SIGNATURES = {
     "kea_config_name": (_cp, [_i32]),
     "kea_quantize": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _f32, _i32, _vp, _i64,
                             _vp, _i32, _vp]),
+    "kea_relpos_attention": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _f32, _vp]),
+    "kea_glu_dwconv": (_i32, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
     "kea_last_error": (_cp, []),
     "kea_version": (_i32, []),
 }

@@ -18,10 +18,12 @@ kk/ternary/layer_fusions4.py:60-80):
 All 11 linears of a layer (W1, W2 of both FFs, W_q, W_k, W_v, W_out, W_pos, W_pw1, W_pw2; formats.PER_LAYER) are
 1-bit x int8 GEMMs through the provider seam (binary.provider.BinaryProjection over Int8MmaPartsLayer), with the
 LayerNorms in front of W1 / W_qkv / W_pw1 fused into the quantizer, SiLU after W1 fused into the GEMM epilogue and
-the SiLU in front of W_pw2 fused into the quantizer (the reference's norm_quant / silu transforms). Everything else
-(subsampling convolutions, attention core, GLU, depthwise convolution with BatchNorm folded into it, residual adds,
-the output LayerNorm) is PyTorch on the GPU. The quantized linears have no bias (Q/K/V must be bias-free to fuse,
-kk/binary/provider.py:230-244).
+the SiLU in front of W_pw2 fused into the quantizer (the reference's norm_quant / silu transforms). The attention core
+(relative-position scores, softmax, P.V) and GLU + depthwise convolution (BatchNorm folded into its weights) are the
+fused HIP kernels of include/kea_encoder.h (the reference's Triton relative_attention and glu_pad). The subsampling
+convolutions and the output LayerNorm are PyTorch on the GPU; the residual adds run in the epilogues of W2, W_out and
+W_pw2 (kea_lowbit_gemm_residual, the reference's row-epilogue residual). The quantized linears have no bias
+(Q/K/V must be bias-free to fuse, kk/binary/provider.py:230-244).
 
 `EncoderGraph` captures preprocessing + encoder for a fixed (batch, samples) into one HIP graph, as the reference
 captures its encoder (kk/ternary/graphs.py). `dense=True` builds the same model with the quantized linears replaced by
@@ -37,7 +39,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor
 
-from kea_kernels import formats
+from kea_kernels import _hip, formats, lowbit
 from kea_kernels.binary import bits, layer_parts, provider
 
 
@@ -196,6 +198,36 @@ def rel_shift(x: Tensor) -> Tensor:
     return x[..., :t]
 
 
+# --- fused HIP kernels (include/kea_encoder.h) ----------------------------------------------------------------------
+
+def relpos_attention(qkv: Tensor, pos: Tensor, bias_u: Tensor, bias_v: Tensor, heads: int) -> Tensor:
+    """qkv [B, T, 3d] (rows contiguous), pos [2T-1, d] (W_pos of the relative encodings), biases [H, dk] ->
+    attention output [B, T, d] (kea_relpos_attention)."""
+    b, t, three_d = qkv.shape
+    d = three_d // 3
+    out = torch.empty(b, t, d, device=qkv.device, dtype=torch.float32)
+    if qkv.stride(2) != 1 or pos.stride(1) != 1 or qkv.stride(0) != t * qkv.stride(1):
+        raise ValueError("qkv and pos need contiguous rows")
+    rc = _hip.lib().kea_relpos_attention(qkv.data_ptr(), qkv.stride(1), pos.data_ptr(), pos.stride(0),
+                                         bias_u.data_ptr(), bias_v.data_ptr(), out.data_ptr(), d, b, t, heads,
+                                         d // heads, 1.0 / math.sqrt(d // heads), _hip.stream_handle(qkv.device))
+    _hip.check(rc, "kea_relpos_attention")
+    return out
+
+
+def glu_dwconv(x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
+    """x [B, T, 2C] (rows contiguous) -> depthwise_conv(GLU(x)) [B, T, C] with weight [C, 1, KW] (kea_glu_dwconv)."""
+    b, t, two_c = x.shape
+    c, kw = two_c // 2, weight.shape[-1]
+    if x.stride(2) != 1 or x.stride(0) != t * x.stride(1) or not weight.is_contiguous():
+        raise ValueError("x needs contiguous rows and a contiguous weight")
+    y = torch.empty(b, t, c, device=x.device, dtype=torch.float32)
+    rc = _hip.lib().kea_glu_dwconv(x.data_ptr(), x.stride(1), weight.data_ptr(), _hip.ptr(bias), y.data_ptr(), c,
+                                   b, t, c, kw, _hip.stream_handle(x.device))
+    _hip.check(rc, "kea_glu_dwconv")
+    return y
+
+
 # --- the encoder -----------------------------------------------------------------------------------------------------
 
 class _DenseLinear:
@@ -225,11 +257,14 @@ class _Norm:
 
 class FastConformerEncoder:
     """audio [B, S] -> encoder output [B, T', d]. parts = int8 activation parts of every quantized linear (1 = the
-    Kea-B x1 mode); dense=True swaps the quantized linears for FP32 dense matmuls (the parity reference)."""
+    Kea-B x1 mode); dense=True swaps the quantized linears for FP32 dense matmuls (the parity reference);
+    fused=False runs attention and the GLU + depthwise convolution as PyTorch ops instead of the fused HIP kernels
+    (the dense twin always does)."""
 
     def __init__(self, weights: dict, cfg: EncoderConfig = EncoderConfig(), device="cuda", *, parts: int = 1,
-                 dense: bool = False):
+                 dense: bool = False, fused: bool = True):
         self.cfg, self.parts, self.dense = cfg, parts, dense
+        self.fused = fused and not dense
         self.device = device = torch.device(device)
         if device.type == "cuda" and device.index is None:
             self.device = device = torch.device("cuda", torch.cuda.current_device())
@@ -287,41 +322,61 @@ class FastConformerEncoder:
         mod = self._fused.get(name) or self.modules[name]
         return self.project(x, mod, False, self.parts, activation, norm, None, input_activation)
 
+    def _residual(self, name: str, z: Tensor, r: Tensor, factor: float, *, input_activation="") -> Tensor:
+        """r + factor * linear(z). Quantized: the residual add runs in the GEMM epilogue, in place into r
+        (kea_lowbit_gemm_residual; r is not used afterwards). Dense: PyTorch."""
+        if self.dense:
+            return torch.add(r, self._linear(name, z, input_activation=input_activation), alpha=factor)
+        layer = self.modules[name]._entry.layer
+        b, t, k = z.shape
+        m, n = b * t, layer.out_features
+        q, qs, _ = lowbit.quantize(z, (z.stride(0), z.stride(1), z.stride(2), t), m, k, self.parts,
+                                   input_activation=input_activation)
+        r2 = r.view(m, n)
+        lowbit.gemm(layer.WBITS, q, qs, layer.words, n, k, layer.scale, layer.bias, r2, None, residual=r2,
+                    residual_factor=factor)
+        return r
+
     def weight_bytes(self) -> int:
         return 0 if self.table is None else self.table.weight_bytes()
 
     def subsample(self, feats: Tensor) -> Tensor:
-        """[B, mels, frames] -> [B, T', d] (dw-striding x8, then the output linear)."""
+        """[B, mels, frames] -> [B, T', d] (dw-striding x8, then the output linear).
+
+        The convolutions run on PyTorch's own GPU kernels (the library-convolution path is switched off here): its
+        algorithm choice varied from box to box, by up to 10x on the first 3x3 convolution."""
         s = self.sub
         c = self.cfg.sub_channels
-        x = feats.transpose(1, 2).unsqueeze(1)                                        # [B, 1, frames, mels]
-        x = F.relu(F.conv2d(x, s["conv.0.weight"], s["conv.0.bias"], stride=2, padding=1))
-        for i in (2, 5):
-            x = F.conv2d(x, s[f"conv.{i}.weight"], s[f"conv.{i}.bias"], stride=2, padding=1, groups=c)
-            x = F.relu(F.conv2d(x, s[f"conv.{i + 1}.weight"], s[f"conv.{i + 1}.bias"]))
+        with torch.backends.cudnn.flags(enabled=False):
+            x = feats.transpose(1, 2).unsqueeze(1)                                    # [B, 1, frames, mels]
+            x = F.relu(F.conv2d(x, s["conv.0.weight"], s["conv.0.bias"], stride=2, padding=1))
+            for i in (2, 5):
+                x = F.conv2d(x, s[f"conv.{i}.weight"], s[f"conv.{i}.bias"], stride=2, padding=1, groups=c)
+                x = F.relu(F.conv2d(x, s[f"conv.{i + 1}.weight"], s[f"conv.{i + 1}.bias"]))
         b, _, t, f = x.shape
         x = x.transpose(1, 2).reshape(b, t, c * f)
         return F.linear(x, s["out.weight"], s["out.bias"])
 
     def positions(self, t: int) -> list:
-        """W_pos applied to the relative encodings, per layer, for length t: [H, 2t-1, dk] each. Frozen per length
+        """W_pos applied to the relative encodings, per layer, for length t: [2t-1, d] each. Frozen per length
         (the reference freezes them for graph capture too, kk/ternary/transforms.py:18-21); computed with the same
         quantized GEMM as every other call."""
         hit = self._pos_cache.get(t)
         if hit is None:
             cfg = self.cfg
             pe = relative_positions(cfg, t, self.device).unsqueeze(0)
-            hit = []
-            for layer in range(cfg.layers):
-                p = self._linear(f"encoder.layers.{layer}.self_attn.linear_pos", pe)[0]
-                hit.append(p.view(2 * t - 1, cfg.heads, -1).permute(1, 2, 0).contiguous())  # [H, dk, 2t-1]
+            hit = [self._linear(f"encoder.layers.{layer}.self_attn.linear_pos", pe)[0].contiguous()
+                   for layer in range(cfg.layers)]
             self._pos_cache[t] = hit
         return hit
 
-    def attention(self, qkv: Tensor, pos_t: Tensor, u: Tensor, v_bias: Tensor) -> Tensor:
+    def attention(self, qkv: Tensor, pos: Tensor, u: Tensor, v_bias: Tensor) -> Tensor:
         b, t, _ = qkv.shape
         h = self.cfg.heads
         dk = self.cfg.d_model // h
+        if self.fused and t <= 256 and dk == 128:
+            return relpos_attention(qkv, pos, u, v_bias, h)
+        pos_t = pos.view(2 * t - 1, h, dk).permute(1, 2, 0).contiguous()  # [H, dk, 2t-1]
         q, k, v = qkv.view(b, t, 3, h, dk).unbind(2)
         qu = (q + u).transpose(1, 2).contiguous()                                   # [B, H, T, dk]
         qv = (q + v_bias).transpose(1, 2).contiguous()
@@ -332,20 +387,23 @@ class FastConformerEncoder:
         out = torch.matmul(attn, v.transpose(1, 2).contiguous())                    # [B, H, T, dk]
         return out.transpose(1, 2).reshape(b, t, h * dk)
 
-    def layer(self, i: int, x: Tensor, pos_t: Tensor) -> Tensor:
+    def layer(self, i: int, x: Tensor, pos: Tensor) -> Tensor:
         fp = self.layers[i]
         pre = f"encoder.layers.{i}."
         y = self._linear(pre + "feed_forward1.linear1", x, norm=fp["norm_feed_forward1"], activation="silu")
-        r = torch.add(x, self._linear(pre + "feed_forward1.linear2", y), alpha=0.5)
+        r = self._residual(pre + "feed_forward1.linear2", y, x, 0.5)
         qkv = self._linear(pre + "self_attn.qkv", r, norm=fp["norm_self_att"])
-        r = r + self._linear(pre + "self_attn.linear_out", self.attention(qkv, pos_t, fp["u"], fp["v"]))
+        r = self._residual(pre + "self_attn.linear_out", self.attention(qkv, pos, fp["u"], fp["v"]), r, 1.0)
         z = self._linear(pre + "conv.pointwise_conv1", r, norm=fp["norm_conv"])
-        z = F.glu(z, dim=-1)                                                        # a * sigmoid(g)
-        z = F.conv1d(z.transpose(1, 2), fp["dw_w"], fp["dw_b"], padding=self.cfg.conv_kernel // 2,
-                     groups=self.cfg.d_model).transpose(1, 2)
-        r = r + self._linear(pre + "conv.pointwise_conv2", z, input_activation="silu")
+        if self.fused:
+            z = glu_dwconv(z, fp["dw_w"], fp["dw_b"])
+        else:
+            z = F.glu(z, dim=-1)                                                    # a * sigmoid(g)
+            z = F.conv1d(z.transpose(1, 2), fp["dw_w"], fp["dw_b"], padding=self.cfg.conv_kernel // 2,
+                         groups=self.cfg.d_model).transpose(1, 2)
+        r = self._residual(pre + "conv.pointwise_conv2", z, r, 1.0, input_activation="silu")
         y = self._linear(pre + "feed_forward2.linear1", r, norm=fp["norm_feed_forward2"], activation="silu")
-        r = torch.add(r, self._linear(pre + "feed_forward2.linear2", y), alpha=0.5)
+        r = self._residual(pre + "feed_forward2.linear2", y, r, 0.5)
         n = fp["norm_out"]
         return F.layer_norm(r, n.normalized_shape, n.weight, n.bias, n.eps)
 
@@ -384,12 +442,19 @@ class EncoderGraph:
         torch.cuda.synchronize(dev)
 
     def replay(self) -> Tensor:
+        """Replays on the graph's stream, ordered after the caller's current stream and before its later work."""
+        caller = torch.cuda.current_stream(self.audio.device)
+        self.stream.wait_stream(caller)
         with torch.cuda.stream(self.stream):
             self.graph.replay()
+        caller.wait_stream(self.stream)
         return self.out
 
     def __call__(self, audio: Tensor) -> Tensor:
+        caller = torch.cuda.current_stream(self.audio.device)
+        self.stream.wait_stream(caller)
         with torch.cuda.stream(self.stream):
             self.audio.copy_(audio)
             self.graph.replay()
+        caller.wait_stream(self.stream)
         return self.out

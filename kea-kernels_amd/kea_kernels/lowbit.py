@@ -23,9 +23,11 @@ def _on(device: torch.device, *tensors: Tensor | None) -> None:
 
 def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscale: Tensor, bias: Tensor | None,
          y: Tensor | None = None, acc_out: Tensor | None = None, *, m: int | None = None, silu: bool = False,
-         order: int = 0, config=None, ws_group: int = 0) -> None:
+         order: int = 0, config=None, ws_group: int = 0, residual: Tensor | None = None,
+         residual_factor: float = 1.0) -> None:
     """y[:m] (rows of stride y.stride(0)) and/or acc_out [P, m, N] from q int8 [P, M, ldq] (16-byte aligned rows) and
-    qs [P, M] (f32 or f16). words: native layout of `wbits`-bit weights; wscale [N] (or [N, G] with ws_group)."""
+    qs [P, M] (f32 or f16). words: native layout of `wbits`-bit weights; wscale [N] (or [N, G] with ws_group).
+    residual (FP32 [>= m, >= N] rows, may be y itself): y = residual + value * residual_factor."""
     if q.dtype != torch.int8 or q.dim() != 3:
         raise ValueError(f"q must be int8 [P, M, ldq], got {q.dtype} {tuple(q.shape)}")
     parts, rows, ldq = q.shape
@@ -48,10 +50,13 @@ def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscal
                                 or acc_out.shape[1] != m or acc_out.shape[2] < n or acc_out.stride(2) != 1
                                 or acc_out.stride(0) != m * acc_out.stride(1)):
         raise ValueError(f"acc_out must be int32 [{parts}, {m}, >= {n}] with dense part planes")
+    if residual is not None and (y is None or residual.dtype != torch.float32 or residual.dim() != 2
+                                 or residual.shape[0] < m or residual.shape[1] < n or residual.stride(1) != 1):
+        raise ValueError(f"residual must be a row-major FP32 [>= {m}, >= {n}] view and needs y")
     if torch.is_grad_enabled() and (q.requires_grad or qs.requires_grad):
         raise RuntimeError("the low-bit GEMM is inference only: an input requires grad")
     device = q.device
-    _on(device, qs, words, wscale, bias, y, acc_out)
+    _on(device, qs, words, wscale, bias, y, acc_out, residual)
     L = _hip.lib()
     if config is not None and not hasattr(config, "tile"):
         config = None  # a reference tile tuple (its RTX 5090 tiling): accepted, results never depend on tiles
@@ -61,17 +66,20 @@ def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscal
     if need < 0:
         _hip.check(-1, "kea_lowbit_gemm_workspace")
     workspace = torch.empty(need, dtype=torch.uint8, device=device) if need else None
-    rc = L.kea_lowbit_gemm(
-        wbits, q.data_ptr(), q.stride(0), ldq, parts,
-        qs.data_ptr(), _hip.dtype_code(qs.dtype), qs.stride(0),
-        words.data_ptr(), n, k,
-        wscale.data_ptr(), _hip.dtype_code(wscale.dtype), ws_group,
-        _hip.ptr(bias), _hip.dtype_code(bias.dtype) if bias is not None else 0,
-        _hip.ptr(y), _hip.dtype_code(y.dtype) if y is not None else 0, y.stride(0) if y is not None else 0,
-        _hip.ptr(acc_out), acc_out.stride(1) if acc_out is not None else 0,
-        m, int(silu) | (2 * int(order)), split, tile,
-        _hip.ptr(workspace), need, _hip.stream_handle(device))
-    _hip.check(rc, "kea_lowbit_gemm")
+    args = (wbits, q.data_ptr(), q.stride(0), ldq, parts,
+            qs.data_ptr(), _hip.dtype_code(qs.dtype), qs.stride(0),
+            words.data_ptr(), n, k,
+            wscale.data_ptr(), _hip.dtype_code(wscale.dtype), ws_group,
+            _hip.ptr(bias), _hip.dtype_code(bias.dtype) if bias is not None else 0,
+            _hip.ptr(y), _hip.dtype_code(y.dtype) if y is not None else 0, y.stride(0) if y is not None else 0,
+            _hip.ptr(acc_out), acc_out.stride(1) if acc_out is not None else 0,
+            m, int(silu) | (2 * int(order)), split, tile,
+            _hip.ptr(workspace), need)
+    if residual is None:
+        _hip.check(L.kea_lowbit_gemm(*args, _hip.stream_handle(device)), "kea_lowbit_gemm")
+    else:
+        _hip.check(L.kea_lowbit_gemm_residual(*args, residual.data_ptr(), residual.stride(0), float(residual_factor),
+                                              _hip.stream_handle(device)), "kea_lowbit_gemm_residual")
 
 
 def gemm_slices(wbits: int, q: Tensor, words: Tensor, n: int, k: int, slices: Tensor, *, m: int | None = None,

@@ -98,3 +98,50 @@ def test_encoder_graph_replays_equal_eager():
         torch.cuda.synchronize()
         torch.testing.assert_close(got, eager, rtol=0, atol=0)
         _ = enc(audio)  # eager work between replays
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,t", [(1, 125), (2, 37), (1, 256), (3, 1)])
+@torch.inference_mode()
+def test_fused_relpos_attention_matches_fp64(b, t):
+    """The fused kernel against the same formula in FP64 (rel_shift form); FP32 accumulation over 128-dim dot
+    products and T-term sums bounds the error near 1e-6 relative."""
+    h, dk = 8, 128
+    g = torch.Generator().manual_seed(b * 1000 + t)
+    qkv = torch.randn(b, t, 3 * h * dk, generator=g)
+    pos = torch.randn(2 * t - 1, h * dk, generator=g)
+    u, v = torch.randn(h, dk, generator=g) * 0.1, torch.randn(h, dk, generator=g) * 0.1
+    got = E.relpos_attention(qkv.cuda(), pos.cuda(), u.cuda(), v.cuda(), h).cpu().double()
+    q, k, vv = qkv.double().view(b, t, 3, h, dk).unbind(2)
+    qu = (q + u.double()).transpose(1, 2)
+    qv = (q + v.double()).transpose(1, 2)
+    ac = qu @ k.permute(0, 2, 3, 1)
+    bd = E.rel_shift(qv @ pos.double().view(2 * t - 1, h, dk).permute(1, 2, 0))
+    a = torch.softmax((ac + bd) / math.sqrt(dk), dim=-1)
+    ref = (a @ vv.transpose(1, 2)).transpose(1, 2).reshape(b, t, h * dk)
+    assert float((got - ref).abs().max() / ref.abs().max()) < 2e-6
+
+
+@pytest.mark.gpu
+@torch.inference_mode()
+def test_fused_glu_dwconv_matches_torch():
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(2, 50, 2 * 96, generator=g)
+    w = torch.randn(96, 1, 9, generator=g) / 3
+    bias = torch.randn(96, generator=g)
+    got = E.glu_dwconv(x.cuda(), w.cuda(), bias.cuda()).cpu().double()
+    ref = F.conv1d(F.glu(x.double(), dim=-1).transpose(1, 2), w.double(), bias.double(), padding=4,
+                   groups=96).transpose(1, 2)
+    assert float((got - ref).abs().max()) < 1e-5
+
+
+@pytest.mark.gpu
+@torch.inference_mode()
+def test_fused_encoder_matches_unfused():
+    cfg = E.EncoderConfig(layers=3)
+    w = E.synthetic_weights(cfg, seed=21)
+    audio = torch.randn(2, 64000, generator=torch.Generator().manual_seed(22)).cuda()
+    fused = E.FastConformerEncoder(w, cfg, "cuda", parts=3)(audio)
+    plain = E.FastConformerEncoder(w, cfg, "cuda", parts=3, fused=False)(audio)
+    rel = float((fused.double() - plain.double()).norm() / plain.double().norm())
+    assert rel < 5e-6, rel

@@ -366,3 +366,41 @@ def test_group_scales_reject_unsupported_arguments():
         _group_run(case, 64, alpha_g, out_dtype=torch.float32, config=kernels.GemmConfig(tile=2, split=1))
     with pytest.raises(ValueError, match="unsplit"):
         _group_run(case, 64, alpha_g, out_dtype=torch.float32, config=kernels.GemmConfig(tile=4, split=2))
+
+
+# --- residual epilogue ------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("wbits,p,m,n,k,split", [(1, 1, 125, 1024, 4096, 1), (1, 3, 38, 1024, 4096, 4),
+                                                 (2, 2, 300, 512, 640, 1), (1, 1, 1000, 1024, 1024, 1)])
+@pytest.mark.parametrize("in_place", [False, True])
+@torch.inference_mode()
+def test_residual_epilogue_bitwise(wbits, p, m, n, k, split, in_place):
+    """y = residual + value * factor (IEEE multiply, then add) on the unsplit and the split-K (finish) paths."""
+    case = Case(wbits, p, m, n, k, seed=m + n + p, bias=True, scale_dtype=torch.float32)
+    g = torch.Generator().manual_seed(m * 3 + split)
+    res = torch.randn(m, n, generator=g)
+    factor = 0.5
+    dres = res.to(DEV)
+    y = dres if in_place else torch.empty(m, n, device=DEV)
+    lowbit.gemm(case.wbits, case.dq, case.dqs, case.words, n, k, case.dalpha, case.dbias, y, None,
+                config=kernels.GemmConfig(tile=1 if p > 1 else 4, split=split), residual=dres, residual_factor=factor)
+    torch.cuda.synchronize()
+    value = case.oracle_y(case.oracle_acc())
+    want = (res.numpy() + value * np.float32(factor)).astype(np.float32)
+    got = y.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@torch.inference_mode()
+def test_residual_epilogue_with_group_scales():
+    case = Case(2, 1, 70, 300, 1000, seed=5, bias=True, scale_dtype=torch.float32)
+    g = torch.Generator().manual_seed(6)
+    alpha_g = (torch.rand(case.n, 8, generator=g) * 0.09 + 0.01)
+    res = torch.randn(case.m, case.n, generator=g)
+    y = torch.empty(case.m, case.n, device=DEV)
+    lowbit.gemm(2, case.dq, case.dqs, case.words, case.n, case.k, alpha_g.to(DEV), case.dbias, y, None,
+                ws_group=128, residual=res.to(DEV), residual_factor=0.25)
+    torch.cuda.synchronize()
+    ref_y, _ = _group_ref(case, 128, alpha_g)
+    want = (res.numpy() + ref_y * np.float32(0.25)).astype(np.float32)
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
