@@ -179,6 +179,139 @@ relpos_attention_kernel(const float *qkv, long long ld, const float *pos, long l
     }
 }
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Matrix-core form of the same attention for T <= 128 (one workgroup = 16 query rows of one (b, h), 4 waves), on
+// v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16] per step and ends with
+// D[4 (l / 16) + r][l % 16]. The head dimension is walked in the order d = 32 g + s (g = l / 16 the k lane group,
+// s = 0..31 the step), so a lane's operand values are 32 contiguous floats (8 float4 loads straight from global
+// memory); any order of the 128 terms is the same dot product up to FP32 rounding.
+//   content scores   D = (q + u) K^T                      16 x 16 key tiles, waves over key tiles
+//   position scores  D = (q + v) P_band^T                  the band of 16 + KP - 1 relative rows this block needs,
+//                                                          taken back as bd[i][j] = band[i][j + 15 - i]
+//   softmax          per row in LDS (exact two-pass, keys past T masked)
+//   output           D = probs V over keys k = (KP/4) g + s, V transposed into LDS so operands are contiguous
+template <int NKT>
+__global__ void __launch_bounds__(256)
+relpos_attention_mfma_kernel(const float *qkv, long long ld, const float *pos, long long ldp, const float *bias_u,
+                             const float *bias_v, float *out, long long ldo, int T, int H, float scale) {
+    constexpr int DK = 128, KP = 16 * NKT, NPT = NKT + 1, KS = KP / 4;
+    constexpr int SP = KP + 4, BP = 16 * NPT + 4, VP = KP + 4;  // padded LDS row strides (floats)
+    extern __shared__ __attribute__((aligned(16))) float sm[];
+    float *Sc = sm, *Bd = Sc + 16 * SP, *Vt = Bd + 16 * BP;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, g = lane >> 4;
+    const int b = blockIdx.z, h = blockIdx.y, i0 = blockIdx.x * 16;
+    const float *qbase = qkv + (long long)b * T * ld + (long long)h * DK;
+    const float *kbase = qbase + (long long)H * DK, *vbase = qbase + 2LL * H * DK;
+
+    // V transposed into LDS: Vt[d][j] = V[j][d] (zero for j >= T); consecutive threads take consecutive keys
+    for (int idx = tid; idx < KP * (DK / 4); idx += 256) {
+        const int j = idx % KP, d = (idx / KP) * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (j < T) v = *(const float4 *)(vbase + (long long)j * ld + d);
+        Vt[(d + 0) * VP + j] = v.x;
+        Vt[(d + 1) * VP + j] = v.y;
+        Vt[(d + 2) * VP + j] = v.z;
+        Vt[(d + 3) * VP + j] = v.w;
+    }
+
+    // query operands with both position biases: row i0 + li, columns 32 g .. 32 g + 31
+    float qa[32], qb[32];
+    {
+        const int t = i0 + li;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (t < T) q = *(const float4 *)(qbase + (long long)t * ld + 32 * g + 4 * c);
+            const float4 u = *(const float4 *)(bias_u + h * DK + 32 * g + 4 * c);
+            const float4 v = *(const float4 *)(bias_v + h * DK + 32 * g + 4 * c);
+            qa[4 * c] = q.x + u.x; qa[4 * c + 1] = q.y + u.y; qa[4 * c + 2] = q.z + u.z; qa[4 * c + 3] = q.w + u.w;
+            qb[4 * c] = q.x + v.x; qb[4 * c + 1] = q.y + v.y; qb[4 * c + 2] = q.z + v.z; qb[4 * c + 3] = q.w + v.w;
+        }
+    }
+    // one 16 x 16 tile of dot products: rows = the 16 queries, columns = 16 rows of `src` (zero where invalid)
+    auto tile = [&](const float *q, const float *src, long long stride, int row, bool valid) {
+        float kb[32];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (valid) v = *(const float4 *)(src + (long long)row * stride + 32 * g + 4 * c);
+            kb[4 * c] = v.x; kb[4 * c + 1] = v.y; kb[4 * c + 2] = v.z; kb[4 * c + 3] = v.w;
+        }
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 32; ++st) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(q[st], kb[st], acc, 0, 0, 0);
+        return acc;
+    };
+    for (int kt = wave; kt < NKT; kt += 4) {
+        const int j = kt * 16 + li;
+        const v4f acc = tile(qa, kbase, ld, j, j < T);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Sc[(4 * g + r) * SP + kt * 16 + li] = acc[r];
+    }
+    const int rbase = T - 1 - (i0 + 15);  // relative row of band position 0
+    for (int pt = wave; pt < NPT; pt += 4) {
+        const int r = rbase + pt * 16 + li;
+        const v4f acc = tile(qb, pos + (long long)h * DK, ldp, r, r >= 0 && r <= 2 * T - 2);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) Bd[(4 * g + rr) * BP + pt * 16 + li] = acc[rr];
+    }
+    __syncthreads();
+
+    // softmax: wave w owns rows 4w .. 4w + 3; lane takes keys lane, lane + 64
+    for (int i = 4 * wave; i < 4 * wave + 4; ++i) {
+        float sv[2];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            const int j = lane + 64 * n;
+            sv[n] = -INFINITY;
+            if (j < KP && j < T) sv[n] = (Sc[i * SP + j] + Bd[i * BP + j + 15 - i]) * scale;
+            mx = fmaxf(mx, sv[n]);
+        }
+        mx = wave_max(mx);
+        float sum = 0.f;
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            sv[n] = expf(sv[n] - mx);
+            sum = sum + sv[n];
+        }
+        const float inv = 1.0f / wave_sum(sum);
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            const int j = lane + 64 * n;
+            if (j < KP) Sc[i * SP + j] = sv[n] * inv;
+        }
+    }
+    __syncthreads();
+
+    // output: wave w computes head columns 32 w .. 32 w + 31 (two 16-column tiles)
+    float pa[KS];
+#pragma unroll
+    for (int c = 0; c < KS; c += 4) {
+        const float4 v = *(const float4 *)(Sc + li * SP + KS * g + c);
+        pa[c] = v.x; pa[c + 1] = v.y; pa[c + 2] = v.z; pa[c + 3] = v.w;
+    }
+#pragma unroll
+    for (int dt = 2 * wave; dt < 2 * wave + 2; ++dt) {
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+        const float *vrow = Vt + (dt * 16 + li) * VP + KS * g;
+#pragma unroll
+        for (int c = 0; c < KS; c += 4) {
+            const float4 v = *(const float4 *)(vrow + c);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[c], v.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[c + 1], v.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[c + 2], v.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[c + 3], v.w, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = i0 + 4 * g + r;
+            if (t < T) out[((long long)b * T + t) * ldo + (long long)h * DK + dt * 16 + li] = acc[r];
+        }
+    }
+}
+
 // y[b][t][c] = bias[c] + sum_j w[c][j] * glu(x)[b][t + j - KW/2][c],  glu(x)[.][c] = x[.][c] * sigmoid(x[.][C + c]),
 // zero outside [0, T). One thread per output element, threads along c (coalesced).
 __global__ void __launch_bounds__(256)
@@ -215,6 +348,32 @@ int kea_relpos_attention(const float *qkv, int64_t ld, const float *pos, int64_t
     if (((uintptr_t)qkv | (uintptr_t)pos | (uintptr_t)out | (uintptr_t)bias_u | (uintptr_t)bias_v) & 15 ||
         (ld | ldp | ldo) & 3)
         return kea::fail(KEA_EALIGN, "qkv, pos, out and the biases need 16-byte aligned rows");
+    if (t <= 128) {
+        const int nkt = (int)((t + 15) / 16), kp = 16 * nkt;
+        const size_t lds = sizeof(float) * (size_t)(16 * (kp + 4) + 16 * (16 * (nkt + 1) + 4) + head_dim * (kp + 4));
+        const dim3 grid((unsigned)((t + 15) / 16), (unsigned)heads, (unsigned)batch);
+        void (*fn)(const float *, long long, const float *, long long, const float *, const float *, float *,
+                   long long, int, int, float) = nullptr;
+        switch (nkt) {
+            case 1: fn = relpos_attention_mfma_kernel<1>; break;
+            case 2: fn = relpos_attention_mfma_kernel<2>; break;
+            case 3: fn = relpos_attention_mfma_kernel<3>; break;
+            case 4: fn = relpos_attention_mfma_kernel<4>; break;
+            case 5: fn = relpos_attention_mfma_kernel<5>; break;
+            case 6: fn = relpos_attention_mfma_kernel<6>; break;
+            case 7: fn = relpos_attention_mfma_kernel<7>; break;
+            default: fn = relpos_attention_mfma_kernel<8>; break;
+        }
+        if (lds > 65536) {
+            hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return kea::fail((int)e, std::string("LDS attribute refused: ") + hipGetErrorString(e));
+        }
+        hipLaunchKernelGGL(fn, grid, dim3(256), lds, (hipStream_t)stream, qkv, (long long)ld, pos, (long long)ldp,
+                           bias_u, bias_v, out, (long long)ldo, (int)t, heads, scale);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return kea::fail((int)e, std::string("attention launch failed: ") + hipGetErrorString(e));
+        return KEA_OK;
+    }
     const int nk = (int)((t + 63) / 64), kp = 64 * nk;
     const size_t lds = sizeof(float) * (size_t)(2 * kQB * head_dim + kQB * kp + (kQB - 1 + kp) * (head_dim + 4));
     const dim3 grid((unsigned)((t + kQB - 1) / kQB), (unsigned)heads, (unsigned)batch);
