@@ -37,6 +37,24 @@ int kea_relpos_attention(const float *qkv_dev, int64_t ld, const float *pos_dev,
 int kea_glu_dwconv(const float *x_dev, int64_t ldx, const float *w_dev, const float *bias_dev, float *y_dev,
                    int64_t ldy, int64_t batch, int64_t t, int64_t channels, int kernel, void *stream);
 
+/* x_out = LayerNorm0(x) (stored, FP32), then the P-part residual int8 quantization of LayerNorm1(x_out) exactly as
+ * kea_quantize (f32 scales): one encoder layer's output LayerNorm fused with the normalised quantizer of the next
+ * layer's first projection. Rows contiguous: x [m][ldx], x_out [m][ldo], 4 <= k <= 4096, k % 4 == 0; q [parts][m][ldq]
+ * (zero padded), qs f32 [parts][m]. Replaces the reference's row epilogue LayerNorm + INT8x3 quantization
+ * (kk/ternary/row_fusion.py:28-53, kk/binary/row_exact.py:98-156). */
+int kea_norm_quantize(const float *x_dev, int64_t ldx, int64_t m, int64_t k, const float *norm0_w_dev,
+                      const float *norm0_b_dev, float eps0, float *x_out_dev, int64_t ldo, const float *norm1_w_dev,
+                      const float *norm1_b_dev, float eps1, int parts, int8_t *q_dev, int64_t ldq, float *qs_dev,
+                      void *stream);
+
+/* GLU + depthwise convolution as kea_glu_dwconv, then SiLU, then the P-part quantization of each token row (as
+ * kea_quantize, f32 scales): the middle of the convolution module fused with the quantizer of its second pointwise
+ * convolution (the reference's glu_pad + depthwise conv + BatchNorm + input SiLU of pointwise_conv2,
+ * kk/ternary/layer_fusions4.py:62-72). channels % 4 == 0, channels <= 2048; q [parts][batch * t][ldq]. */
+int kea_glu_dwconv_quantize(const float *x_dev, int64_t ldx, const float *w_dev, const float *bias_dev,
+                            int64_t batch, int64_t t, int64_t channels, int kernel, int parts, int8_t *q_dev,
+                            int64_t ldq, float *qs_dev, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

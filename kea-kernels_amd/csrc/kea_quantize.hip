@@ -8,7 +8,7 @@
 // reproduced). With fp16 scales the scale is rounded to fp16 (kept >= the smallest fp16 subnormal, <= the largest
 // finite fp16) before use and q is clamped to [-127, 127].
 //
-// Layout: a row is handled by WPR wave64s (1 for K <= 1024, 4 above), thread th of the row holding the 4-element
+// Layout: a row is handled by WPR wave64s (1 for K <= 256, 4 above), thread th of the row holding the 4-element
 // chunks k = 4 * (th + 64 * WPR * i) + j: consecutive threads read consecutive 16-byte chunks (one float4 load each
 // when the row is contiguous and aligned) and store the 4 quantized bytes as one dword. The LayerNorm sums, the only
 // reductions that are not exact, use one fixed order that the CPU oracle restates: each thread sums its elements in
@@ -20,6 +20,7 @@
 #include <string>
 
 #include "kea_internal.h"
+#include "../../include/kea_encoder.h"
 
 namespace {
 
@@ -179,6 +180,171 @@ quantize_kernel(const void *x, int x_dtype, long long xb, long long xt, long lon
     }
 }
 
+// Quantizes the row a thread group holds in registers (thread th of TPR = 64 * WPR holds the 4-element chunks
+// k = 4 * (th + TPR * i) + j; zero past K) into P residual parts, exactly as quantize_kernel (f32 scales, ldq % 4 == 0).
+template <int VPT, int WPR>
+__device__ __forceinline__ void quantize_parts(float (*z)[4], int K, int parts, int8_t *q, long long ldq, float *qs,
+                                               int M, int m, int th, float (*red)[WPR], int wave) {
+    constexpr int TPR = 64 * WPR;
+    for (int c = 0; c < parts; ++c) {
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(z[i][j]));
+        amax = row_reduce<WPR, true>(amax, red, 2 + c, wave);
+        const float s = fmaxf(amax / 127.0f, 1.0e-30f);
+        if (th == 0) qs[(long long)c * M + m] = s;
+        int8_t *row = q + ((long long)c * M + m) * ldq;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int k0 = 4 * (th + TPR * i);
+            uint32_t packed = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float v = rintf(z[i][j] / s);
+                v = fminf(fmaxf(v, -127.0f), 127.0f);
+                packed |= (uint32_t)(uint8_t)(int8_t)(int)v << (8 * j);
+                z[i][j] = z[i][j] - v * s;
+            }
+            if (k0 < K) *(uint32_t *)(row + k0) = packed;
+        }
+        for (long long k = ((K + 3) & ~3) + th; k < ldq; k += TPR) row[k] = 0;
+    }
+}
+
+// LayerNorm of the row in registers with the library's fixed summation order (see the file comment).
+template <int VPT, int WPR>
+__device__ __forceinline__ void layer_norm_row(float (*z)[4], int K, const float *w, const float *b, float eps,
+                                               int th, float (*red)[WPR], int wave, int slot) {
+    constexpr int TPR = 64 * WPR;
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sum = sum + z[i][j];
+    const float mean = row_reduce<WPR, false>(sum, red, slot, wave) / (float)K;
+    float sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = 4 * (th + TPR * i) + j;
+            z[i][j] = k < K ? z[i][j] - mean : 0.f;
+            sq = sq + z[i][j] * z[i][j];
+        }
+    const float var = row_reduce<WPR, false>(sq, red, slot + 1, wave) / (float)K;
+    const float inv = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int k0 = 4 * (th + TPR * i);
+        if (k0 < K) {
+            const float4 lw = *(const float4 *)(w + k0), lb = *(const float4 *)(b + k0);
+            z[i][0] = z[i][0] * inv * lw.x + lb.x; z[i][1] = z[i][1] * inv * lw.y + lb.y;
+            z[i][2] = z[i][2] * inv * lw.z + lb.z; z[i][3] = z[i][3] * inv * lw.w + lb.w;
+        }
+    }
+}
+
+// x_out = LayerNorm0(x) (stored), then the P-part quantization of LayerNorm1(x_out): the output LayerNorm of one
+// encoder layer fused with the normalised quantization that feeds the next layer's first projection (the reference's
+// row epilogue, kk/ternary/row_fusion.py:28-53). WPR waves per row with the quantizer's rule and summation order,
+// rows contiguous, K % 4 == 0.
+template <int VPT, int WPR>
+__global__ void __launch_bounds__(256)
+norm_quantize_kernel(const float *x, long long ldx, int M, int K, const float *w0, const float *b0, float eps0,
+                     float *x_out, long long ldo, const float *w1, const float *b1, float eps1, int parts, int8_t *q,
+                     long long ldq, float *qs) {
+    constexpr int RPB = 4 / WPR, TPR = 64 * WPR;
+    __shared__ float red[RPB][7][WPR];
+    const int th = threadIdx.x % TPR, rl = threadIdx.x / TPR, wave = th >> 6, m = blockIdx.x * RPB + rl;
+    if (m >= M) return;  // whole rows leave together: the row's barriers stay matched
+    float z[VPT][4];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int k0 = 4 * (th + TPR * i);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (k0 < K) v = *(const float4 *)(x + (long long)m * ldx + k0);
+        z[i][0] = v.x; z[i][1] = v.y; z[i][2] = v.z; z[i][3] = v.w;
+    }
+    layer_norm_row<VPT, WPR>(z, K, w0, b0, eps0, th, red[rl], wave, 5);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int k0 = 4 * (th + TPR * i);
+        if (k0 < K) *(float4 *)(x_out + (long long)m * ldo + k0) = make_float4(z[i][0], z[i][1], z[i][2], z[i][3]);
+    }
+    layer_norm_row<VPT, WPR>(z, K, w1, b1, eps1, th, red[rl], wave, 0);
+    quantize_parts<VPT, WPR>(z, K, parts, q, ldq, qs, M, m, th, red[rl], wave);
+}
+
+// GLU + depthwise convolution (as glu_dwconv_kernel, same operation order), SiLU, then the P-part quantization of the
+// row: the middle of the convolution module fused with the quantizer of the second pointwise convolution. One
+// workgroup (4 waves) per token row; thread th holds the channel chunks 4 * (th + 256 i) .. + 3 (C % 4 == 0).
+// KW > 0: compile-time kernel width; every tap's loads are issued before the arithmetic (rows clamped into [0, T) so
+// each address is in bounds; taps outside the sequence are then skipped, exactly as in the runtime-width loop).
+template <int VPT, int KW>
+__global__ void __launch_bounds__(256)
+glu_dwconv_quantize_kernel(const float *x, long long ldx, const float *w, const float *bias, int T, int C, int kw_rt,
+                           int parts, int8_t *q, long long ldq, float *qs) {
+    __shared__ float red[1][7][4];
+    const int th = threadIdx.x, wave = th >> 6, t = blockIdx.x, b = blockIdx.y, m = b * T + t;
+    const int M = gridDim.y * T;
+    const float *xb = x + (long long)b * T * ldx;
+    float z[VPT][4];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int c0 = 4 * (th + 256 * i);
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        if (c0 < C) {
+            if (bias) {
+                const float4 bv = *(const float4 *)(bias + c0);
+                acc[0] = bv.x; acc[1] = bv.y; acc[2] = bv.z; acc[3] = bv.w;
+            }
+            if constexpr (KW > 0) {
+                constexpr int half = KW / 2;
+                float4 a[KW], g[KW];
+#pragma unroll
+                for (int j = 0; j < KW; ++j) {
+                    const int tt = min(max(t + j - half, 0), T - 1);
+                    a[j] = *(const float4 *)(xb + (long long)tt * ldx + c0);
+                    g[j] = *(const float4 *)(xb + (long long)tt * ldx + C + c0);
+                }
+                float4 wv[KW];   // w[(c0 + e) * KW + j]: the 4 channels' taps are 4 * KW consecutive floats
+                const float *wc = w + (long long)c0 * KW;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int j = 0; j < KW; ++j) (&wv[j].x)[e] = wc[e * KW + j];
+#pragma unroll
+                for (int j = 0; j < KW; ++j) {
+                    if (t + j - half < 0 || t + j - half >= T) continue;
+                    const float av[4] = {a[j].x, a[j].y, a[j].z, a[j].w}, gv[4] = {g[j].x, g[j].y, g[j].z, g[j].w};
+                    const float ww[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc[e] = __builtin_fmaf(ww[e], av[e] * (1.0f / (1.0f + expf(-gv[e]))), acc[e]);
+                }
+            } else {
+                const int half = kw_rt / 2;
+                for (int j = 0; j < kw_rt; ++j) {
+                    const int tt = t + j - half;
+                    if (tt < 0 || tt >= T) continue;
+                    const float *row = xb + (long long)tt * ldx;
+                    const float4 a = *(const float4 *)(row + c0), g = *(const float4 *)(row + C + c0);
+                    const float av[4] = {a.x, a.y, a.z, a.w}, gv[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc[e] = __builtin_fmaf(w[(c0 + e) * kw_rt + j], av[e] * (1.0f / (1.0f + expf(-gv[e]))),
+                                                acc[e]);
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) z[i][e] = acc[e] * (1.0f / (1.0f + expf(-acc[e])));  // SiLU (0 past C)
+    }
+    quantize_parts<VPT, 4>(z, C, parts, q, ldq, qs, M, m, th, red[0], wave);
+}
+
 }  // namespace
 
 extern "C" int kea_quantize(const void *x, int x_dtype, int64_t xb, int64_t xt, int64_t xk, int64_t t, int64_t m,
@@ -195,7 +361,7 @@ extern "C" int kea_quantize(const void *x, int x_dtype, int64_t xb, int64_t xt, 
     if (!x || !q || !qs) return kea::fail(KEA_EINVAL, "x, q and qs are required");
     hipStream_t st = (hipStream_t)stream;
     const int esz = x_dtype == KEA_F16 ? 2 : 4;
-    const int wpr = k > 1024 ? 4 : 1;              // waves per row (the oracle restates this rule)
+    const int wpr = k > 256 ? 4 : 1;               // waves per row (the oracle restates this rule)
     const int vpt = (int)((k + 256 * wpr - 1) / (256 * wpr));
     const bool vec = xk == 1 && k % 4 == 0 && ldq % 4 == 0 && xb % 4 == 0 && xt % 4 == 0 &&
                      ((uintptr_t)x % (4 * esz)) == 0 && ((uintptr_t)q % 4) == 0;
@@ -210,16 +376,76 @@ extern "C" int kea_quantize(const void *x, int x_dtype, int64_t xb, int64_t xt, 
                                (int)m, (int)k, parts, norm_w, norm_b, eps, input_silu, q, ldq, qs, qs_dtype);       \
     } while (0)
     if (wpr == 1) {
-        if (vpt <= 1) KEA_Q(1, 1);
-        else if (vpt <= 2) KEA_Q(2, 1);
-        else KEA_Q(4, 1);
+        KEA_Q(1, 1);
     } else {
-        if (vpt <= 2) KEA_Q(2, 4);
+        if (vpt <= 1) KEA_Q(1, 4);
+        else if (vpt <= 2) KEA_Q(2, 4);
         else if (vpt <= 4) KEA_Q(4, 4);
         else KEA_Q(8, 4);
     }
 #undef KEA_Q
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return kea::fail((int)e, std::string("quantize launch failed: ") + hipGetErrorString(e));
+    return KEA_OK;
+}
+
+extern "C" int kea_norm_quantize(const float *x, int64_t ldx, int64_t m, int64_t k, const float *norm0_w,
+                                 const float *norm0_b, float eps0, float *x_out, int64_t ldo, const float *norm1_w,
+                                 const float *norm1_b, float eps1, int parts, int8_t *q, int64_t ldq, float *qs,
+                                 void *stream) {
+    if (parts < 1 || parts > 3) return kea::fail(KEA_EINVAL, "parts must be 1, 2 or 3");
+    if (m < 0 || k < 4 || k > 4096 || m > INT32_MAX || k % 4) return kea::fail(KEA_EINVAL, "bad sizes (k in 4..4096, k % 4 == 0)");
+    if (ldx < k || ldo < k || ldq < k) return kea::fail(KEA_EINVAL, "leading dimension too small");
+    if (m == 0) return KEA_OK;
+    if (!x || !x_out || !q || !qs || !norm0_w || !norm0_b || !norm1_w || !norm1_b)
+        return kea::fail(KEA_EINVAL, "null pointer");
+    if (((uintptr_t)x | (uintptr_t)x_out | (uintptr_t)norm0_w | (uintptr_t)norm0_b | (uintptr_t)norm1_w |
+         (uintptr_t)norm1_b) & 15 || (ldx | ldo) & 3 || ((uintptr_t)q | (uintptr_t)ldq) & 3)
+        return kea::fail(KEA_EALIGN, "rows and norm weights need 16-byte alignment, q rows 4-byte alignment");
+    const int wpr = k > 256 ? 4 : 1, vpt = (int)((k + 256 * wpr - 1) / (256 * wpr));
+    const dim3 grid((unsigned)((m + 4 / wpr - 1) / (4 / wpr))), block(256);
+    hipStream_t st = (hipStream_t)stream;
+#define KEA_NQ(V, W)                                                                                             \
+    hipLaunchKernelGGL((norm_quantize_kernel<V, W>), grid, block, 0, st, x, (long long)ldx, (int)m, (int)k,        \
+                       norm0_w, norm0_b, eps0, x_out, (long long)ldo, norm1_w, norm1_b, eps1, parts, q,           \
+                       (long long)ldq, qs)
+    if (wpr == 1) KEA_NQ(1, 1);
+    else if (vpt <= 1) KEA_NQ(1, 4);
+    else if (vpt <= 2) KEA_NQ(2, 4);
+    else KEA_NQ(4, 4);
+#undef KEA_NQ
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("norm_quantize launch failed: ") + hipGetErrorString(e));
+    return KEA_OK;
+}
+
+extern "C" int kea_glu_dwconv_quantize(const float *x, int64_t ldx, const float *w, const float *bias, int64_t batch,
+                                       int64_t t, int64_t channels, int kernel, int parts, int8_t *q, int64_t ldq,
+                                       float *qs, void *stream) {
+    if (parts < 1 || parts > 3) return kea::fail(KEA_EINVAL, "parts must be 1, 2 or 3");
+    if (batch < 0 || t < 0 || batch > 65535 || t > INT32_MAX || channels < 4 || channels > 2048 || channels % 4 ||
+        kernel < 1 || kernel % 2 == 0)
+        return kea::fail(KEA_EINVAL, "bad sizes (channels in 4..2048, a multiple of 4; odd kernel width)");
+    if (ldx < 2 * channels || ldq < channels) return kea::fail(KEA_EINVAL, "leading dimension too small");
+    if (batch == 0 || t == 0) return KEA_OK;
+    if (!x || !w || !q || !qs) return kea::fail(KEA_EINVAL, "null pointer");
+    if (((uintptr_t)x | (uintptr_t)bias) & 15 || ldx & 3 || ((uintptr_t)q | (uintptr_t)ldq) & 3)
+        return kea::fail(KEA_EALIGN, "x rows and bias need 16-byte alignment, q rows 4-byte alignment");
+    const int vpt = (int)((channels + 1023) / 1024);
+    const dim3 grid((unsigned)t, (unsigned)batch), block(256);
+    hipStream_t st = (hipStream_t)stream;
+#define KEA_GQ(V, W)                                                                                             \
+    hipLaunchKernelGGL((glu_dwconv_quantize_kernel<V, W>), grid, block, 0, st, x, (long long)ldx, w, bias, (int)t, \
+                       (int)channels, kernel, parts, q, (long long)ldq, qs)
+    if (kernel == 9) {
+        if (vpt <= 1) KEA_GQ(1, 9);
+        else KEA_GQ(2, 9);
+    } else {
+        if (vpt <= 1) KEA_GQ(1, 0);
+        else KEA_GQ(2, 0);
+    }
+#undef KEA_GQ
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("glu_dwconv_quantize launch failed: ") + hipGetErrorString(e));
     return KEA_OK;
 }

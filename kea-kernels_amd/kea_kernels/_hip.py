@@ -49,6 +49,9 @@ SIGNATURES = {
                             _vp, _i32, _vp]),
     "kea_relpos_attention": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _f32, _vp]),
     "kea_glu_dwconv": (_i32, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
+    "kea_norm_quantize": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _f32, _vp, _i64, _vp, _vp, _f32, _i32, _vp, _i64,
+                                 _vp, _vp]),
+    "kea_glu_dwconv_quantize": (_i32, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _i64, _vp, _vp]),
     "kea_last_error": (_cp, []),
     "kea_version": (_i32, []),
 }

@@ -20,9 +20,11 @@ All 11 linears of a layer (W1, W2 of both FFs, W_q, W_k, W_v, W_out, W_pos, W_pw
 LayerNorms in front of W1 / W_qkv / W_pw1 fused into the quantizer, SiLU after W1 fused into the GEMM epilogue and
 the SiLU in front of W_pw2 fused into the quantizer (the reference's norm_quant / silu transforms). The attention core
 (relative-position scores, softmax, P.V) and GLU + depthwise convolution (BatchNorm folded into its weights) are the
-fused HIP kernels of include/kea_encoder.h (the reference's Triton relative_attention and glu_pad). The subsampling
-convolutions and the output LayerNorm are PyTorch on the GPU; the residual adds run in the epilogues of W2, W_out and
-W_pw2 (kea_lowbit_gemm_residual, the reference's row-epilogue residual). The quantized linears have no bias
+fused HIP kernels of include/kea_encoder.h (the reference's Triton relative_attention and glu_pad); the GLU kernel
+also applies the SiLU and quantizes for W_pw2 (kea_glu_dwconv_quantize), and each layer's output LayerNorm is fused
+with the next layer's normalised quantization for its W1 (kea_norm_quantize, the reference's row epilogue). The
+subsampling convolutions and the last layer's output LayerNorm are PyTorch on the GPU; the residual adds run in the
+epilogues of W2, W_out and W_pw2 (kea_lowbit_gemm_residual, the reference's row-epilogue residual). The quantized linears have no bias
 (Q/K/V must be bias-free to fuse, kk/binary/provider.py:230-244).
 
 `EncoderGraph` captures preprocessing + encoder for a fixed (batch, samples) into one HIP graph, as the reference
@@ -228,6 +230,39 @@ def glu_dwconv(x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
     return y
 
 
+def norm_quantize(x: Tensor, norm0, norm1, parts: int) -> tuple[Tensor, Tensor, Tensor]:
+    """x [B, T, K] contiguous -> (LayerNorm0(x), q, qs): q / qs the P-part quantization of LayerNorm1(LayerNorm0(x))
+    (kea_norm_quantize)."""
+    b, t, k = x.shape
+    m = b * t
+    ldq = lowbit.round_up(k, 16)
+    out = torch.empty_like(x)
+    q = torch.empty(parts, m, ldq, device=x.device, dtype=torch.int8)
+    qs = torch.empty(parts, m, device=x.device, dtype=torch.float32)
+    rc = _hip.lib().kea_norm_quantize(x.data_ptr(), k, m, k, norm0.weight.data_ptr(), norm0.bias.data_ptr(),
+                                      float(norm0.eps), out.data_ptr(), k, norm1.weight.data_ptr(),
+                                      norm1.bias.data_ptr(), float(norm1.eps), parts, q.data_ptr(), ldq,
+                                      qs.data_ptr(), _hip.stream_handle(x.device))
+    _hip.check(rc, "kea_norm_quantize")
+    return out, q, qs
+
+
+def glu_dwconv_quantize(x: Tensor, weight: Tensor, bias: Tensor | None, parts: int) -> tuple[Tensor, Tensor]:
+    """x [B, T, 2C] (rows contiguous) -> the P-part quantization (q, qs) of silu(depthwise_conv(GLU(x)))
+    (kea_glu_dwconv_quantize)."""
+    b, t, two_c = x.shape
+    c, kw = two_c // 2, weight.shape[-1]
+    if x.stride(2) != 1 or x.stride(0) != t * x.stride(1) or not weight.is_contiguous():
+        raise ValueError("x needs contiguous rows and a contiguous weight")
+    ldq = lowbit.round_up(c, 16)
+    q = torch.empty(parts, b * t, ldq, device=x.device, dtype=torch.int8)
+    qs = torch.empty(parts, b * t, device=x.device, dtype=torch.float32)
+    rc = _hip.lib().kea_glu_dwconv_quantize(x.data_ptr(), x.stride(1), weight.data_ptr(), _hip.ptr(bias), b, t, c, kw,
+                                            parts, q.data_ptr(), ldq, qs.data_ptr(), _hip.stream_handle(x.device))
+    _hip.check(rc, "kea_glu_dwconv_quantize")
+    return q, qs
+
+
 # --- the encoder -----------------------------------------------------------------------------------------------------
 
 class _DenseLinear:
@@ -322,20 +357,33 @@ class FastConformerEncoder:
         mod = self._fused.get(name) or self.modules[name]
         return self.project(x, mod, False, self.parts, activation, norm, None, input_activation)
 
-    def _residual(self, name: str, z: Tensor, r: Tensor, factor: float, *, input_activation="") -> Tensor:
+    def _residual(self, name: str, z: Tensor | None, r: Tensor, factor: float, *, input_activation="",
+                  quantized=None) -> Tensor:
         """r + factor * linear(z). Quantized: the residual add runs in the GEMM epilogue, in place into r
-        (kea_lowbit_gemm_residual; r is not used afterwards). Dense: PyTorch."""
+        (kea_lowbit_gemm_residual; r is not used afterwards); `quantized` = (q, qs) skips the quantizer. Dense:
+        PyTorch."""
         if self.dense:
             return torch.add(r, self._linear(name, z, input_activation=input_activation), alpha=factor)
         layer = self.modules[name]._entry.layer
-        b, t, k = z.shape
-        m, n = b * t, layer.out_features
-        q, qs, _ = lowbit.quantize(z, (z.stride(0), z.stride(1), z.stride(2), t), m, k, self.parts,
-                                   input_activation=input_activation)
+        m, n, k = r.shape[0] * r.shape[1], layer.out_features, layer.in_features
+        if quantized is None:
+            t = z.shape[1]
+            q, qs, _ = lowbit.quantize(z, (z.stride(0), z.stride(1), z.stride(2), t), m, k, self.parts,
+                                       input_activation=input_activation)
+        else:
+            q, qs = quantized
         r2 = r.view(m, n)
         lowbit.gemm(layer.WBITS, q, qs, layer.words, n, k, layer.scale, layer.bias, r2, None, residual=r2,
                     residual_factor=factor)
         return r
+
+    def _gemm(self, name: str, q: Tensor, qs: Tensor, m: int, *, silu: bool = False) -> Tensor:
+        """The quantized linear `name` on pre-quantized activations (q, qs): FP32 [m, N]."""
+        layer = self.modules[name]._entry.layer
+        y = torch.empty(m, layer.out_features, device=self.device, dtype=torch.float32)
+        lowbit.gemm(layer.WBITS, q, qs, layer.words, layer.out_features, layer.in_features, layer.scale, layer.bias,
+                    y, None, silu=silu)
+        return y
 
     def weight_bytes(self) -> int:
         return 0 if self.table is None else self.table.weight_bytes()
@@ -387,24 +435,33 @@ class FastConformerEncoder:
         out = torch.matmul(attn, v.transpose(1, 2).contiguous())                    # [B, H, T, dk]
         return out.transpose(1, 2).reshape(b, t, h * dk)
 
-    def layer(self, i: int, x: Tensor, pos: Tensor) -> Tensor:
+    def layer(self, i: int, x: Tensor, pos: Tensor, xq=None) -> Tensor | tuple:
+        """One layer. xq = (q, qs): x already quantized through this layer's first LayerNorm (by the previous layer's
+        fused output LayerNorm). Returns the layer output, or (output, q, qs) for the next layer when fused."""
         fp = self.layers[i]
         pre = f"encoder.layers.{i}."
-        y = self._linear(pre + "feed_forward1.linear1", x, norm=fp["norm_feed_forward1"], activation="silu")
+        if xq is None:
+            y = self._linear(pre + "feed_forward1.linear1", x, norm=fp["norm_feed_forward1"], activation="silu")
+        else:
+            b, t, _ = x.shape
+            y = self._gemm(pre + "feed_forward1.linear1", xq[0], xq[1], b * t, silu=True).view(b, t, -1)
         r = self._residual(pre + "feed_forward1.linear2", y, x, 0.5)
         qkv = self._linear(pre + "self_attn.qkv", r, norm=fp["norm_self_att"])
         r = self._residual(pre + "self_attn.linear_out", self.attention(qkv, pos, fp["u"], fp["v"]), r, 1.0)
         z = self._linear(pre + "conv.pointwise_conv1", r, norm=fp["norm_conv"])
         if self.fused:
-            z = glu_dwconv(z, fp["dw_w"], fp["dw_b"])
+            r = self._residual(pre + "conv.pointwise_conv2", None, r, 1.0,
+                               quantized=glu_dwconv_quantize(z, fp["dw_w"], fp["dw_b"], self.parts))
         else:
             z = F.glu(z, dim=-1)                                                    # a * sigmoid(g)
             z = F.conv1d(z.transpose(1, 2), fp["dw_w"], fp["dw_b"], padding=self.cfg.conv_kernel // 2,
                          groups=self.cfg.d_model).transpose(1, 2)
-        r = self._residual(pre + "conv.pointwise_conv2", z, r, 1.0, input_activation="silu")
+            r = self._residual(pre + "conv.pointwise_conv2", z, r, 1.0, input_activation="silu")
         y = self._linear(pre + "feed_forward2.linear1", r, norm=fp["norm_feed_forward2"], activation="silu")
         r = self._residual(pre + "feed_forward2.linear2", y, r, 0.5)
         n = fp["norm_out"]
+        if self.fused and i + 1 < self.cfg.layers:
+            return norm_quantize(r, n, self.layers[i + 1]["norm_feed_forward1"], self.parts)
         return F.layer_norm(r, n.normalized_shape, n.weight, n.bias, n.eps)
 
     def encode(self, feats: Tensor) -> Tensor:
@@ -412,8 +469,10 @@ class FastConformerEncoder:
         if self.cfg.xscaling:
             x = x * math.sqrt(self.cfg.d_model)
         pos = self.positions(x.shape[1])
+        xq = None
         for i in range(self.cfg.layers):
-            x = self.layer(i, x, pos[i])
+            out = self.layer(i, x, pos[i], xq)
+            x, xq = (out[0], out[1:]) if isinstance(out, tuple) else (out, None)
         return x
 
     @torch.inference_mode()

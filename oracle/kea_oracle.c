@@ -212,15 +212,13 @@ static float f16_to_f32(uint16_t h) {
     return f;
 }
 
-/* Sum of z[0..k) in the library's fixed order: 64 lane partials (lane l sums k = l, l + 64, ... in increasing k),
- * then a xor butterfly with offsets 32, 16, 8, 4, 2, 1 (lane 0's value). */
 /*
- * The library's fixed LayerNorm summation order: a row is split over WPR wave64s (1 for k <= 1024, else 4); thread th
+ * The library's fixed LayerNorm summation order: a row is split over WPR wave64s (1 for k <= 256, else 4); thread th
  * of the row sums, in increasing k, its 4-element chunks k = 4 * (th + 64 * WPR * i) + j; each wave combines its 64
  * partial sums with a xor butterfly (offsets 32, 16, ..., 1); the wave totals are then added in wave order.
  */
 static float row_sum(const float *z, int64_t k) {
-    const int wpr = k > 1024 ? 4 : 1, tpr = 64 * wpr;
+    const int wpr = k > 256 ? 4 : 1, tpr = 64 * wpr;
     float p[256];
     for (int th = 0; th < tpr; ++th) {
         float s = 0.f;

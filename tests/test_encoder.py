@@ -2,6 +2,7 @@
 against its FP32 dense twin on the GPU (relative Frobenius error bars per part count), and graph replay = eager."""
 from __future__ import annotations
 
+import copy
 import math
 
 import numpy as np
@@ -145,3 +146,56 @@ def test_fused_encoder_matches_unfused():
     plain = E.FastConformerEncoder(w, cfg, "cuda", parts=3, fused=False)(audio)
     rel = float((fused.double() - plain.double()).norm() / plain.double().norm())
     assert rel < 5e-6, rel
+
+
+def _layer_norm(k: int, g: torch.Generator) -> torch.nn.LayerNorm:
+    n = torch.nn.LayerNorm(k)
+    with torch.no_grad():
+        n.weight.copy_(torch.rand(k, generator=g) + 0.5)
+        n.bias.copy_(torch.randn(k, generator=g) * 0.1)
+    return n
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k,rows", [(1024, 74), (300, 9), (64, 1), (516, 130)])
+@torch.inference_mode()
+def test_norm_quantize_matches_layer_norm_and_oracle(k, rows):
+    """kea_norm_quantize: x_out = LayerNorm0(x) within FP32 rounding of an FP64 LayerNorm; q / qs bitwise the oracle's
+    normalised quantization (LayerNorm1) of that x_out, zero padding to ldq included."""
+    from oracle import oracle as O
+    g = torch.Generator().manual_seed(k + rows)
+    x = torch.randn(1, rows, k, generator=g) * 3 + 0.5
+    n0, n1 = _layer_norm(k, g), _layer_norm(k, g)
+    out, q, qs = E.norm_quantize(x.cuda(), copy.deepcopy(n0).cuda(), copy.deepcopy(n1).cuda(), 3)
+    torch.cuda.synchronize()
+    ref = F.layer_norm(x.double(), (k,), n0.weight.double(), n0.bias.double(), n0.eps)
+    assert float((out.cpu().double() - ref).abs().max()) < 2e-5
+    ldq = q.shape[2]
+    rq, rqs = O.quantize(out.cpu().reshape(rows, k).numpy(), 3, ldq=ldq,
+                         norm=(n1.weight.detach().numpy(), n1.bias.detach().numpy()), eps=n1.eps)
+    assert np.array_equal(q.cpu().numpy(), rq)
+    assert np.array_equal(qs.cpu().numpy(), rqs)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,t,c", [(2, 50, 96), (1, 125, 1024), (3, 17, 1536), (1, 1, 1024)])
+@torch.inference_mode()
+def test_glu_dwconv_quantize_equals_the_two_kernel_path(b, t, c):
+    """kea_glu_dwconv_quantize: bitwise kea_glu_dwconv followed by kea_quantize with the input SiLU; and the parts sum
+    to silu(conv(GLU(x))) (FP64) within half the last part's step."""
+    from kea_kernels import lowbit
+    g = torch.Generator().manual_seed(b * 1000 + t + c)
+    x = torch.randn(b, t, 2 * c, generator=g)
+    w = torch.randn(c, 1, 9, generator=g) / 3
+    bias = torch.randn(c, generator=g)
+    xd, wd, bd = x.cuda(), w.cuda(), bias.cuda()
+    q, qs = E.glu_dwconv_quantize(xd, wd, bd, 3)
+    z = E.glu_dwconv(xd, wd, bd)
+    rq, rqs, _ = lowbit.quantize(z, (z.stride(0), z.stride(1), 1, t), b * t, c, 3, input_activation="silu")
+    torch.cuda.synchronize()
+    assert torch.equal(q, rq) and torch.equal(qs, rqs)
+    conv = F.conv1d(F.glu(x.double(), dim=-1).transpose(1, 2), w.double(), bias.double(), padding=4,
+                    groups=c).transpose(1, 2).reshape(b * t, c)
+    ref = conv * torch.sigmoid(conv)
+    deq = sum(q[i, :, :c].cpu().double() * qs[i].cpu().double()[:, None] for i in range(3))
+    assert bool(((deq - ref).abs() <= 0.5 * qs[2].cpu().double()[:, None] + 2e-6 * ref.abs().amax(1, keepdim=True)).all())
