@@ -285,6 +285,8 @@ def main(argv=None) -> int:
                     help="only run BASELINE.json config 5 (24-layer encoder, batch 1 and 8; one JSON line each)")
     ap.add_argument("--encoder-cases", default="1x1,8x1,1x3,8x3", metavar="BxP,...",
                     help="batch x parts cases of --encoder")
+    ap.add_argument("--no-check-dense", action="store_true",
+                    help="--encoder: skip the FP32 dense comparison (profiles then hold only the quantized encoder)")
     ap.add_argument("--suite", action="store_true",
                     help="only time BASELINE.json configs 2-4 and the reference's tuned shapes (one JSON line each)")
     args = ap.parse_args(argv)
@@ -294,7 +296,7 @@ def main(argv=None) -> int:
     if args.encoder:
         for case in args.encoder_cases.split(","):
             batch, parts = (int(v) for v in case.split("x"))
-            print(json.dumps(encoder_bench(batch, parts)), flush=True)
+            print(json.dumps(encoder_bench(batch, parts, check_dense=not args.no_check_dense)), flush=True)
         return 0
     if args.copy_calibration:
         import torch

@@ -158,6 +158,28 @@ int kea_lowbit_slices_finish(const int32_t *slices_dev, int split, int parts, in
                              void *y_dev, int y_dtype, int64_t ldy, int32_t *acc_out_dev, int64_t acc_ld,
                              int flags, void *stream);
 
+/* The exact row epilogue, one launch per projection: for every row m of the [m][n] output,
+ *   value = kea_lowbit_slices_finish's value (slices summed in slice order, then the unsplit epilogue: bitwise
+ *           the unsplit kea_lowbit_gemm result; qs f32 [parts][qs_stride], wscale / bias f32 or f16 [n])
+ *   x     = residual ? residual[m*ldr + j] + value * factor : value      (an IEEE multiply, then an IEEE add)
+ *   x     = LayerNorm(x; out_norm_w, out_norm_b, out_eps)                 when out_norm_w != NULL
+ *   y[m*ldy + j] = x                                                      (FP32; y may be the residual itself)
+ *   q, q_scales = the q_parts-part quantization of LayerNorm(x; norm_w, norm_b, eps) (or of x when norm_w is NULL),
+ *                 bitwise what kea_quantize returns for y's rows (q int8 [q_parts][m][ldq] zero padded, q_scales f32
+ *                 [q_parts][m]); skipped when q is NULL.
+ * n in 4..4096 with n % 4 == 0; slices, y, residual and the LayerNorm weights 16-byte aligned, ldy and ldr multiples
+ * of 4, ldq >= n a multiple of 4. LayerNorm sums follow kea_quantize's fixed order. Replaces the reference's
+ * _row_epilogue_exact / _row_epilogue (kk/binary/row_exact.py:62-122, kk/ternary/row_fusion.py:27-52) behind
+ * finish_residual_exact / finish_residual (kk/binary/row_exact.py:125-156, kk/ternary/row_fusion.py:90-111). */
+int kea_row_epilogue(const int32_t *slices_dev, int split, int parts, int64_t m, int64_t n,
+                     const float *qs_dev, int64_t qs_stride, const void *wscale_dev, int ws_dtype,
+                     const void *bias_dev, int bias_dtype, int flags,
+                     const float *residual_dev, int64_t ldr, float factor,
+                     const float *out_norm_w_dev, const float *out_norm_b_dev, float out_eps,
+                     float *y_dev, int64_t ldy,
+                     const float *norm_w_dev, const float *norm_b_dev, float eps,
+                     int q_parts, int8_t *q_dev, int64_t ldq, float *q_scales_dev, void *stream);
+
 /* Workspace bytes kea_lowbit_gemm needs for these arguments (0 when split_k resolves to 1). */
 int64_t kea_lowbit_gemm_workspace(int wbits, int parts, int64_t m, int64_t n, int64_t k, int64_t ws_group,
                                   int split_k, int config);

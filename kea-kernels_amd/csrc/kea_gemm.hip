@@ -24,6 +24,7 @@
 #include <cstdio>
 #include <string>
 
+#include "kea_epilogue.h"
 #include "kea_internal.h"
 
 namespace kea {
@@ -69,10 +70,9 @@ struct Params {
     int gp_shift;   // log2 of the padded group count held in LDS (a power of two >= the groups the stages span)
 };
 
-__device__ __forceinline__ float load_scalar(const void *p, int dtype, long long i) {
-    if (dtype == KEA_F16) return (float)(((const _Float16 *)p)[i]);
-    return ((const float *)p)[i];
-}
+using kea::combine;
+using kea::finish;
+using kea::load_scalar;
 
 // 1-bit: plane (4h + d) of a native word -> four int8 weights. Stored bits are inverted signs, so after the mask
 // each selector byte is 0 (weight +1) or 2^(4h+d) (weight -1). The permute table {S0:S1} = {0x000000FF:0x00FFFF01}
@@ -90,26 +90,6 @@ __device__ __forceinline__ int t2_lo(uint32_t w) {
 }
 __device__ __forceinline__ int t2_hi(uint32_t w) {
     return (int)__builtin_amdgcn_perm(0x00000001u, 0x00008000u, w & 0x0C0C0C0Cu);
-}
-
-// The reference's P-part combination (comb<P>, kk/binary/kernels_parts.py:28-39). Built with -ffp-contract=off:
-// each * is one IEEE multiply, each fma an explicit fused multiply-add.
-template <int P>
-__device__ __forceinline__ float combine(const int *a, const float *s, int flags) {
-    if constexpr (P == 1) {
-        return (float)a[0] * s[0];
-    } else {
-        float r = (flags & KEA_FLAG_ORDER) ? __builtin_fmaf((float)a[1], s[1], (float)a[0] * s[0])
-                                           : __builtin_fmaf((float)a[0], s[0], (float)a[1] * s[1]);
-        if constexpr (P == 3) r = __builtin_fmaf((float)a[2], s[2], r);
-        return r;
-    }
-}
-
-__device__ __forceinline__ float finish(float r, float alpha, bool has_bias, float b, int flags) {
-    r = has_bias ? __builtin_fmaf(r, alpha, b) : r * alpha;
-    if (flags & KEA_FLAG_SILU) r = r / (1.0f + expf(-r));
-    return r;
 }
 
 __device__ __forceinline__ uint16_t to_f16_bits(float v) {
@@ -252,7 +232,9 @@ struct StageShape {
 constexpr int kLdsBudget = 160 * 1024;
 // Ring depth cap. Sweeps on MI355X over the BASELINE shapes: two buffers per workgroup beat deeper rings nearly
 // everywhere (up to 1.7x at P = 3), because the LDS a deeper ring takes costs more in co-resident workgroups (the
-// latency hiding that matters) than the extra stages in flight give back.
+// latency hiding that matters) than the extra stages in flight give back. Grids of at most one workgroup per CU
+// (small M, K = 4096) measured slower with eight buffers too: there a stage's time is set by the copies' throughput,
+// not by their latency.
 #ifndef KEA_MAX_STAGES
 #define KEA_MAX_STAGES 2
 #endif
@@ -461,20 +443,25 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     };
 
     // One stage of MFMAs: straight-line code (no accumulator ever passes a control-flow merge; merges made the
-    // compiler emit AGPR copy chains). The LDS reads of word w + 1 are issued before the MFMAs of word w. MASKED (the
-    // last stage) zeroes the weights at k >= kend: per 16-byte group of a lane's operand, or per byte for KTAIL.
+    // compiler emit AGPR copy chains). Operand reads from LDS run ahead of the MFMAs: narrow tiles (P * RM <= 3, few
+    // MFMAs per k-step) issue every read of the stage before the first MFMA, so a stage pays one LDS latency instead
+    // of one per k-step; wider tiles read k-step t + 1 while the MFMAs of step t run. MASKED (the last stage) zeroes
+    // the weights at k >= kend: per 16-byte group of a lane's operand, or per byte for KTAIL.
     auto compute = [&](int s, auto masked_tag) {
         constexpr bool MASKED = decltype(masked_tag)::value;
         const int8_t *buf = lds + (s % NS) * STAGE_BYTES;
         constexpr int STEPS = SW * KS;  // MFMA k-steps per stage
-        v4i af[2][P][RM];
-        uint32_t wv[2][RN];
+        constexpr bool FULL = P * RM <= 3;
+        constexpr int ASLOTS = FULL ? STEPS : 2, WSLOTS = FULL ? SW : 2;
+        v4i af[ASLOTS][P][RM];
+        uint32_t wv[WSLOTS][RN];
         auto fetch = [&](int t, int slot) {
             const int w = t / KS, h = t % KS;
             if (h == 0) {
 #pragma unroll
                 for (int jn = 0; jn < RN; ++jn)
-                    wv[w & 1][jn] = *(const uint32_t *)(buf + A_BYTES + ((wn * RN + jn) * SW + w) * 256 + lane * 4);
+                    wv[w % WSLOTS][jn] =
+                        *(const uint32_t *)(buf + A_BYTES + ((wn * RN + jn) * SW + w) * 256 + lane * 4);
             }
 #pragma unroll
             for (int c = 0; c < P; ++c)
@@ -485,17 +472,22 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
                     af[slot][c][i] = *(const v4i *)(buf + ((c * BM + r) * CHS + (ch ^ swz(r))) * 16);
                 }
         };
-        fetch(0, 0);
+        if constexpr (FULL) {
+#pragma unroll
+            for (int t = 0; t < STEPS; ++t) fetch(t, t);
+        } else {
+            fetch(0, 0);
+        }
 #pragma unroll
         for (int t = 0; t < STEPS; ++t) {
             const int w = t / KS, h = t % KS;
-            if (t + 1 < STEPS) fetch(t + 1, (t + 1) & 1);
+            if (!FULL && t + 1 < STEPS) fetch(t + 1, (t + 1) & 1);
             __builtin_amdgcn_sched_barrier(0);  // keep the next k-step's LDS reads ahead of this one's MFMAs
-            const int slot = t & 1;
+            const int slot = FULL ? t : t & 1;
             const int kstep = (ja + s * SW + w) * KW + h * 64;
 #pragma unroll
             for (int jn = 0; jn < RN; ++jn) {
-                const uint32_t w32 = wv[w & 1][jn];
+                const uint32_t w32 = wv[w % WSLOTS][jn];
                 v4i bf;
                 if constexpr (WBITS == 1) {
                     if (h == 0) {
@@ -967,11 +959,12 @@ static int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ld
 
     const Tile &t = kTiles[tile - 1];
     const int bm = t.wm * t.rm * 16, bn = t.wn * t.rn * 16;
-    const StageShape shape = stage_shape(wbits, parts, t.rm, t.rn, t.wm, t.wn);
     // Ring buffers actually used: a workgroup touches buffer s % NS for its stages s < nst, so with nst < NS only
     // the first nst buffers need LDS.
     const long long words_per_wg = std::min<long long>(4LL * qps, (long long)p.J);
-    const int nst = (int)cdivl(words_per_wg, shape.sw);
+    const int sw = wbits == 1 ? 2 : 4;
+    const int nst = (int)cdivl(words_per_wg, sw);
+    const StageShape shape = stage_shape(wbits, parts, t.rm, t.rn, t.wm, t.wn);
     int lds_bytes = std::min(shape.ns, nst) * shape.stage_bytes;
     if (gq) {
         // alpha block: the groups the stages span (4 k-steps of 64 per stage), padded to a power of two
@@ -1066,9 +1059,10 @@ int kea_lowbit_gemm_slices(int wbits, const int8_t *q, int64_t part_stride, int6
     p.slice_vec = (n % 4 == 0);
     const Tile &t = kTiles[tile - 1];
     const int bm = t.wm * t.rm * 16, bn = t.wn * t.rn * 16;
-    const StageShape shape = stage_shape(wbits, parts, t.rm, t.rn, t.wm, t.wn);
     const long long words_per_wg = std::min<long long>(4LL * qps, (long long)p.J);
-    const int lds_bytes = std::min(shape.ns, (int)cdivl(words_per_wg, shape.sw)) * shape.stage_bytes;
+    const int nst = (int)cdivl(words_per_wg, wbits == 1 ? 2 : 4);
+    const StageShape shape = stage_shape(wbits, parts, t.rm, t.rn, t.wm, t.wn);
+    const int lds_bytes = std::min(shape.ns, nst) * shape.stage_bytes;
     KernelFn fn = pick_kernel(wbits, parts, tile, true, false);
     if (lds_bytes > 65536) {
         hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);

@@ -19,6 +19,7 @@
 #include <cstdint>
 #include <string>
 
+#include "kea_epilogue.h"
 #include "kea_internal.h"
 #include "../../include/kea_encoder.h"
 
@@ -345,6 +346,107 @@ glu_dwconv_quantize_kernel(const float *x, long long ldx, const float *w, const 
     quantize_parts<VPT, 4>(z, C, parts, q, ldq, qs, M, m, th, red[0], wave);
 }
 
+// The exact row epilogue: per row m (WPR waves, the quantizer's layout and reduction order), the split-K slices
+// summed in slice order (exact int32), the GEMM epilogue (kea::combine / kea::finish: the unsplit kernel's value, bit
+// for bit), the residual x = res + value * factor, an optional LayerNorm stored as y, then optionally the P-part
+// quantization of LayerNorm(y) for the next projection. The reference's _row_epilogue_exact / _row_epilogue
+// (kk/binary/row_exact.py:62-122, kk/ternary/row_fusion.py:27-52).
+struct RowParams {
+    const int32_t *slices;
+    int split, M, N, flags;
+    const float *qs;
+    long long qs_stride;
+    const void *ws, *bias;
+    int ws_dtype, bias_dtype;
+    const float *res;
+    long long ldr;
+    float factor;
+    const float *ow, *ob;
+    float oeps;
+    float *y;
+    long long ldy;
+    const float *nw, *nb;
+    float eps;
+    int qparts;
+    int8_t *q;
+    long long ldq;
+    float *qsc;
+};
+
+template <int P, int VPT, int WPR>
+__global__ void __launch_bounds__(256) row_epilogue_kernel(RowParams rp) {
+    constexpr int RPB = 4 / WPR, TPR = 64 * WPR;
+    constexpr int G = VPT >= 4 ? 1 : (VPT == 2 ? 2 : 4);  // slices whose loads are issued together
+    __shared__ float red[RPB][7][WPR];
+    const int th = threadIdx.x % TPR, rl = threadIdx.x / TPR, wave = th >> 6, m = blockIdx.x * RPB + rl;
+    if (m >= rp.M) return;  // whole rows leave together: the row's barriers stay matched
+    const int N = rp.N;
+    const long long plane = (long long)rp.M * N;
+    int a[VPT][P][4];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+#pragma unroll
+        for (int c = 0; c < P; ++c) a[i][c][0] = a[i][c][1] = a[i][c][2] = a[i][c][3] = 0;
+    for (int z0 = 0; z0 < rp.split; z0 += G) {
+        int4 v[G][P][VPT];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int c = 0; c < P; ++c)
+#pragma unroll
+                for (int i = 0; i < VPT; ++i) {
+                    const int n0 = 4 * (th + TPR * i);
+                    v[g][c][i] = make_int4(0, 0, 0, 0);
+                    if (z0 + g < rp.split && n0 < N)
+                        v[g][c][i] = *(const int4 *)(rp.slices + ((long long)(z0 + g) * P + c) * plane +
+                                                     (long long)m * N + n0);
+                }
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int c = 0; c < P; ++c)
+#pragma unroll
+                for (int i = 0; i < VPT; ++i) {
+                    a[i][c][0] += v[g][c][i].x; a[i][c][1] += v[g][c][i].y;
+                    a[i][c][2] += v[g][c][i].z; a[i][c][3] += v[g][c][i].w;
+                }
+    }
+    float s[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) s[c] = c < P ? rp.qs[c * rp.qs_stride + m] : 0.f;
+    float z[VPT][4];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int n0 = 4 * (th + TPR * i);
+        z[i][0] = z[i][1] = z[i][2] = z[i][3] = 0.f;
+        if (n0 < N) {
+            float4 r4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (rp.res) r4 = *(const float4 *)(rp.res + (long long)m * rp.ldr + n0);
+            const float res[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int ar[3] = {a[i][0][e], P > 1 ? a[i][P > 1 ? 1 : 0][e] : 0,
+                                   P > 2 ? a[i][P > 2 ? 2 : 0][e] : 0};
+                const float alpha = kea::load_scalar(rp.ws, rp.ws_dtype, n0 + e);
+                const float b = rp.bias ? kea::load_scalar(rp.bias, rp.bias_dtype, n0 + e) : 0.f;
+                float v = kea::finish(kea::combine<P>(ar, s, rp.flags), alpha, rp.bias != nullptr, b, rp.flags);
+                if (rp.res) v = res[e] + v * rp.factor;
+                z[i][e] = v;
+            }
+        }
+    }
+    if (rp.ow) layer_norm_row<VPT, WPR>(z, N, rp.ow, rp.ob, rp.oeps, th, red[rl], wave, 5);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int n0 = 4 * (th + TPR * i);
+        if (n0 < N) *(float4 *)(rp.y + (long long)m * rp.ldy + n0) = make_float4(z[i][0], z[i][1], z[i][2], z[i][3]);
+    }
+    if (rp.q) {
+        if (rp.nw) layer_norm_row<VPT, WPR>(z, N, rp.nw, rp.nb, rp.eps, th, red[rl], wave, 0);
+        quantize_parts<VPT, WPR>(z, N, rp.qparts, rp.q, rp.ldq, rp.qsc, rp.M, m, th, red[rl], wave);
+    }
+}
+
 }  // namespace
 
 extern "C" int kea_quantize(const void *x, int x_dtype, int64_t xb, int64_t xt, int64_t xk, int64_t t, int64_t m,
@@ -447,5 +549,58 @@ extern "C" int kea_glu_dwconv_quantize(const float *x, int64_t ldx, const float 
 #undef KEA_GQ
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return kea::fail((int)e, std::string("glu_dwconv_quantize launch failed: ") + hipGetErrorString(e));
+    return KEA_OK;
+}
+
+extern "C" int kea_row_epilogue(const int32_t *slices, int split, int parts, int64_t m, int64_t n, const float *qs,
+                                int64_t qs_stride, const void *wscale, int ws_dtype, const void *bias, int bias_dtype,
+                                int flags, const float *residual, int64_t ldr, float factor, const float *out_norm_w,
+                                const float *out_norm_b, float out_eps, float *y, int64_t ldy, const float *norm_w,
+                                const float *norm_b, float eps, int q_parts, int8_t *q, int64_t ldq, float *q_scales,
+                                void *stream) {
+    if (split < 1 || parts < 1 || parts > 3) return kea::fail(KEA_EINVAL, "split must be >= 1 and parts 1, 2 or 3");
+    if (m < 0 || n < 4 || n > 4096 || n % 4 || m > INT32_MAX)
+        return kea::fail(KEA_EINVAL, "bad sizes (n in 4..4096, a multiple of 4)");
+    if (flags & ~(KEA_FLAG_SILU | KEA_FLAG_ORDER)) return kea::fail(KEA_EINVAL, "unknown flags");
+    if (ws_dtype != KEA_F32 && ws_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "wscale dtype must be f32 or f16");
+    if (bias && bias_dtype != KEA_F32 && bias_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "bias dtype must be f32 or f16");
+    if ((out_norm_w == nullptr) != (out_norm_b == nullptr) || (norm_w == nullptr) != (norm_b == nullptr))
+        return kea::fail(KEA_EINVAL, "LayerNorm weight and bias go together");
+    if (norm_w && !q) return kea::fail(KEA_EINVAL, "a LayerNorm for the next projection needs q");
+    if (q && (q_parts < 1 || q_parts > 3 || !q_scales || ldq < n || ldq % 4))
+        return kea::fail(KEA_EINVAL, "q needs q_parts 1..3, q_scales and ldq >= n, ldq % 4 == 0");
+    if (ldy < n || (residual && ldr < n) || (parts > 1 && qs_stride < m)) return kea::fail(KEA_EINVAL, "leading dimension too small");
+    if (m == 0) return KEA_OK;
+    if (!slices || !qs || !wscale || !y) return kea::fail(KEA_EINVAL, "slices, qs, wscale and y are required");
+    if (((uintptr_t)slices | (uintptr_t)y | (uintptr_t)residual | (uintptr_t)out_norm_w | (uintptr_t)out_norm_b |
+         (uintptr_t)norm_w | (uintptr_t)norm_b) & 15 || (ldy | (residual ? ldr : 0)) & 3 || (uintptr_t)q & 3)
+        return kea::fail(KEA_EALIGN, "slices, y, residual and LayerNorm weights need 16-byte alignment");
+    RowParams rp = {};
+    rp.slices = slices; rp.split = split; rp.M = (int)m; rp.N = (int)n; rp.flags = flags;
+    rp.qs = qs; rp.qs_stride = qs_stride; rp.ws = wscale; rp.ws_dtype = ws_dtype;
+    rp.bias = bias; rp.bias_dtype = bias_dtype;
+    rp.res = residual; rp.ldr = ldr; rp.factor = factor;
+    rp.ow = out_norm_w; rp.ob = out_norm_b; rp.oeps = out_eps;
+    rp.y = y; rp.ldy = ldy;
+    rp.nw = norm_w; rp.nb = norm_b; rp.eps = eps;
+    rp.qparts = q_parts; rp.q = q; rp.ldq = ldq; rp.qsc = q_scales;
+    const int wpr = n > 256 ? 4 : 1, vpt = (int)((n + 256 * wpr - 1) / (256 * wpr));
+    const dim3 grid((unsigned)((m + 4 / wpr - 1) / (4 / wpr))), block(256);
+    hipStream_t st = (hipStream_t)stream;
+#define KEA_RE(P_, V, W) hipLaunchKernelGGL((row_epilogue_kernel<P_, V, W>), grid, block, 0, st, rp)
+#define KEA_RE_P(P_)                         \
+    do {                                     \
+        if (wpr == 1) KEA_RE(P_, 1, 1);      \
+        else if (vpt <= 1) KEA_RE(P_, 1, 4); \
+        else if (vpt <= 2) KEA_RE(P_, 2, 4); \
+        else KEA_RE(P_, 4, 4);               \
+    } while (0)
+    if (parts == 1) KEA_RE_P(1);
+    else if (parts == 2) KEA_RE_P(2);
+    else KEA_RE_P(3);
+#undef KEA_RE_P
+#undef KEA_RE
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("row epilogue launch failed: ") + hipGetErrorString(e));
     return KEA_OK;
 }

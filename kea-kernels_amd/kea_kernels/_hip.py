@@ -40,6 +40,8 @@ SIGNATURES = {
     "kea_lowbit_gemm_slices": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _vp]),
     "kea_lowbit_slices_finish": (_i32, [_vp, _i32, _i32, _i64, _i64, _vp, _i32, _i64, _vp, _i32, _vp, _i32, _vp,
                                         _i32, _i64, _vp, _i64, _i32, _vp]),
+    "kea_row_epilogue": (_i32, [_vp, _i32, _i32, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _i32, _i32, _vp, _i64, _f32,
+                                _vp, _vp, _f32, _vp, _i64, _vp, _vp, _f32, _i32, _vp, _i64, _vp, _vp]),
     "kea_lowbit_gemm_workspace": (_i64, [_i32, _i32, _i64, _i64, _i64, _i64, _i32, _i32]),
     "kea_lowbit_gemm_tile": (_i32, [_i32, _i32, _i64, _i64, _i64]),
     "kea_lowbit_gemm_split": (_i32, [_i32, _i32, _i64, _i64, _i64, _i64, _i32]),

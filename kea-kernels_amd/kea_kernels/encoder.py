@@ -21,10 +21,12 @@ LayerNorms in front of W1 / W_qkv / W_pw1 fused into the quantizer, SiLU after W
 the SiLU in front of W_pw2 fused into the quantizer (the reference's norm_quant / silu transforms). The attention core
 (relative-position scores, softmax, P.V) and GLU + depthwise convolution (BatchNorm folded into its weights) are the
 fused HIP kernels of include/kea_encoder.h (the reference's Triton relative_attention and glu_pad); the GLU kernel
-also applies the SiLU and quantizes for W_pw2 (kea_glu_dwconv_quantize), and each layer's output LayerNorm is fused
-with the next layer's normalised quantization for its W1 (kea_norm_quantize, the reference's row epilogue). The
-subsampling convolutions and the last layer's output LayerNorm are PyTorch on the GPU; the residual adds run in the
-epilogues of W2, W_out and W_pw2 (kea_lowbit_gemm_residual, the reference's row-epilogue residual). The quantized linears have no bias
+also applies the SiLU and quantizes for W_pw2 (kea_glu_dwconv_quantize). The four residual projections (W2 of both
+FFs, W_out, W_pw2) write exact int32 K-slices, and one row epilogue per block (kea_row_epilogue, the reference's
+row_fusions with _row_epilogue_exact) adds the residual, applies the output LayerNorm at the end of a layer and
+quantizes the next block's input through its LayerNorm. The subsampling convolutions are PyTorch on the GPU.
+With fused=False the same model runs with separate quantizers, the residual in the GEMM epilogue
+(kea_lowbit_gemm_residual) and PyTorch attention, GLU and convolution. The quantized linears have no bias
 (Q/K/V must be bias-free to fuse, kk/binary/provider.py:230-244).
 
 `EncoderGraph` captures preprocessing + encoder for a fixed (batch, samples) into one HIP graph, as the reference
@@ -230,13 +232,15 @@ def glu_dwconv(x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
     return y
 
 
-def norm_quantize(x: Tensor, norm0, norm1, parts: int) -> tuple[Tensor, Tensor, Tensor]:
+def norm_quantize(x: Tensor, norm0, norm1, parts: int, *, out: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """x [B, T, K] contiguous -> (LayerNorm0(x), q, qs): q / qs the P-part quantization of LayerNorm1(LayerNorm0(x))
-    (kea_norm_quantize)."""
+    (kea_norm_quantize). `out` (contiguous like x, may be x itself) receives LayerNorm0(x)."""
     b, t, k = x.shape
     m = b * t
     ldq = lowbit.round_up(k, 16)
-    out = torch.empty_like(x)
+    if not x.is_contiguous() or (out is not None and (not out.is_contiguous() or out.shape != x.shape)):
+        raise ValueError("x and out must be contiguous [B, T, K]")
+    out = torch.empty_like(x) if out is None else out
     q = torch.empty(parts, m, ldq, device=x.device, dtype=torch.int8)
     qs = torch.empty(parts, m, device=x.device, dtype=torch.float32)
     rc = _hip.lib().kea_norm_quantize(x.data_ptr(), k, m, k, norm0.weight.data_ptr(), norm0.bias.data_ptr(),
@@ -357,29 +361,34 @@ class FastConformerEncoder:
         mod = self._fused.get(name) or self.modules[name]
         return self.project(x, mod, False, self.parts, activation, norm, None, input_activation)
 
-    def _residual(self, name: str, z: Tensor | None, r: Tensor, factor: float, *, input_activation="",
-                  quantized=None) -> Tensor:
+    def _residual(self, name: str, z: Tensor, r: Tensor, factor: float, *, input_activation="") -> Tensor:
         """r + factor * linear(z). Quantized: the residual add runs in the GEMM epilogue, in place into r
-        (kea_lowbit_gemm_residual; r is not used afterwards); `quantized` = (q, qs) skips the quantizer. Dense:
-        PyTorch."""
+        (kea_lowbit_gemm_residual; r is not used afterwards). Dense: PyTorch."""
         if self.dense:
             return torch.add(r, self._linear(name, z, input_activation=input_activation), alpha=factor)
         layer = self.modules[name]._entry.layer
-        m, n, k = r.shape[0] * r.shape[1], layer.out_features, layer.in_features
-        if quantized is None:
-            t = z.shape[1]
-            q, qs, _ = lowbit.quantize(z, (z.stride(0), z.stride(1), z.stride(2), t), m, k, self.parts,
-                                       input_activation=input_activation)
-        else:
-            q, qs = quantized
+        b, t, k = z.shape
+        m, n = b * t, layer.out_features
+        q, qs, _ = lowbit.quantize(z, (z.stride(0), z.stride(1), z.stride(2), t), m, k, self.parts,
+                                   input_activation=input_activation)
         r2 = r.view(m, n)
         lowbit.gemm(layer.WBITS, q, qs, layer.words, n, k, layer.scale, layer.bias, r2, None, residual=r2,
                     residual_factor=factor)
         return r
 
+    def _layer(self, name: str):
+        """The prepared layer behind `name` (the fused QKV handle resolves through the provider's table)."""
+        mod = self._fused.get(name)
+        if mod is None:
+            return self.modules[name]._entry.layer
+        entry, offset, count = self.project._lookup(mod)
+        if offset or count != entry.out_features:
+            raise ValueError(f"{name} does not cover a whole prepared layer")
+        return entry.layer
+
     def _gemm(self, name: str, q: Tensor, qs: Tensor, m: int, *, silu: bool = False) -> Tensor:
         """The quantized linear `name` on pre-quantized activations (q, qs): FP32 [m, N]."""
-        layer = self.modules[name]._entry.layer
+        layer = self._layer(name)
         y = torch.empty(m, layer.out_features, device=self.device, dtype=torch.float32)
         lowbit.gemm(layer.WBITS, q, qs, layer.words, layer.out_features, layer.in_features, layer.scale, layer.bias,
                     y, None, silu=silu)
@@ -435,33 +444,88 @@ class FastConformerEncoder:
         out = torch.matmul(attn, v.transpose(1, 2).contiguous())                    # [B, H, T, dk]
         return out.transpose(1, 2).reshape(b, t, h * dk)
 
-    def layer(self, i: int, x: Tensor, pos: Tensor, xq=None) -> Tensor | tuple:
-        """One layer. xq = (q, qs): x already quantized through this layer's first LayerNorm (by the previous layer's
-        fused output LayerNorm). Returns the layer output, or (output, q, qs) for the next layer when fused."""
+    def _quantize(self, z: Tensor, *, norm=None) -> tuple[Tensor, Tensor]:
+        """The P-part quantization of the rows of z ([B, T, K] or [M, K], unit element stride)."""
+        z3 = z if z.dim() == 3 else z.unsqueeze(0)
+        b, t, k = z3.shape
+        q, qs, _ = lowbit.quantize(z3, (z3.stride(0), z3.stride(1), z3.stride(2), t), b * t, k, self.parts, norm=norm)
+        return q, qs
+
+    @staticmethod
+    def _split(m: int, k: int) -> int:
+        """K slices of a residual projection. Small batches cut the FFN down projections (K = 4096) in 4 so that
+        the GEMM fills the chip (measured on MI355X: batch 1, 125 frames, 0.2 ms per clip); at batch 8 the int32
+        slices cost more traffic than the split saves. Exact integer slices make every choice give the same bits."""
+        return 4 if k >= 4096 and m <= 256 else 1
+
+    def _block(self, name: str, q: Tensor, qs: Tensor, r: Tensor, factor: float, *, norm=None, out_norm=None):
+        """r <- out_norm(r + factor * linear(q)) in place; with `norm`, returns the next projection's (q, qs) = the
+        P-part quantization of norm(r). Split K: the GEMM writes exact int32 K-slices and one row epilogue launch
+        (kea_row_epilogue) finishes them, adds the residual, normalises and quantizes. Unsplit: the residual add
+        runs in the GEMM epilogue and the LayerNorm(s) + quantization in one row kernel (kea_norm_quantize /
+        kea_quantize). Both give the same bits."""
+        layer = self._layer(name)
+        b, t, n = r.shape
+        m, k = b * t, layer.in_features
+        split = self._split(m, k)
+        r2 = r.view(m, n)
+        if split > 1:
+            slices = torch.empty(split, self.parts, m, n, device=self.device, dtype=torch.int32)
+            lowbit.gemm_slices(layer.WBITS, q, layer.words, n, k, slices, m=m)
+            return lowbit.row_epilogue(slices, qs, layer.scale, layer.bias, r2, residual=r2, factor=factor,
+                                       out_norm=out_norm, norm=norm,
+                                       quantize_parts=self.parts if norm is not None else 0)
+        lowbit.gemm(layer.WBITS, q, qs, layer.words, n, k, layer.scale, layer.bias, r2, None, residual=r2,
+                    residual_factor=factor)
+        if out_norm is not None and norm is not None:
+            return norm_quantize(r, out_norm, norm, self.parts, out=r)[1:]
+        if out_norm is not None:
+            r.copy_(F.layer_norm(r, out_norm.normalized_shape, out_norm.weight, out_norm.bias, out_norm.eps))
+            return None
+        return self._quantize(r, norm=norm) if norm is not None else None
+
+    def _layer_rows(self, i: int, x: Tensor, pos: Tensor, xq=None):
+        """The fused layer: each residual block ends in one row epilogue that also quantizes the next block's
+        input (the reference's row_fusions forward, kk/ternary/row_fusion.py:121-152). x is updated in place."""
         fp = self.layers[i]
         pre = f"encoder.layers.{i}."
+        b, t, _ = x.shape
+        m = b * t
         if xq is None:
-            y = self._linear(pre + "feed_forward1.linear1", x, norm=fp["norm_feed_forward1"], activation="silu")
-        else:
-            b, t, _ = x.shape
-            y = self._gemm(pre + "feed_forward1.linear1", xq[0], xq[1], b * t, silu=True).view(b, t, -1)
+            xq = self._quantize(x, norm=fp["norm_feed_forward1"])
+        y = self._gemm(pre + "feed_forward1.linear1", *xq, m, silu=True)
+        xq = self._block(pre + "feed_forward1.linear2", *self._quantize(y), x, 0.5, norm=fp["norm_self_att"])
+        qkv = self._gemm(pre + "self_attn.qkv", *xq, m).view(b, t, -1)
+        att = self.attention(qkv, pos, fp["u"], fp["v"])
+        xq = self._block(pre + "self_attn.linear_out", *self._quantize(att), x, 1.0, norm=fp["norm_conv"])
+        z = self._gemm(pre + "conv.pointwise_conv1", *xq, m).view(b, t, -1)
+        xq = self._block(pre + "conv.pointwise_conv2", *glu_dwconv_quantize(z, fp["dw_w"], fp["dw_b"], self.parts),
+                         x, 1.0, norm=fp["norm_feed_forward2"])
+        y = self._gemm(pre + "feed_forward2.linear1", *xq, m, silu=True)
+        following = self.layers[i + 1]["norm_feed_forward1"] if i + 1 < self.cfg.layers else None
+        xq = self._block(pre + "feed_forward2.linear2", *self._quantize(y), x, 0.5, norm=following,
+                         out_norm=fp["norm_out"])
+        return x, xq
+
+    def layer(self, i: int, x: Tensor, pos: Tensor, xq=None) -> Tensor | tuple:
+        """One layer. Fused (quantized, fused=True): returns (x, xq) with x updated in place and xq = (q, qs) the
+        next layer's quantized input (None after the last layer). Otherwise returns the layer output."""
+        if self.fused:
+            return self._layer_rows(i, x, pos, xq)
+        fp = self.layers[i]
+        pre = f"encoder.layers.{i}."
+        y = self._linear(pre + "feed_forward1.linear1", x, norm=fp["norm_feed_forward1"], activation="silu")
         r = self._residual(pre + "feed_forward1.linear2", y, x, 0.5)
         qkv = self._linear(pre + "self_attn.qkv", r, norm=fp["norm_self_att"])
         r = self._residual(pre + "self_attn.linear_out", self.attention(qkv, pos, fp["u"], fp["v"]), r, 1.0)
         z = self._linear(pre + "conv.pointwise_conv1", r, norm=fp["norm_conv"])
-        if self.fused:
-            r = self._residual(pre + "conv.pointwise_conv2", None, r, 1.0,
-                               quantized=glu_dwconv_quantize(z, fp["dw_w"], fp["dw_b"], self.parts))
-        else:
-            z = F.glu(z, dim=-1)                                                    # a * sigmoid(g)
-            z = F.conv1d(z.transpose(1, 2), fp["dw_w"], fp["dw_b"], padding=self.cfg.conv_kernel // 2,
-                         groups=self.cfg.d_model).transpose(1, 2)
-            r = self._residual(pre + "conv.pointwise_conv2", z, r, 1.0, input_activation="silu")
+        z = F.glu(z, dim=-1)                                                    # a * sigmoid(g)
+        z = F.conv1d(z.transpose(1, 2), fp["dw_w"], fp["dw_b"], padding=self.cfg.conv_kernel // 2,
+                     groups=self.cfg.d_model).transpose(1, 2)
+        r = self._residual(pre + "conv.pointwise_conv2", z, r, 1.0, input_activation="silu")
         y = self._linear(pre + "feed_forward2.linear1", r, norm=fp["norm_feed_forward2"], activation="silu")
         r = self._residual(pre + "feed_forward2.linear2", y, r, 0.5)
         n = fp["norm_out"]
-        if self.fused and i + 1 < self.cfg.layers:
-            return norm_quantize(r, n, self.layers[i + 1]["norm_feed_forward1"], self.parts)
         return F.layer_norm(r, n.normalized_shape, n.weight, n.bias, n.eps)
 
     def encode(self, feats: Tensor) -> Tensor:
@@ -472,7 +536,7 @@ class FastConformerEncoder:
         xq = None
         for i in range(self.cfg.layers):
             out = self.layer(i, x, pos[i], xq)
-            x, xq = (out[0], out[1:]) if isinstance(out, tuple) else (out, None)
+            x, xq = out if isinstance(out, tuple) else (out, None)
         return x
 
     @torch.inference_mode()

@@ -133,6 +133,61 @@ def slices_finish(slices: Tensor, qs: Tensor, wscale: Tensor, bias: Tensor | Non
     _hip.check(rc, "kea_lowbit_slices_finish")
 
 
+def _norm_params(norm, n: int, device) -> tuple[Tensor | None, Tensor | None, float]:
+    if norm is None:
+        return None, None, 0.0
+    w = norm.weight.detach()
+    b = norm.bias.detach()
+    if w.numel() != n or b.numel() != n:
+        raise ValueError("LayerNorm shape does not match the row length")
+    if w.dtype != torch.float32 or w.device != device or not w.is_contiguous():
+        w = w.to(device=device, dtype=torch.float32).contiguous()
+    if b.dtype != torch.float32 or b.device != device or not b.is_contiguous():
+        b = b.to(device=device, dtype=torch.float32).contiguous()
+    return w, b, float(norm.eps)
+
+
+def row_epilogue(slices: Tensor, qs: Tensor, wscale: Tensor, bias: Tensor | None, y: Tensor, *,
+                 residual: Tensor | None = None, factor: float = 1.0, out_norm=None, norm=None,
+                 quantize_parts: int = 0, silu: bool = False, order: int = 0) -> tuple[Tensor, Tensor] | None:
+    """The exact row epilogue (kea_row_epilogue): y [M, N] FP32 rows <- [out_norm](residual + factor * value), value
+    the unsplit GEMM epilogue of the int32 slices [S, P, M, N]; with quantize_parts > 0 also returns (q, q_scales),
+    the quantize_parts-part quantization of norm(y) (of y when norm is None), as kea_quantize would."""
+    if slices.dtype != torch.int32 or slices.dim() != 4 or not slices.is_contiguous():
+        raise ValueError("slices must be contiguous int32 [S, P, M, N]")
+    split, parts, m, n = slices.shape
+    if qs.dim() != 2 or qs.shape[0] != parts or qs.shape[1] < m or qs.stride(1) != 1 or qs.dtype != torch.float32:
+        raise ValueError(f"qs must be FP32 [{parts}, >= {m}] with unit column stride")
+    if wscale.dtype not in _SCALE_DTYPES or not wscale.is_contiguous() or wscale.numel() != n:
+        raise ValueError("weight scales must be contiguous f32 or f16 [N]")
+    if bias is not None and (bias.dtype not in _SCALE_DTYPES or not bias.is_contiguous() or bias.numel() != n):
+        raise ValueError("bias must be contiguous f32 or f16 [N]")
+    if y.dtype != torch.float32 or y.dim() != 2 or y.shape[0] < m or y.shape[1] < n or y.stride(1) != 1:
+        raise ValueError(f"y must be a row-major FP32 [>= {m}, >= {n}] view")
+    if residual is not None and (residual.dtype != torch.float32 or residual.dim() != 2 or residual.shape[0] < m
+                                 or residual.shape[1] < n or residual.stride(1) != 1):
+        raise ValueError(f"residual must be a row-major FP32 [>= {m}, >= {n}] view")
+    if not 0 <= quantize_parts <= 3 or (norm is not None and quantize_parts == 0):
+        raise ValueError("quantize_parts must be 1..3 when a next LayerNorm is given (0: no quantization)")
+    device = slices.device
+    _on(device, qs, wscale, bias, y, residual)
+    ow, ob, oeps = _norm_params(out_norm, n, device)
+    nw, nb, eps = _norm_params(norm, n, device)
+    q = qsc = None
+    ldq = round_up(n, 16)
+    if quantize_parts:
+        q = torch.empty(quantize_parts, m, ldq, device=device, dtype=torch.int8)
+        qsc = torch.empty(quantize_parts, m, device=device, dtype=torch.float32)
+    rc = _hip.lib().kea_row_epilogue(
+        slices.data_ptr(), split, parts, m, n, qs.data_ptr(), qs.stride(0), wscale.data_ptr(),
+        _hip.dtype_code(wscale.dtype), _hip.ptr(bias), _hip.dtype_code(bias.dtype) if bias is not None else 0,
+        int(silu) | (2 * int(order)), _hip.ptr(residual), residual.stride(0) if residual is not None else 0,
+        float(factor), _hip.ptr(ow), _hip.ptr(ob), oeps, y.data_ptr(), y.stride(0), _hip.ptr(nw), _hip.ptr(nb), eps,
+        quantize_parts, _hip.ptr(q), ldq, _hip.ptr(qsc), _hip.stream_handle(device))
+    _hip.check(rc, "kea_row_epilogue")
+    return (q, qsc) if quantize_parts else None
+
+
 def round_up(v: int, multiple: int) -> int:
     return -(-v // multiple) * multiple
 

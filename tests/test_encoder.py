@@ -166,8 +166,12 @@ def test_norm_quantize_matches_layer_norm_and_oracle(k, rows):
     g = torch.Generator().manual_seed(k + rows)
     x = torch.randn(1, rows, k, generator=g) * 3 + 0.5
     n0, n1 = _layer_norm(k, g), _layer_norm(k, g)
-    out, q, qs = E.norm_quantize(x.cuda(), copy.deepcopy(n0).cuda(), copy.deepcopy(n1).cuda(), 3)
+    d0, d1 = copy.deepcopy(n0).cuda(), copy.deepcopy(n1).cuda()
+    out, q, qs = E.norm_quantize(x.cuda(), d0, d1, 3)
+    xi = x.cuda()
+    _, qi, qsi = E.norm_quantize(xi, d0, d1, 3, out=xi)  # in place
     torch.cuda.synchronize()
+    assert torch.equal(xi, out) and torch.equal(qi, q) and torch.equal(qsi, qs)
     ref = F.layer_norm(x.double(), (k,), n0.weight.double(), n0.bias.double(), n0.eps)
     assert float((out.cpu().double() - ref).abs().max()) < 2e-5
     ldq = q.shape[2]
