@@ -181,133 +181,201 @@ relpos_attention_kernel(const float *qkv, long long ld, const float *pos, long l
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// Matrix-core form of the same attention for T <= 128 (one workgroup = 16 query rows of one (b, h), 4 waves), on
+// Xor-butterfly max / sum of R independent values over the 64 lanes of a wave (R chains interleaved).
+template <int R>
+__device__ __forceinline__ void wave_max_n(float *v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[r] = fmaxf(v[r], __shfl_xor(v[r], off, 64));
+}
+template <int R>
+__device__ __forceinline__ void wave_sum_n(float *v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[r] = v[r] + __shfl_xor(v[r], off, 64);
+}
+
+// Matrix-core form of the same attention for T <= 128 (one workgroup = 16 query rows of one (b, h), NW waves), on
 // v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16] per step and ends with
-// D[4 (l / 16) + r][l % 16]. The head dimension is walked in the order d = 32 g + s (g = l / 16 the k lane group,
-// s = 0..31 the step), so a lane's operand values are 32 contiguous floats (8 float4 loads straight from global
-// memory); any order of the 128 terms is the same dot product up to FP32 rounding.
-//   content scores   D = (q + u) K^T                      16 x 16 key tiles, waves over key tiles
+// D[4 (l / 16) + r][l % 16]. A dot product over the head dimension takes d = 16 (s / 4) + 4 g + s % 4 at step s
+// (g = l / 16 the k lane group): a lane's operands are 8 float4 loads straight from global memory, and the 4 lanes
+// of a row read 64 contiguous bytes per load; any order of the 128 terms is the same dot product up to FP32
+// rounding.
+//   content scores   D = (q + u) K^T                      16 x 16 key tiles
 //   position scores  D = (q + v) P_band^T                  the band of 16 + KP - 1 relative rows this block needs,
 //                                                          taken back as bd[i][j] = band[i][j + 15 - i]
-//   softmax          per row in LDS (exact two-pass, keys past T masked)
-//   output           D = probs V over keys k = (KP/4) g + s, V transposed into LDS so operands are contiguous
-template <int NKT>
-__global__ void __launch_bounds__(256)
+//   softmax          per row from LDS (exact two-pass, keys past T masked); a wave reduces its 16 / NW rows together
+//   output           D^T = V^T probs^T over keys k = (KP/4) g + s: wave w owns 128 / NW head columns. With 4 waves
+//                    they are two 16-row tiles, tile c holding columns 32 w + 2 j + c, so one float2 load of a V row
+//                    per step feeds both tiles and each lane stores 8 consecutive output columns; with 8 waves one
+//                    tile of columns 16 w + j.
+// Every wave's score tiles (content tiles w, w + NW, ..., then position tiles w, w + NW, ...) run as one list whose
+// next operand loads are issued before the current tile's MFMAs; the V operands are loaded at the start and consumed
+// last. 8 waves halve a workgroup's serial MFMA work for grids too small to fill the CUs (batch 1).
+template <int NKT, int NW>
+__global__ void __launch_bounds__(NW * 64)
 relpos_attention_mfma_kernel(const float *qkv, long long ld, const float *pos, long long ldp, const float *bias_u,
                              const float *bias_v, float *out, long long ldo, int T, int H, float scale) {
-    constexpr int DK = 128, KP = 16 * NKT, NPT = NKT + 1, KS = KP / 4;
-    constexpr int SP = KP + 4, BP = 16 * NPT + 4, VP = KP + 4;  // padded LDS row strides (floats)
-    extern __shared__ __attribute__((aligned(16))) float sm[];
-    float *Sc = sm, *Bd = Sc + 16 * SP, *Vt = Bd + 16 * BP;
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    constexpr int DK = 128, KP = 16 * NKT, NPT = NKT + 1, KS = KP / 4, RPW = 16 / NW, VC = 128 / NW / 16;
+    constexpr int SP = KP + 4, BP = 16 * NPT + 4;  // padded LDS row strides (floats)
+    constexpr int NC = (NKT + NW - 1) / NW, NPOS = (NPT + NW - 1) / NW, NTASK = NC + NPOS;  // tiles per wave (max)
+    constexpr int QP = DK + 4;
+    __shared__ __attribute__((aligned(16))) float Sc[16 * SP];
+    __shared__ __attribute__((aligned(16))) float Bd[16 * BP];
+    __shared__ __attribute__((aligned(16))) float Qu[16 * QP];
+    __shared__ __attribute__((aligned(16))) float Qv[16 * QP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, g = lane >> 4;
-    const int b = blockIdx.z, h = blockIdx.y, i0 = blockIdx.x * 16;
+    // blockIdx.x is the head: consecutive workgroups go to different XCDs, so the query tiles of one head share an
+    // XCD and its L2 serves their K, V and position rows after the first fetch
+    const int b = blockIdx.z, h = blockIdx.x, i0 = blockIdx.y * 16;
     const float *qbase = qkv + (long long)b * T * ld + (long long)h * DK;
     const float *kbase = qbase + (long long)H * DK, *vbase = qbase + 2LL * H * DK;
 
-    // V transposed into LDS: Vt[d][j] = V[j][d] (zero for j >= T); consecutive threads take consecutive keys
-    for (int idx = tid; idx < KP * (DK / 4); idx += 256) {
-        const int j = idx % KP, d = (idx / KP) * 4;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (j < T) v = *(const float4 *)(vbase + (long long)j * ld + d);
-        Vt[(d + 0) * VP + j] = v.x;
-        Vt[(d + 1) * VP + j] = v.y;
-        Vt[(d + 2) * VP + j] = v.z;
-        Vt[(d + 3) * VP + j] = v.w;
-    }
-
-    // query operands with both position biases: row i0 + li, columns 32 g .. 32 g + 31
-    float qa[32], qb[32];
-    {
-        const int t = i0 + li;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (t < T) q = *(const float4 *)(qbase + (long long)t * ld + 32 * g + 4 * c);
-            const float4 u = *(const float4 *)(bias_u + h * DK + 32 * g + 4 * c);
-            const float4 v = *(const float4 *)(bias_v + h * DK + 32 * g + 4 * c);
-            qa[4 * c] = q.x + u.x; qa[4 * c + 1] = q.y + u.y; qa[4 * c + 2] = q.z + u.z; qa[4 * c + 3] = q.w + u.w;
-            qb[4 * c] = q.x + v.x; qb[4 * c + 1] = q.y + v.y; qb[4 * c + 2] = q.z + v.z; qb[4 * c + 3] = q.w + v.w;
-        }
-    }
-    // one 16 x 16 tile of dot products: rows = the 16 queries, columns = 16 rows of `src` (zero where invalid)
-    auto tile = [&](const float *q, const float *src, long long stride, int row, bool valid) {
-        float kb[32];
+    // This wave's score tiles: task i < nc is content tile wave + NW i, then position tile wave + NW (i - nc).
+    // DEPTH operand buffers: every tile's loads up front with 8 waves (at most 3 tiles a wave), one ahead with 4.
+    constexpr int DEPTH = NW == 8 ? NTASK : 2;
+    const int nc = max(NKT - wave + NW - 1, 0) / NW, npos = max(NPT - wave + NW - 1, 0) / NW;
+    const int rbase = T - 1 - (i0 + 15);  // relative row of band position 0
+    float kb[DEPTH][32];
+    auto load_task = [&](int i, float *dst) {
+        const bool content = i < nc;
+        const int tile = wave + NW * (content ? i : i - nc);
+        const int row = content ? tile * 16 + li : rbase + tile * 16 + li;
+        const bool valid = i < nc + npos && (content ? row < T : (row >= 0 && row <= 2 * T - 2));
+        const float *src = content ? kbase + (long long)row * ld : pos + (long long)row * ldp + (long long)h * DK;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (valid) v = *(const float4 *)(src + (long long)row * stride + 32 * g + 4 * c);
-            kb[4 * c] = v.x; kb[4 * c + 1] = v.y; kb[4 * c + 2] = v.z; kb[4 * c + 3] = v.w;
+            if (valid) v = *(const float4 *)(src + 16 * c + 4 * g);
+            dst[4 * c] = v.x; dst[4 * c + 1] = v.y; dst[4 * c + 2] = v.z; dst[4 * c + 3] = v.w;
         }
-        v4f acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int st = 0; st < 32; ++st) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(q[st], kb[st], acc, 0, 0, 0);
-        return acc;
     };
-    for (int kt = wave; kt < NKT; kt += 4) {
-        const int j = kt * 16 + li;
-        const v4f acc = tile(qa, kbase, ld, j, j < T);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Sc[(4 * g + r) * SP + kt * 16 + li] = acc[r];
+    for (int i = 0; i < DEPTH; ++i)
+        if (i < NTASK) load_task(i, kb[i]);
+
+    // V operands of the output phase: V[KS g + s][(128 / NW) wave + VC li .. + VC - 1] (zero for keys >= T)
+    float vr[KS][VC];
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+        const int j = KS * g + st;
+        const float *src = vbase + (long long)j * ld + (128 / NW) * wave + VC * li;
+        if constexpr (VC == 2) {
+            float2 v = make_float2(0.f, 0.f);
+            if (j < T) v = *(const float2 *)src;
+            vr[st][0] = v.x;
+            vr[st][VC - 1] = v.y;
+        } else {
+            vr[st][0] = j < T ? *src : 0.f;
+        }
     }
-    const int rbase = T - 1 - (i0 + 15);  // relative row of band position 0
-    for (int pt = wave; pt < NPT; pt += 4) {
-        const int r = rbase + pt * 16 + li;
-        const v4f acc = tile(qb, pos + (long long)h * DK, ldp, r, r >= 0 && r <= 2 * T - 2);
+
+    // The 16 query rows with both position biases are formed once per workgroup in LDS (qu, qv [16][DK + 4]; every
+    // wave reads its operands there instead of loading the rows again). Their loads go out after the wave's tile and
+    // V loads, so all of a wave's memory traffic is in flight at once.
+    for (int idx = tid; idx < 16 * (DK / 4); idx += NW * 64) {
+        const int r = idx / (DK / 4), d = (idx % (DK / 4)) * 4, t = i0 + r;
+        float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (t < T) q = *(const float4 *)(qbase + (long long)t * ld + d);
+        const float4 u = *(const float4 *)(bias_u + h * DK + d), v = *(const float4 *)(bias_v + h * DK + d);
+        *(float4 *)(Qu + r * QP + d) = make_float4(q.x + u.x, q.y + u.y, q.z + u.z, q.w + u.w);
+        *(float4 *)(Qv + r * QP + d) = make_float4(q.x + v.x, q.y + v.y, q.z + v.z, q.w + v.w);
+    }
+
+    // query operands: row li of qu / qv, columns 16 c + 4 g .. + 3 for c = 0..7
+    __syncthreads();
+    float qa[32], qb[32];
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) Bd[(4 * g + rr) * BP + pt * 16 + li] = acc[rr];
+    for (int c = 0; c < 8; ++c) {
+        const float4 a = *(const float4 *)(Qu + li * QP + 16 * c + 4 * g);
+        const float4 v = *(const float4 *)(Qv + li * QP + 16 * c + 4 * g);
+        qa[4 * c] = a.x; qa[4 * c + 1] = a.y; qa[4 * c + 2] = a.z; qa[4 * c + 3] = a.w;
+        qb[4 * c] = v.x; qb[4 * c + 1] = v.y; qb[4 * c + 2] = v.z; qb[4 * c + 3] = v.w;
+    }
+
+#pragma unroll
+    for (int i = 0; i < NTASK; ++i) {
+        if (i < nc + npos) {
+            const bool content = i < nc;
+            const int tile = wave + NW * (content ? i : i - nc);
+            v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 32; ++st)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(content ? qa[st] : qb[st], kb[i % DEPTH][st], acc, 0, 0, 0);
+            float *dst = content ? Sc + tile * 16 + li : Bd + tile * 16 + li;
+            const int stride = content ? SP : BP;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dst[(4 * g + r) * stride] = acc[r];
+        }
+        if (i + DEPTH < NTASK) load_task(i + DEPTH, kb[i % DEPTH]);  // this tile's buffer is free again
     }
     __syncthreads();
 
-    // softmax: wave w owns rows 4w .. 4w + 3; lane takes keys lane, lane + 64
-    for (int i = 4 * wave; i < 4 * wave + 4; ++i) {
-        float sv[2];
-        float mx = -INFINITY;
+    // softmax: wave w owns rows RPW w .. RPW w + RPW - 1 (reduced together); lane takes keys lane, lane + 64
+    {
+        float sv[RPW][2], mx[RPW], sum[RPW];
 #pragma unroll
-        for (int n = 0; n < 2; ++n) {
-            const int j = lane + 64 * n;
-            sv[n] = -INFINITY;
-            if (j < KP && j < T) sv[n] = (Sc[i * SP + j] + Bd[i * BP + j + 15 - i]) * scale;
-            mx = fmaxf(mx, sv[n]);
+        for (int rr = 0; rr < RPW; ++rr) {
+            const int i = RPW * wave + rr;
+            mx[rr] = -INFINITY;
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                const int j = lane + 64 * n;
+                sv[rr][n] = -INFINITY;
+                if (j < KP && j < T) sv[rr][n] = (Sc[i * SP + j] + Bd[i * BP + j + 15 - i]) * scale;
+                mx[rr] = fmaxf(mx[rr], sv[rr][n]);
+            }
         }
-        mx = wave_max(mx);
-        float sum = 0.f;
+        wave_max_n<RPW>(mx);
 #pragma unroll
-        for (int n = 0; n < 2; ++n) {
-            sv[n] = expf(sv[n] - mx);
-            sum = sum + sv[n];
+        for (int rr = 0; rr < RPW; ++rr) {
+            sum[rr] = 0.f;
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                sv[rr][n] = expf(sv[rr][n] - mx[rr]);
+                sum[rr] = sum[rr] + sv[rr][n];
+            }
         }
-        const float inv = 1.0f / wave_sum(sum);
+        wave_sum_n<RPW>(sum);
 #pragma unroll
-        for (int n = 0; n < 2; ++n) {
-            const int j = lane + 64 * n;
-            if (j < KP) Sc[i * SP + j] = sv[n] * inv;
+        for (int rr = 0; rr < RPW; ++rr) {
+            const int i = RPW * wave + rr;
+            const float inv = 1.0f / sum[rr];
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                const int j = lane + 64 * n;
+                if (j < KP) Sc[i * SP + j] = sv[rr][n] * inv;
+            }
         }
     }
     __syncthreads();
 
-    // output: wave w computes head columns 32 w .. 32 w + 31 (two 16-column tiles)
+    // output: D^T[j][q] for the wave's two column tiles; B operand = probs[q = li][KS g + s]
     float pa[KS];
 #pragma unroll
     for (int c = 0; c < KS; c += 4) {
         const float4 v = *(const float4 *)(Sc + li * SP + KS * g + c);
         pa[c] = v.x; pa[c + 1] = v.y; pa[c + 2] = v.z; pa[c + 3] = v.w;
     }
+    v4f acc[VC];
 #pragma unroll
-    for (int dt = 2 * wave; dt < 2 * wave + 2; ++dt) {
-        v4f acc = {0.f, 0.f, 0.f, 0.f};
-        const float *vrow = Vt + (dt * 16 + li) * VP + KS * g;
+    for (int c = 0; c < VC; ++c) acc[c] = (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < KS; c += 4) {
-            const float4 v = *(const float4 *)(vrow + c);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[c], v.x, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[c + 1], v.y, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[c + 2], v.z, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[c + 3], v.w, acc, 0, 0, 0);
-        }
+    for (int st = 0; st < KS; ++st)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = i0 + 4 * g + r;
-            if (t < T) out[((long long)b * T + t) * ldo + (long long)h * DK + dt * 16 + li] = acc[r];
+        for (int c = 0; c < VC; ++c) acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[st][c], pa[st], acc[c], 0, 0, 0);
+    // lane holds rows j = 4 g + r for query q = li: column (128 / NW) w + VC (4 g + r) + c
+    const int t = i0 + li;
+    if (t < T) {
+        float *o = out + ((long long)b * T + t) * ldo + (long long)h * DK + (128 / NW) * wave + 4 * VC * g;
+        if constexpr (VC == 2) {
+            *(float4 *)o = make_float4(acc[0][0], acc[VC - 1][0], acc[0][1], acc[VC - 1][1]);
+            *(float4 *)(o + 4) = make_float4(acc[0][2], acc[VC - 1][2], acc[0][3], acc[VC - 1][3]);
+        } else {
+            *(float4 *)o = make_float4(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
         }
     }
 }
@@ -349,27 +417,26 @@ int kea_relpos_attention(const float *qkv, int64_t ld, const float *pos, int64_t
         (ld | ldp | ldo) & 3)
         return kea::fail(KEA_EALIGN, "qkv, pos, out and the biases need 16-byte aligned rows");
     if (t <= 128) {
-        const int nkt = (int)((t + 15) / 16), kp = 16 * nkt;
-        const size_t lds = sizeof(float) * (size_t)(16 * (kp + 4) + 16 * (16 * (nkt + 1) + 4) + head_dim * (kp + 4));
-        const dim3 grid((unsigned)((t + 15) / 16), (unsigned)heads, (unsigned)batch);
+        const int nkt = (int)((t + 15) / 16);
+        const dim3 grid((unsigned)heads, (unsigned)((t + 15) / 16), (unsigned)batch);
         void (*fn)(const float *, long long, const float *, long long, const float *, const float *, float *,
                    long long, int, int, float) = nullptr;
+        // 8 waves per workgroup when the grid leaves CUs idle (fewer workgroups than the 256 CUs)
+        const bool wide = (long long)grid.x * grid.y * grid.z < 256;
+#define KEA_ATT(N) fn = wide ? relpos_attention_mfma_kernel<N, 8> : relpos_attention_mfma_kernel<N, 4>
         switch (nkt) {
-            case 1: fn = relpos_attention_mfma_kernel<1>; break;
-            case 2: fn = relpos_attention_mfma_kernel<2>; break;
-            case 3: fn = relpos_attention_mfma_kernel<3>; break;
-            case 4: fn = relpos_attention_mfma_kernel<4>; break;
-            case 5: fn = relpos_attention_mfma_kernel<5>; break;
-            case 6: fn = relpos_attention_mfma_kernel<6>; break;
-            case 7: fn = relpos_attention_mfma_kernel<7>; break;
-            default: fn = relpos_attention_mfma_kernel<8>; break;
+            case 1: KEA_ATT(1); break;
+            case 2: KEA_ATT(2); break;
+            case 3: KEA_ATT(3); break;
+            case 4: KEA_ATT(4); break;
+            case 5: KEA_ATT(5); break;
+            case 6: KEA_ATT(6); break;
+            case 7: KEA_ATT(7); break;
+            default: KEA_ATT(8); break;
         }
-        if (lds > 65536) {
-            hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return kea::fail((int)e, std::string("LDS attribute refused: ") + hipGetErrorString(e));
-        }
-        hipLaunchKernelGGL(fn, grid, dim3(256), lds, (hipStream_t)stream, qkv, (long long)ld, pos, (long long)ldp,
-                           bias_u, bias_v, out, (long long)ldo, (int)t, heads, scale);
+#undef KEA_ATT
+        hipLaunchKernelGGL(fn, grid, dim3(wide ? 512 : 256), 0, (hipStream_t)stream, qkv, (long long)ld, pos,
+                           (long long)ldp, bias_u, bias_v, out, (long long)ldo, (int)t, heads, scale);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return kea::fail((int)e, std::string("attention launch failed: ") + hipGetErrorString(e));
         return KEA_OK;

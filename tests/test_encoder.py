@@ -102,7 +102,7 @@ def test_encoder_graph_replays_equal_eager():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("b,t", [(1, 125), (2, 37), (1, 256), (3, 1)])
+@pytest.mark.parametrize("b,t", [(1, 125), (2, 37), (1, 256), (3, 1), (8, 100), (5, 128), (4, 200)])
 @torch.inference_mode()
 def test_fused_relpos_attention_matches_fp64(b, t):
     """The fused kernel against the same formula in FP64 (rel_shift form); FP32 accumulation over 128-dim dot
