@@ -55,6 +55,15 @@ int kea_glu_dwconv_quantize(const float *x_dev, int64_t ldx, const float *w_dev,
                             int64_t batch, int64_t t, int64_t channels, int kernel, int parts, int8_t *q_dev,
                             int64_t ldq, float *qs_dev, void *stream);
 
+/* kea_glu_dwconv_quantize on GLU values already formed (u [batch*t][ldu], channels columns, rows 16-byte aligned):
+ * the depthwise convolution, SiLU and quantization only. The GLU comes from the producing projection's epilogue
+ * (kea_lowbit_gemm with KEA_FLAG_GLU and interleaved value / gate weight rows), which computes it with the same
+ * formula, so the result is bitwise kea_glu_dwconv_quantize's. The reference's _glu_pad + depthwise Conv1d +
+ * quantization of the next projection (kk/ternary/layer_fusions4.py:9-30, :62-72). */
+int kea_dwconv_quantize(const float *u_dev, int64_t ldu, const float *w_dev, const float *bias_dev, int64_t batch,
+                        int64_t t, int64_t channels, int kernel, int parts, int8_t *q_dev, int64_t ldq, float *qs_dev,
+                        void *stream);
+
 #ifdef __cplusplus
 }
 #endif

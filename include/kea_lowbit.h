@@ -51,6 +51,7 @@ extern "C" {
 /* epilogue flags */
 #define KEA_FLAG_SILU 1     /* y = y * sigmoid(y) after scale and bias */
 #define KEA_FLAG_ORDER 2    /* P = 2 / 3: first FP32 contraction fma(a1, s1, a0 * s0) instead of fma(a0, s0, a1 * s1) */
+#define KEA_FLAG_GLU 4      /* kea_lowbit_gemm only: column pairs (2j, 2j + 1) -> y[j] = r[2j] * sigmoid(r[2j + 1]) */
 
 /* ---------------------------------------------------------------------------------------------------------
  * Weight layouts
@@ -179,6 +180,12 @@ int kea_row_epilogue(const int32_t *slices_dev, int split, int parts, int64_t m,
                      float *y_dev, int64_t ldy,
                      const float *norm_w_dev, const float *norm_b_dev, float eps,
                      int q_parts, int8_t *q_dev, int64_t ldq, float *q_scales_dev, void *stream);
+
+/* GLU pairs (flags & KEA_FLAG_GLU; kea_lowbit_gemm and kea_lowbit_gemm_residual without a residual; per-channel
+ * scales, no SiLU, n even): after scale and bias, y[m*ldy + j] = RN(r[2j] * (1 / (1 + exp(-r[2j+1])))) for
+ * j < n/2, ldy >= n/2; acc_out still receives all n accumulators. A GLU whose value / gate halves are separate row
+ * blocks (NeMo's conv module, GLU over [value; gate]) runs with the weight rows interleaved value, gate, value, ...
+ * (scale and bias rows alike). Replaces the GLU of the reference's _glu_pad (kk/ternary/layer_fusions4.py:9-22). */
 
 /* Workspace bytes kea_lowbit_gemm needs for these arguments (0 when split_k resolves to 1). */
 int64_t kea_lowbit_gemm_workspace(int wbits, int parts, int64_t m, int64_t n, int64_t k, int64_t ws_group,

@@ -128,6 +128,30 @@ __device__ __forceinline__ void store4(const Params &p, long long off, int nb, c
     }
 }
 
+// GLU pairs: u[0..1] = y[row][cb], y[row][cb + 1] (cb = nb / 2; the second only when nb + 3 < N).
+__device__ __forceinline__ void store2(const Params &p, long long off, int nb, const float *u) {
+    const bool full = p.y_vec && nb + 3 < p.N;
+    if (p.y_dtype == KEA_F32) {
+        float *y = (float *)p.y + off;
+        if (full) {
+            *(float2 *)y = make_float2(u[0], u[1]);
+        } else {
+            y[0] = u[0];
+            if (nb + 3 < p.N) y[1] = u[1];
+        }
+    } else {
+        uint16_t h[2];
+        for (int r = 0; r < 2; ++r) h[r] = p.y_dtype == KEA_F16 ? to_f16_bits(u[r]) : to_bf16_bits(u[r]);
+        uint16_t *y = (uint16_t *)p.y + off;
+        if (full) {
+            *(uint32_t *)y = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+        } else {
+            y[0] = h[0];
+            if (nb + 3 < p.N) y[1] = h[1];
+        }
+    }
+}
+
 __device__ __forceinline__ void store_int4(int32_t *dst, bool vec, int nb, int N, const int *v) {
     if (vec && nb + 3 < N) {
         *(int4 *)dst = make_int4(v[0], v[1], v[2], v[3]);
@@ -187,7 +211,12 @@ __device__ __forceinline__ void epilogue4(const Params &p, int m, int nb, const 
             v[r] = finish(combine<P>(ar, e.s, p.flags), e.alpha[r], p.bias != nullptr, e.bias[r], p.flags);
             if (p.res) v[r] = e.res[r] + v[r] * p.res_factor;
         }
-        store4(p, (long long)m * p.ldy + nb, nb, v);
+        if (p.flags & KEA_FLAG_GLU) {  // column pairs (value, gate): value * sigmoid(gate)
+            const float u[2] = {v[0] * (1.0f / (1.0f + expf(-v[1]))), v[2] * (1.0f / (1.0f + expf(-v[3])))};
+            store2(p, (long long)m * p.ldy + nb / 2, nb, u);
+        } else {
+            store4(p, (long long)m * p.ldy + nb, nb, v);
+        }
     }
     if (p.acc) {
 #pragma unroll
@@ -240,10 +269,13 @@ constexpr int kLdsBudget = 160 * 1024;
 #endif
 constexpr int kMaxStages = KEA_MAX_STAGES;
 
+#ifndef KEA_STAGE_K
+#define KEA_STAGE_K 256
+#endif
 __host__ __device__ constexpr StageShape stage_shape(int wbits, int parts, int rm, int rn, int wm, int wn) {
     const int nw = wm * wn, bm = wm * rm * 16, bn = wn * rn * 16;
-    const int sw = wbits == 1 ? 2 : 4;
-    const int a_units = parts * bm * 16;
+    const int sw = KEA_STAGE_K / (wbits == 1 ? 128 : 64);
+    const int a_units = parts * bm * (KEA_STAGE_K / 16);
     const int b_words = (bn / 16) * sw;
     const int stage = a_units * 16 + b_words * 256;
     const int copies = a_units / 64 / nw + b_words / nw;
@@ -323,6 +355,7 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     static_assert(L * (NS - 1) < 64, "in-flight copies exceed the vmcnt range");
     static_assert(L == SHAPE.copies && STAGE_BYTES == SHAPE.stage_bytes, "host and device stage geometry differ");
     static_assert(NS >= 2, "at least double buffering");
+    static_assert(NS * STAGE_BYTES <= kLdsBudget, "the ring exceeds the LDS a workgroup may allocate");
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];  // NS * STAGE_BYTES
 
     // the wavefront index is uniform; readfirstlane tells the compiler so (wave-derived math then runs on SALU)
@@ -724,8 +757,12 @@ constexpr Tile kTiles[] = {
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
-// Register budget of a tile: accumulators plus double-buffered activation fragments (in 32-bit registers).
-constexpr bool tile_fits(int parts, int rm, int rn) { return parts * rm * rn * 4 + 2 * parts * rm * 4 <= 256; }
+// Register budget of a tile: accumulators plus double-buffered activation fragments (in 32-bit registers); and two
+// ring buffers of the tile's stage within the LDS a workgroup may allocate.
+constexpr bool tile_fits(int wbits, int parts, int rm, int rn, int wm, int wn) {
+    return parts * rm * rn * 4 + 2 * parts * rm * 4 <= 256 &&
+           2 * stage_shape(wbits, parts, rm, rn, wm, wn).stage_bytes <= kLdsBudget;
+}
 
 inline long long cdivl(long long a, long long b) { return (a + b - 1) / b; }
 
@@ -739,7 +776,7 @@ KernelFn pick_sliced(bool sliced) {
 
 template <int WBITS, int P, int RM, int RN, int WM, int WN>
 KernelFn pick_fit(bool sliced) {
-    if constexpr (tile_fits(P, RM, RN)) return pick_sliced<WBITS, P, RM, RN, WM, WN>(sliced);
+    if constexpr (tile_fits(WBITS, P, RM, RN, WM, WN)) return pick_sliced<WBITS, P, RM, RN, WM, WN>(sliced);
     else return nullptr;
 }
 
@@ -858,7 +895,8 @@ static int resolve(int wbits, int parts, int64_t m, int64_t n, int64_t k, int sp
     if (config < 0 || config > kNumTiles) return kea::fail(KEA_EINVAL, "unknown config id");
     if (split_k < 0) return kea::fail(KEA_EINVAL, "split_k must be >= 0");
     int id = config ? config : choose_tile(wbits, parts, m, n, k);
-    if (!tile_fits(parts, kTiles[id - 1].rm, kTiles[id - 1].rn))
+    const Tile &tl = kTiles[id - 1];
+    if (!tile_fits(wbits, parts, tl.rm, tl.rn, tl.wm, tl.wn))
         return kea::fail(KEA_EINVAL, std::string("tile ") + kTiles[id - 1].name + " does not fit " +
                                          std::to_string(parts) + " activation parts");
     const long long J = wbits == 1 ? cdivl(k, 128) : cdivl(k, 64);
@@ -918,7 +956,10 @@ static int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ld
     }
     int rc = resolve(wbits, parts, m, n, k, split_k, config, &tile, &s, &qps);
     if (rc != KEA_OK) return rc;
-    if (flags & ~(KEA_FLAG_SILU | KEA_FLAG_ORDER)) return kea::fail(KEA_EINVAL, "unknown flags");
+    if (flags & ~(KEA_FLAG_SILU | KEA_FLAG_ORDER | KEA_FLAG_GLU)) return kea::fail(KEA_EINVAL, "unknown flags");
+    const bool glu = (flags & KEA_FLAG_GLU) != 0;
+    if (glu && ((flags & KEA_FLAG_SILU) || ws_group || residual || (n & 1)))
+        return kea::fail(KEA_EINVAL, "GLU pairs need an even n, per-channel scales, no SiLU and no residual");
     if (m > 0 && (!w || !qs || !wscale)) return kea::fail(KEA_EINVAL, "q, qs, w and wscale are required");
     if (m > 0 && !y && !acc_out) return kea::fail(KEA_EINVAL, "nothing to write: y and acc_out are both NULL");
     if (qs_dtype != KEA_F32 && qs_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "qs dtype must be f32 or f16");
@@ -926,7 +967,7 @@ static int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ld
     if (bias && bias_dtype != KEA_F32 && bias_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "bias dtype must be f32 or f16");
     if (y && y_dtype != KEA_F32 && y_dtype != KEA_F16 && y_dtype != KEA_BF16)
         return kea::fail(KEA_EINVAL, "y dtype must be f32, f16 or bf16");
-    if (y && ldy < n) return kea::fail(KEA_EINVAL, "ldy < n");
+    if (y && ldy < (glu ? n / 2 : n)) return kea::fail(KEA_EINVAL, glu ? "ldy < n / 2" : "ldy < n");
     if (acc_out && acc_ld < n) return kea::fail(KEA_EINVAL, "acc_ld < n");
     if (residual && !y) return kea::fail(KEA_EINVAL, "a residual needs y");
     if (residual && ldr < n) return kea::fail(KEA_EINVAL, "ldr < n");
@@ -954,7 +995,8 @@ static int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ld
     p.quads_per_slice = qps;
     p.flags = flags;
     const int esz = (y_dtype == KEA_F32) ? 4 : 2;
-    p.y_vec = y && (ldy % 4 == 0) && ((uintptr_t)y % (4 * esz) == 0);
+    const int yv = glu ? 2 : 4;  // elements per vector store
+    p.y_vec = y && (ldy % yv == 0) && ((uintptr_t)y % (yv * esz) == 0);
     p.acc_vec = acc_out && (acc_ld % 4 == 0) && ((uintptr_t)acc_out % 16 == 0);
 
     const Tile &t = kTiles[tile - 1];
@@ -962,13 +1004,12 @@ static int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ld
     // Ring buffers actually used: a workgroup touches buffer s % NS for its stages s < nst, so with nst < NS only
     // the first nst buffers need LDS.
     const long long words_per_wg = std::min<long long>(4LL * qps, (long long)p.J);
-    const int sw = wbits == 1 ? 2 : 4;
-    const int nst = (int)cdivl(words_per_wg, sw);
     const StageShape shape = stage_shape(wbits, parts, t.rm, t.rn, t.wm, t.wn);
+    const int nst = (int)cdivl(words_per_wg, shape.sw);
     int lds_bytes = std::min(shape.ns, nst) * shape.stage_bytes;
     if (gq) {
-        // alpha block: the groups the stages span (4 k-steps of 64 per stage), padded to a power of two
-        const int spanned = nst * 4 / gq;
+        // alpha block: the groups the stages span (KEA_STAGE_K / 64 k-steps per stage), padded to a power of two
+        const int spanned = nst * (KEA_STAGE_K / 64) / gq;
         int shift = 0;
         while ((1 << shift) < spanned) ++shift;
         p.groups = (int)cdivl(k, ws_group);
@@ -1060,8 +1101,8 @@ int kea_lowbit_gemm_slices(int wbits, const int8_t *q, int64_t part_stride, int6
     const Tile &t = kTiles[tile - 1];
     const int bm = t.wm * t.rm * 16, bn = t.wn * t.rn * 16;
     const long long words_per_wg = std::min<long long>(4LL * qps, (long long)p.J);
-    const int nst = (int)cdivl(words_per_wg, wbits == 1 ? 2 : 4);
     const StageShape shape = stage_shape(wbits, parts, t.rm, t.rn, t.wm, t.wn);
+    const int nst = (int)cdivl(words_per_wg, shape.sw);
     const int lds_bytes = std::min(shape.ns, nst) * shape.stage_bytes;
     KernelFn fn = pick_kernel(wbits, parts, tile, true, false);
     if (lds_bytes > 65536) {

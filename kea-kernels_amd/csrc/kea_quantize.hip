@@ -283,7 +283,9 @@ norm_quantize_kernel(const float *x, long long ldx, int M, int K, const float *w
 // workgroup (4 waves) per token row; thread th holds the channel chunks 4 * (th + 256 i) .. + 3 (C % 4 == 0).
 // KW > 0: compile-time kernel width; every tap's loads are issued before the arithmetic (rows clamped into [0, T) so
 // each address is in bounds; taps outside the sequence are then skipped, exactly as in the runtime-width loop).
-template <int VPT, int KW>
+// GLU = false: x already holds the GLU values (C columns; the GLU ran in the producing GEMM's epilogue with the same
+// formula), so the convolution reads them directly.
+template <int VPT, int KW, bool GLU>
 __global__ void __launch_bounds__(256)
 glu_dwconv_quantize_kernel(const float *x, long long ldx, const float *w, const float *bias, int T, int C, int kw_rt,
                            int parts, int8_t *q, long long ldq, float *qs) {
@@ -303,12 +305,12 @@ glu_dwconv_quantize_kernel(const float *x, long long ldx, const float *w, const 
             }
             if constexpr (KW > 0) {
                 constexpr int half = KW / 2;
-                float4 a[KW], g[KW];
+                float4 a[KW], g[GLU ? KW : 1];
 #pragma unroll
                 for (int j = 0; j < KW; ++j) {
                     const int tt = min(max(t + j - half, 0), T - 1);
                     a[j] = *(const float4 *)(xb + (long long)tt * ldx + c0);
-                    g[j] = *(const float4 *)(xb + (long long)tt * ldx + C + c0);
+                    if constexpr (GLU) g[j] = *(const float4 *)(xb + (long long)tt * ldx + C + c0);
                 }
                 float4 wv[KW];   // w[(c0 + e) * KW + j]: the 4 channels' taps are 4 * KW consecutive floats
                 const float *wc = w + (long long)c0 * KW;
@@ -319,11 +321,17 @@ glu_dwconv_quantize_kernel(const float *x, long long ldx, const float *w, const 
 #pragma unroll
                 for (int j = 0; j < KW; ++j) {
                     if (t + j - half < 0 || t + j - half >= T) continue;
-                    const float av[4] = {a[j].x, a[j].y, a[j].z, a[j].w}, gv[4] = {g[j].x, g[j].y, g[j].z, g[j].w};
+                    const float av[4] = {a[j].x, a[j].y, a[j].z, a[j].w};
                     const float ww[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+                    if constexpr (GLU) {
+                        const float gv[4] = {g[j].x, g[j].y, g[j].z, g[j].w};
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        acc[e] = __builtin_fmaf(ww[e], av[e] * (1.0f / (1.0f + expf(-gv[e]))), acc[e]);
+                        for (int e = 0; e < 4; ++e)
+                            acc[e] = __builtin_fmaf(ww[e], av[e] * (1.0f / (1.0f + expf(-gv[e]))), acc[e]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(ww[e], av[e], acc[e]);
+                    }
                 }
             } else {
                 const int half = kw_rt / 2;
@@ -331,12 +339,19 @@ glu_dwconv_quantize_kernel(const float *x, long long ldx, const float *w, const 
                     const int tt = t + j - half;
                     if (tt < 0 || tt >= T) continue;
                     const float *row = xb + (long long)tt * ldx;
-                    const float4 a = *(const float4 *)(row + c0), g = *(const float4 *)(row + C + c0);
-                    const float av[4] = {a.x, a.y, a.z, a.w}, gv[4] = {g.x, g.y, g.z, g.w};
+                    const float4 a = *(const float4 *)(row + c0);
+                    const float av[4] = {a.x, a.y, a.z, a.w};
+                    if constexpr (GLU) {
+                        const float4 g = *(const float4 *)(row + C + c0);
+                        const float gv[4] = {g.x, g.y, g.z, g.w};
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        acc[e] = __builtin_fmaf(w[(c0 + e) * kw_rt + j], av[e] * (1.0f / (1.0f + expf(-gv[e]))),
-                                                acc[e]);
+                        for (int e = 0; e < 4; ++e)
+                            acc[e] = __builtin_fmaf(w[(c0 + e) * kw_rt + j], av[e] * (1.0f / (1.0f + expf(-gv[e]))),
+                                                    acc[e]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(w[(c0 + e) * kw_rt + j], av[e], acc[e]);
+                    }
                 }
             }
         }
@@ -521,14 +536,14 @@ extern "C" int kea_norm_quantize(const float *x, int64_t ldx, int64_t m, int64_t
     return KEA_OK;
 }
 
-extern "C" int kea_glu_dwconv_quantize(const float *x, int64_t ldx, const float *w, const float *bias, int64_t batch,
-                                       int64_t t, int64_t channels, int kernel, int parts, int8_t *q, int64_t ldq,
-                                       float *qs, void *stream) {
+static int dwconv_quantize(bool glu, const float *x, int64_t ldx, const float *w, const float *bias, int64_t batch,
+                           int64_t t, int64_t channels, int kernel, int parts, int8_t *q, int64_t ldq, float *qs,
+                           void *stream) {
     if (parts < 1 || parts > 3) return kea::fail(KEA_EINVAL, "parts must be 1, 2 or 3");
     if (batch < 0 || t < 0 || batch > 65535 || t > INT32_MAX || channels < 4 || channels > 2048 || channels % 4 ||
         kernel < 1 || kernel % 2 == 0)
         return kea::fail(KEA_EINVAL, "bad sizes (channels in 4..2048, a multiple of 4; odd kernel width)");
-    if (ldx < 2 * channels || ldq < channels) return kea::fail(KEA_EINVAL, "leading dimension too small");
+    if (ldx < (glu ? 2 : 1) * channels || ldq < channels) return kea::fail(KEA_EINVAL, "leading dimension too small");
     if (batch == 0 || t == 0) return KEA_OK;
     if (!x || !w || !q || !qs) return kea::fail(KEA_EINVAL, "null pointer");
     if (((uintptr_t)x | (uintptr_t)bias) & 15 || ldx & 3 || ((uintptr_t)q | (uintptr_t)ldq) & 3)
@@ -536,20 +551,38 @@ extern "C" int kea_glu_dwconv_quantize(const float *x, int64_t ldx, const float 
     const int vpt = (int)((channels + 1023) / 1024);
     const dim3 grid((unsigned)t, (unsigned)batch), block(256);
     hipStream_t st = (hipStream_t)stream;
-#define KEA_GQ(V, W)                                                                                             \
-    hipLaunchKernelGGL((glu_dwconv_quantize_kernel<V, W>), grid, block, 0, st, x, (long long)ldx, w, bias, (int)t, \
-                       (int)channels, kernel, parts, q, (long long)ldq, qs)
-    if (kernel == 9) {
-        if (vpt <= 1) KEA_GQ(1, 9);
-        else KEA_GQ(2, 9);
+#define KEA_GQ(V, W, G)                                                                                          \
+    hipLaunchKernelGGL((glu_dwconv_quantize_kernel<V, W, G>), grid, block, 0, st, x, (long long)ldx, w, bias,    \
+                       (int)t, (int)channels, kernel, parts, q, (long long)ldq, qs)
+#define KEA_GQ_V(W, G)                 \
+    do {                               \
+        if (vpt <= 1) KEA_GQ(1, W, G); \
+        else KEA_GQ(2, W, G);          \
+    } while (0)
+    if (glu) {
+        if (kernel == 9) KEA_GQ_V(9, true);
+        else KEA_GQ_V(0, true);
     } else {
-        if (vpt <= 1) KEA_GQ(1, 0);
-        else KEA_GQ(2, 0);
+        if (kernel == 9) KEA_GQ_V(9, false);
+        else KEA_GQ_V(0, false);
     }
+#undef KEA_GQ_V
 #undef KEA_GQ
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return kea::fail((int)e, std::string("glu_dwconv_quantize launch failed: ") + hipGetErrorString(e));
+    if (e != hipSuccess) return kea::fail((int)e, std::string("dwconv_quantize launch failed: ") + hipGetErrorString(e));
     return KEA_OK;
+}
+
+extern "C" int kea_glu_dwconv_quantize(const float *x, int64_t ldx, const float *w, const float *bias, int64_t batch,
+                                       int64_t t, int64_t channels, int kernel, int parts, int8_t *q, int64_t ldq,
+                                       float *qs, void *stream) {
+    return dwconv_quantize(true, x, ldx, w, bias, batch, t, channels, kernel, parts, q, ldq, qs, stream);
+}
+
+extern "C" int kea_dwconv_quantize(const float *u, int64_t ldu, const float *w, const float *bias, int64_t batch,
+                                   int64_t t, int64_t channels, int kernel, int parts, int8_t *q, int64_t ldq,
+                                   float *qs, void *stream) {
+    return dwconv_quantize(false, u, ldu, w, bias, batch, t, channels, kernel, parts, q, ldq, qs, stream);
 }
 
 extern "C" int kea_row_epilogue(const int32_t *slices, int split, int parts, int64_t m, int64_t n, const float *qs,

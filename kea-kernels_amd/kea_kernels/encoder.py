@@ -267,6 +267,30 @@ def glu_dwconv_quantize(x: Tensor, weight: Tensor, bias: Tensor | None, parts: i
     return q, qs
 
 
+def dwconv_quantize(u: Tensor, weight: Tensor, bias: Tensor | None, parts: int) -> tuple[Tensor, Tensor]:
+    """u [B, T, C] GLU values (rows contiguous) -> the P-part quantization (q, qs) of silu(depthwise_conv(u))
+    (kea_dwconv_quantize)."""
+    b, t, c = u.shape
+    kw = weight.shape[-1]
+    if u.stride(2) != 1 or u.stride(0) != t * u.stride(1) or not weight.is_contiguous():
+        raise ValueError("u needs contiguous rows and a contiguous weight")
+    ldq = lowbit.round_up(c, 16)
+    q = torch.empty(parts, b * t, ldq, device=u.device, dtype=torch.int8)
+    qs = torch.empty(parts, b * t, device=u.device, dtype=torch.float32)
+    rc = _hip.lib().kea_dwconv_quantize(u.data_ptr(), u.stride(1), weight.data_ptr(), _hip.ptr(bias), b, t, c, kw,
+                                        parts, q.data_ptr(), ldq, qs.data_ptr(), _hip.stream_handle(u.device))
+    _hip.check(rc, "kea_dwconv_quantize")
+    return q, qs
+
+
+def glu_interleave(rows: Tensor) -> Tensor:
+    """Rows [2C, ...] of a GLU input projection (value half, then gate half) -> value, gate, value, ... order, the
+    pair layout of the GEMM's GLU epilogue."""
+    c = rows.shape[0] // 2
+    idx = torch.stack([torch.arange(c), torch.arange(c) + c], 1).reshape(-1)
+    return rows[idx.to(rows.device)].contiguous()
+
+
 # --- the encoder -----------------------------------------------------------------------------------------------------
 
 class _DenseLinear:
@@ -330,8 +354,10 @@ class FastConformerEncoder:
             fp["dw_b"] = dev(weights[pre + "conv.batch_norm.bias"] - weights[pre + "conv.batch_norm.running_mean"] * gain)
             self.layers.append(fp)
             for suffix, (n, k, kind) in shapes.items():
-                quantized[pre + suffix] = (weights[pre + suffix + ".codes"], weights[pre + suffix + ".scale"], None,
-                                           kind, k)
+                codes, scale = weights[pre + suffix + ".codes"], weights[pre + suffix + ".scale"]
+                if self.fused and suffix == "conv.pointwise_conv1":  # value / gate row pairs for the GLU epilogue
+                    codes, scale = glu_interleave(codes), glu_interleave(scale)
+                quantized[pre + suffix] = (codes, scale, None, kind, k)
         if dense:
             self.linears = {name: _DenseLinear(codes, scale, k, device)
                             for name, (codes, scale, _, _, k) in quantized.items()}
@@ -386,12 +412,13 @@ class FastConformerEncoder:
             raise ValueError(f"{name} does not cover a whole prepared layer")
         return entry.layer
 
-    def _gemm(self, name: str, q: Tensor, qs: Tensor, m: int, *, silu: bool = False) -> Tensor:
-        """The quantized linear `name` on pre-quantized activations (q, qs): FP32 [m, N]."""
+    def _gemm(self, name: str, q: Tensor, qs: Tensor, m: int, *, silu: bool = False, glu: bool = False) -> Tensor:
+        """The quantized linear `name` on pre-quantized activations (q, qs): FP32 [m, N] (glu: [m, N/2])."""
         layer = self._layer(name)
-        y = torch.empty(m, layer.out_features, device=self.device, dtype=torch.float32)
-        lowbit.gemm(layer.WBITS, q, qs, layer.words, layer.out_features, layer.in_features, layer.scale, layer.bias,
-                    y, None, silu=silu)
+        n = layer.out_features
+        y = torch.empty(m, n // 2 if glu else n, device=self.device, dtype=torch.float32)
+        lowbit.gemm(layer.WBITS, q, qs, layer.words, n, layer.in_features, layer.scale, layer.bias, y, None,
+                    silu=silu, glu=glu)
         return y
 
     def weight_bytes(self) -> int:
@@ -498,8 +525,8 @@ class FastConformerEncoder:
         qkv = self._gemm(pre + "self_attn.qkv", *xq, m).view(b, t, -1)
         att = self.attention(qkv, pos, fp["u"], fp["v"])
         xq = self._block(pre + "self_attn.linear_out", *self._quantize(att), x, 1.0, norm=fp["norm_conv"])
-        z = self._gemm(pre + "conv.pointwise_conv1", *xq, m).view(b, t, -1)
-        xq = self._block(pre + "conv.pointwise_conv2", *glu_dwconv_quantize(z, fp["dw_w"], fp["dw_b"], self.parts),
+        u = self._gemm(pre + "conv.pointwise_conv1", *xq, m, glu=True).view(b, t, -1)   # GLU in the epilogue
+        xq = self._block(pre + "conv.pointwise_conv2", *dwconv_quantize(u, fp["dw_w"], fp["dw_b"], self.parts),
                          x, 1.0, norm=fp["norm_feed_forward2"])
         y = self._gemm(pre + "feed_forward2.linear1", *xq, m, silu=True)
         following = self.layers[i + 1]["norm_feed_forward1"] if i + 1 < self.cfg.layers else None

@@ -24,10 +24,11 @@ def _on(device: torch.device, *tensors: Tensor | None) -> None:
 def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscale: Tensor, bias: Tensor | None,
          y: Tensor | None = None, acc_out: Tensor | None = None, *, m: int | None = None, silu: bool = False,
          order: int = 0, config=None, ws_group: int = 0, residual: Tensor | None = None,
-         residual_factor: float = 1.0) -> None:
+         residual_factor: float = 1.0, glu: bool = False) -> None:
     """y[:m] (rows of stride y.stride(0)) and/or acc_out [P, m, N] from q int8 [P, M, ldq] (16-byte aligned rows) and
     qs [P, M] (f32 or f16). words: native layout of `wbits`-bit weights; wscale [N] (or [N, G] with ws_group).
-    residual (FP32 [>= m, >= N] rows, may be y itself): y = residual + value * residual_factor."""
+    residual (FP32 [>= m, >= N] rows, may be y itself): y = residual + value * residual_factor.
+    glu: y [m, N/2] = value[2j] * sigmoid(value[2j + 1]) (weight rows interleaved value, gate)."""
     if q.dtype != torch.int8 or q.dim() != 3:
         raise ValueError(f"q must be int8 [P, M, ldq], got {q.dtype} {tuple(q.shape)}")
     parts, rows, ldq = q.shape
@@ -44,8 +45,9 @@ def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscal
         raise ValueError("bias must be contiguous f32 or f16 [N]")
     if y is None and acc_out is None:
         raise ValueError("nothing to compute: y and acc_out are both None")
-    if y is not None and (y.dim() != 2 or y.shape[0] < m or y.shape[1] < n or y.stride(1) != 1):
-        raise ValueError(f"y must be a row-major [>= {m}, >= {n}] view")
+    ny = n // 2 if glu else n
+    if y is not None and (y.dim() != 2 or y.shape[0] < m or y.shape[1] < ny or y.stride(1) != 1):
+        raise ValueError(f"y must be a row-major [>= {m}, >= {ny}] view")
     if acc_out is not None and (acc_out.dtype != torch.int32 or acc_out.dim() != 3 or acc_out.shape[0] != parts
                                 or acc_out.shape[1] != m or acc_out.shape[2] < n or acc_out.stride(2) != 1
                                 or acc_out.stride(0) != m * acc_out.stride(1)):
@@ -73,7 +75,7 @@ def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscal
             _hip.ptr(bias), _hip.dtype_code(bias.dtype) if bias is not None else 0,
             _hip.ptr(y), _hip.dtype_code(y.dtype) if y is not None else 0, y.stride(0) if y is not None else 0,
             _hip.ptr(acc_out), acc_out.stride(1) if acc_out is not None else 0,
-            m, int(silu) | (2 * int(order)), split, tile,
+            m, int(silu) | (2 * int(order)) | (4 * int(glu)), split, tile,
             _hip.ptr(workspace), need)
     if residual is None:
         _hip.check(L.kea_lowbit_gemm(*args, _hip.stream_handle(device)), "kea_lowbit_gemm")

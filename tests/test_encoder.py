@@ -203,3 +203,59 @@ def test_glu_dwconv_quantize_equals_the_two_kernel_path(b, t, c):
     ref = conv * torch.sigmoid(conv)
     deq = sum(q[i, :, :c].cpu().double() * qs[i].cpu().double()[:, None] for i in range(3))
     assert bool(((deq - ref).abs() <= 0.5 * qs[2].cpu().double()[:, None] + 2e-6 * ref.abs().amax(1, keepdim=True)).all())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("split,out_dtype", [(1, torch.float32), (2, torch.float32), (1, torch.float16)])
+@torch.inference_mode()
+def test_gemm_glu_pairs_feed_the_convolution_bitwise(split, out_dtype):
+    """The GEMM's GLU epilogue on interleaved (value, gate) weight rows + kea_dwconv_quantize equals the plain GEMM +
+    kea_glu_dwconv_quantize bit for bit; the GLU values match value * sigmoid(gate) of the plain output."""
+    from oracle import oracle as O
+    from kea_kernels import lowbit
+    from kea_kernels.binary import kernels
+    b, t, c, k = 2, 40, 256, 512
+    m = b * t
+    g = torch.Generator().manual_seed(split + 7)
+    signs = torch.where(torch.rand(2 * c, k, generator=g) < 0.5, -1, 1).to(torch.int8)
+    codes = torch.from_numpy(O.pack_signs(signs.numpy()))
+    scale = torch.rand(2 * c, generator=g) * 0.09 + 0.01
+    bias = torch.randn(2 * c, generator=g) * 0.1
+    x = torch.randn(1, m, k, generator=g).cuda()
+    q, qs, _ = lowbit.quantize(x, (0, k, 1, m), m, k, 3)
+    w_plain = kernels.relayout_codes(codes, k, 1).cuda()
+    w_il = kernels.relayout_codes(E.glu_interleave(codes), k, 1).cuda()
+    y = torch.empty(m, 2 * c, device="cuda", dtype=out_dtype)
+    lowbit.gemm(1, q, qs, w_plain, 2 * c, k, scale.cuda(), bias.cuda(), y, None)
+    u = torch.empty(m, c, device="cuda", dtype=out_dtype)
+    lowbit.gemm(1, q, qs, w_il, 2 * c, k, E.glu_interleave(scale).cuda(), E.glu_interleave(bias).cuda(), u, None,
+                glu=True, config=kernels.GemmConfig(4, split))
+    torch.cuda.synchronize()
+    y64 = y.double()
+    ref = y64[:, :c] * torch.sigmoid(y64[:, c:])
+    tol = 1e-6 if out_dtype == torch.float32 else 2e-3
+    assert float(((u.double() - ref).abs() / (ref.abs() + 1e-3)).max()) < tol
+    if out_dtype == torch.float32:
+        dw = torch.randn(c, 1, 9, generator=g).cuda() / 3
+        db = torch.randn(c, generator=g).cuda()
+        qa, qsa = E.glu_dwconv_quantize(y.view(b, t, 2 * c), dw, db, 3)
+        qb, qsb = E.dwconv_quantize(u.view(b, t, c), dw, db, 3)
+        torch.cuda.synchronize()
+        assert torch.equal(qa, qb) and torch.equal(qsa, qsb)
+
+
+@pytest.mark.gpu
+@torch.inference_mode()
+def test_gemm_glu_contract_errors():
+    from kea_kernels import lowbit
+    from kea_kernels.binary import kernels
+    k = 128
+    codes = torch.zeros(6, k // 8, dtype=torch.uint8)
+    w = kernels.relayout_codes(codes, k, 1).cuda()
+    q = torch.zeros(1, 4, k, dtype=torch.int8, device="cuda")
+    qs = torch.ones(1, 4, device="cuda")
+    scale = torch.ones(6, device="cuda")
+    with pytest.raises(ValueError):  # SiLU and GLU together
+        lowbit.gemm(1, q, qs, w, 6, k, scale, None, torch.empty(4, 3, device="cuda"), None, glu=True, silu=True)
+    with pytest.raises(ValueError):  # odd n
+        lowbit.gemm(1, q, qs, w, 5, k, scale[:5], None, torch.empty(4, 3, device="cuda"), None, glu=True)
