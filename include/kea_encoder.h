@@ -64,6 +64,24 @@ int kea_dwconv_quantize(const float *u_dev, int64_t ldu, const float *w_dev, con
                         int64_t t, int64_t channels, int kernel, int parts, int8_t *q_dev, int64_t ldq, float *qs_dev,
                         void *stream);
 
+/* dw-striding subsampling (x8) of NeMo's ConvSubsampling, as the reference runs it inside its encoder (NeMo
+ * modules, not part of kk/): conv 3x3 stride 2 (1 -> C channels, padding 1) + ReLU, then twice [depthwise 3x3 stride 2
+ * + pointwise 1x1 + ReLU], then a linear layer over the flattened (channel, frequency) features. The pointwise
+ * convolutions and the linear layer are matrix products left to the caller; these three launches are the rest.
+ *
+ * kea_subsample_front: x [batch][f][t] (f <= 128 mel bins of t frames) -> y [batch][C][t2][f2] =
+ *   depthwise(relu(conv(x) + b1)) + b2, t1 = (t-1)/2+1, t2 = (t1-1)/2+1 (same for f); w1, w2 [C][9] (3x3, row-major).
+ * kea_dwconv2d_s2: y [batch][C][(h-1)/2+1][(wd-1)/2+1] = depthwise3x3s2(relu(x + in_bias)) + bias, padding 1
+ *   (in_bias NULL: a zero bias; the ReLU applies either way).
+ * kea_bias_relu_flatten: y [batch][h][C * wd] = relu(x [batch][C][h][wd] + bias[c]). */
+int kea_subsample_front(const float *x_dev, int64_t batch, int64_t t, int64_t f, const float *w1_dev,
+                        const float *b1_dev, const float *w2_dev, const float *b2_dev, int64_t channels, float *y_dev,
+                        void *stream);
+int kea_dwconv2d_s2(const float *x_dev, const float *in_bias_dev, const float *w_dev, const float *bias_dev,
+                    float *y_dev, int64_t batch, int64_t channels, int64_t h, int64_t wd, void *stream);
+int kea_bias_relu_flatten(const float *x_dev, const float *bias_dev, float *y_dev, int64_t batch, int64_t channels,
+                          int64_t h, int64_t wd, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

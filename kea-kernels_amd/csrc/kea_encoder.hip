@@ -399,6 +399,114 @@ glu_dwconv_kernel(const float *x, long long ldx, const float *w, const float *bi
     y[((long long)b * T + t) * ldy + c] = acc;
 }
 
+// ---- dw-striding subsampling (x8): the convolution stack in front of the encoder layers -----------------------
+//
+// NeMo's dw_striding subsampling on [B, 1, T, F] (time rows, mel columns): conv 3x3/2 (1 -> C) + ReLU, then twice
+// [depthwise 3x3/2 + pointwise 1x1 (C -> C) + ReLU], then flatten (c, f) and a linear layer. The pointwise convolutions
+// and the linear layer are plain matrix products (PyTorch / rocBLAS); the kernels below are the rest.
+
+// Front: conv 3x3/2 (1 input channel, padding 1) + bias + ReLU, then depthwise 3x3/2 (padding 1) + bias, without
+// materialising the first convolution's [B, C, T1, F1] output. A thread owns one output position (t2, f2) and loops
+// over a group of CG channels: it holds the 7 x 7 input patch its 3 x 3 first-convolution values need and recomputes
+// them per channel (each first-convolution value feeds up to 4 outputs: 2.25x its FMAs, against a 4x larger tensor
+// round trip through HBM). Channel weights are wave-uniform (scalar loads). x: [B][F][T] (mel-major, as the
+// preprocessor writes it), y: [B][C][T2][F2].
+constexpr int kSubTT = 8;   // output rows (t2) per workgroup; 256 threads = 8 rows x 32 columns
+template <int CG>
+__global__ void __launch_bounds__(256)
+subsample_front_kernel(const float *x, int T, int F, const float *w1, const float *b1, const float *w2,
+                       const float *b2, float *y, int C, int T1, int F1, int T2, int F2) {
+    __shared__ float xt[4 * kSubTT + 3][132];   // input rows 4 t2a - 3 .. , columns -1 .. 130 (zero padded)
+    const int b = blockIdx.z, c0 = blockIdx.y * CG, t2a = blockIdx.x * kSubTT;
+    const int r0 = 4 * t2a - 3;
+    const float *xb = x + (long long)b * F * T;
+    for (int idx = threadIdx.x; idx < (4 * kSubTT + 3) * 132; idx += 256) {
+        const int i = idx / 132, j = idx % 132, r = r0 + i, c = j - 1;
+        xt[i][j] = (r >= 0 && r < T && c >= 0 && c < F) ? xb[(long long)c * T + r] : 0.f;
+    }
+    __syncthreads();
+    const int t2 = t2a + threadIdx.x / 32, f2 = threadIdx.x % 32;
+    // this thread's 7 x 7 patch: input rows 4 t2 - 3 + i, columns 4 f2 - 3 + j (tile column 4 f2 - 2 + j); the
+    // first-convolution value at (2 t2 - 1 + dy, 2 f2 - 1 + dx) reads patch rows 2 dy + ky and columns 2 dx + kx
+    float xin[7][7];
+#pragma unroll
+    for (int i = 0; i < 7; ++i)
+#pragma unroll
+        for (int j = 0; j < 7; ++j) {
+            const int col = 4 * f2 - 2 + j;
+            xin[i][j] = col >= 0 && col < 132 ? xt[4 * (threadIdx.x / 32) + i][col] : 0.f;
+        }
+    bool valid1[3][3];   // first-convolution positions inside [0, T1) x [0, F1) (outside: the depthwise padding)
+#pragma unroll
+    for (int dy = 0; dy < 3; ++dy)
+#pragma unroll
+        for (int dx = 0; dx < 3; ++dx) {
+            const int r1 = 2 * t2 - 1 + dy, c1 = 2 * f2 - 1 + dx;
+            valid1[dy][dx] = r1 >= 0 && r1 < T1 && c1 >= 0 && c1 < F1;
+        }
+    const bool live = t2 < T2 && f2 < F2;
+    for (int cc = 0; cc < CG; ++cc) {
+        const int c = c0 + cc;
+        if (c >= C) break;
+        float wa[9], wb[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            wa[k] = w1[c * 9 + k];
+            wb[k] = w2[c * 9 + k];
+        }
+        const float ba = b1[c];
+        float acc = b2[c];
+#pragma unroll
+        for (int dy = 0; dy < 3; ++dy)
+#pragma unroll
+            for (int dx = 0; dx < 3; ++dx) {
+                float h = ba;
+#pragma unroll
+                for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+                    for (int kx = 0; kx < 3; ++kx) h = __builtin_fmaf(wa[ky * 3 + kx], xin[2 * dy + ky][2 * dx + kx], h);
+                h = valid1[dy][dx] ? fmaxf(h, 0.f) : 0.f;
+                acc = __builtin_fmaf(wb[dy * 3 + dx], h, acc);
+            }
+        if (live) y[(((long long)b * C + c) * T2 + t2) * F2 + f2] = acc;
+    }
+}
+
+// Depthwise 3x3/2 (padding 1) + bias on relu(x + in_bias[c]) (the previous pointwise convolution's bias and ReLU,
+// applied on load). x: [B][C][H][W], y: [B][C][H2][W2]; one thread per output element.
+__global__ void __launch_bounds__(256)
+dwconv_s2_kernel(const float *x, const float *in_bias, const float *w, const float *bias, float *y, int C, int H,
+                 int W, int H2, int W2, long long total) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    const int o = (int)(idx % W2), r = (int)((idx / W2) % H2);
+    const long long bc = idx / ((long long)W2 * H2);
+    const int c = (int)(bc % C);
+    const float *xc = x + bc * H * W;
+    const float ib = in_bias ? in_bias[c] : 0.f;
+    float acc = bias[c];
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+        for (int kx = 0; kx < 3; ++kx) {
+            const int rr = 2 * r - 1 + ky, cc = 2 * o - 1 + kx;
+            if (rr < 0 || rr >= H || cc < 0 || cc >= W) continue;
+            acc = __builtin_fmaf(w[c * 9 + ky * 3 + kx], fmaxf(xc[rr * W + cc] + ib, 0.f), acc);
+        }
+    y[idx] = acc;
+}
+
+// y[b][t][c * W + f] = relu(x[b][c][t][f] + bias[c]): the last pointwise convolution's bias and ReLU with the
+// flatten of (channel, frequency) per time step.
+__global__ void __launch_bounds__(256)
+bias_relu_flatten_kernel(const float *x, const float *bias, float *y, int C, int H, int W, long long total) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;  // over y
+    if (idx >= total) return;
+    const int f = (int)(idx % W), c = (int)((idx / W) % C), t = (int)((idx / ((long long)W * C)) % H);
+    const long long b = idx / ((long long)W * C * H);
+    y[idx] = fmaxf(x[((b * C + c) * H + t) * W + f] + bias[c], 0.f);
+}
+
 }  // namespace
 
 extern "C" {
@@ -469,6 +577,52 @@ int kea_glu_dwconv(const float *x, int64_t ldx, const float *w, const float *bia
                        (long long)ldy, (int)t, (int)channels, kernel);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return kea::fail((int)e, std::string("glu_dwconv launch failed: ") + hipGetErrorString(e));
+    return KEA_OK;
+}
+
+int kea_subsample_front(const float *x, int64_t batch, int64_t t, int64_t f, const float *w1, const float *b1,
+                        const float *w2, const float *b2, int64_t channels, float *y, void *stream) {
+    if (batch < 0 || batch > 65535 || t < 1 || f < 1 || f > 128 || channels < 1 || channels > 65535 || t > INT32_MAX / 4)
+        return kea::fail(KEA_EINVAL, "bad sizes (f <= 128)");
+    if (batch == 0) return KEA_OK;
+    if (!x || !w1 || !b1 || !w2 || !b2 || !y) return kea::fail(KEA_EINVAL, "null pointer");
+    const int t1 = (int)((t - 1) / 2 + 1), f1 = (int)((f - 1) / 2 + 1);
+    const int t2 = (t1 - 1) / 2 + 1, f2 = (f1 - 1) / 2 + 1;
+    constexpr int CG = 32;
+    const dim3 grid((unsigned)((t2 + kSubTT - 1) / kSubTT), (unsigned)((channels + CG - 1) / CG), (unsigned)batch);
+    hipLaunchKernelGGL(subsample_front_kernel<CG>, grid, dim3(256), 0, (hipStream_t)stream, x, (int)t, (int)f, w1, b1,
+                       w2, b2, y, (int)channels, t1, f1, t2, f2);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("subsample launch failed: ") + hipGetErrorString(e));
+    return KEA_OK;
+}
+
+int kea_dwconv2d_s2(const float *x, const float *in_bias, const float *w, const float *bias, float *y, int64_t batch,
+                    int64_t channels, int64_t h, int64_t wd, void *stream) {
+    if (batch < 0 || channels < 1 || h < 1 || wd < 1 || batch * channels * h * wd > ((int64_t)1 << 40))
+        return kea::fail(KEA_EINVAL, "bad sizes");
+    if (batch == 0) return KEA_OK;
+    if (!x || !w || !bias || !y) return kea::fail(KEA_EINVAL, "null pointer");
+    const int h2 = (int)((h - 1) / 2 + 1), w2 = (int)((wd - 1) / 2 + 1);
+    const long long total = batch * channels * (long long)h2 * w2;
+    hipLaunchKernelGGL(dwconv_s2_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x,
+                       in_bias, w, bias, y, (int)channels, (int)h, (int)wd, h2, w2, total);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("dwconv2d launch failed: ") + hipGetErrorString(e));
+    return KEA_OK;
+}
+
+int kea_bias_relu_flatten(const float *x, const float *bias, float *y, int64_t batch, int64_t channels, int64_t h,
+                          int64_t wd, void *stream) {
+    if (batch < 0 || channels < 1 || h < 1 || wd < 1 || batch * channels * h * wd > ((int64_t)1 << 40))
+        return kea::fail(KEA_EINVAL, "bad sizes");
+    if (batch == 0) return KEA_OK;
+    if (!x || !bias || !y) return kea::fail(KEA_EINVAL, "null pointer");
+    const long long total = batch * channels * h * wd;
+    hipLaunchKernelGGL(bias_relu_flatten_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, x, bias, y, (int)channels, (int)h, (int)wd, total);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("flatten launch failed: ") + hipGetErrorString(e));
     return KEA_OK;
 }
 

@@ -328,6 +328,7 @@ class FastConformerEncoder:
                  dense: bool = False, fused: bool = True):
         self.cfg, self.parts, self.dense = cfg, parts, dense
         self.fused = fused and not dense
+        self._sub_out = None
         self.device = device = torch.device(device)
         if device.type == "cuda" and device.index is None:
             self.device = device = torch.device("cuda", torch.cuda.current_device())
@@ -427,10 +428,16 @@ class FastConformerEncoder:
     def subsample(self, feats: Tensor) -> Tensor:
         """[B, mels, frames] -> [B, T', d] (dw-striding x8, then the output linear).
 
-        The convolutions run on PyTorch's own GPU kernels (the library-convolution path is switched off here): its
-        algorithm choice varied from box to box, by up to 10x on the first 3x3 convolution."""
+        Fused (quantized) path: the first convolution + ReLU + first depthwise convolution in one kernel
+        (kea_subsample_front), the pointwise convolutions as batched matrix products whose bias + ReLU are applied
+        by the next kernel on load, the second depthwise convolution (kea_dwconv2d_s2), the last bias + ReLU with the
+        (channel, frequency) flatten (kea_bias_relu_flatten), and the output linear as one matrix product. Otherwise
+        PyTorch's own convolution kernels (the library-convolution path is switched off: its algorithm choice varied
+        from box to box, by up to 10x on the first 3x3 convolution)."""
         s = self.sub
         c = self.cfg.sub_channels
+        if self.fused:
+            return self._subsample_fused(feats)
         with torch.backends.cudnn.flags(enabled=False):
             x = feats.transpose(1, 2).unsqueeze(1)                                    # [B, 1, frames, mels]
             x = F.relu(F.conv2d(x, s["conv.0.weight"], s["conv.0.bias"], stride=2, padding=1))
@@ -440,6 +447,32 @@ class FastConformerEncoder:
         b, _, t, f = x.shape
         x = x.transpose(1, 2).reshape(b, t, c * f)
         return F.linear(x, s["out.weight"], s["out.bias"])
+
+    def _subsample_fused(self, feats: Tensor) -> Tensor:
+        s, c = self.sub, self.cfg.sub_channels
+        feats = feats.contiguous()
+        b, f, t = feats.shape
+        t1, f1 = (t - 1) // 2 + 1, (f - 1) // 2 + 1
+        t2, f2 = (t1 - 1) // 2 + 1, (f1 - 1) // 2 + 1
+        t3, f3 = (t2 - 1) // 2 + 1, (f2 - 1) // 2 + 1
+        L = _hip.lib()
+        st = _hip.stream_handle(feats.device)
+        x1 = torch.empty(b, c, t2, f2, device=feats.device, dtype=torch.float32)
+        _hip.check(L.kea_subsample_front(feats.data_ptr(), b, t, f, s["conv.0.weight"].data_ptr(),
+                                         s["conv.0.bias"].data_ptr(), s["conv.2.weight"].data_ptr(),
+                                         s["conv.2.bias"].data_ptr(), c, x1.data_ptr(), st), "kea_subsample_front")
+        p1 = torch.matmul(s["conv.3.weight"].view(c, c), x1.view(b, c, t2 * f2))           # [B, C, t2*f2]
+        x2 = torch.empty(b, c, t3, f3, device=feats.device, dtype=torch.float32)
+        _hip.check(L.kea_dwconv2d_s2(p1.data_ptr(), s["conv.3.bias"].data_ptr(), s["conv.5.weight"].data_ptr(),
+                                     s["conv.5.bias"].data_ptr(), x2.data_ptr(), b, c, t2, f2, st), "kea_dwconv2d_s2")
+        p2 = torch.matmul(s["conv.6.weight"].view(c, c), x2.view(b, c, t3 * f3))           # [B, C, t3*f3]
+        flat = torch.empty(b, t3, c * f3, device=feats.device, dtype=torch.float32)
+        _hip.check(L.kea_bias_relu_flatten(p2.data_ptr(), s["conv.6.bias"].data_ptr(), flat.data_ptr(), b, c, t3,
+                                           f3, st), "kea_bias_relu_flatten")
+        if self._sub_out is None:  # the x sqrt(d) scaling folded into the output linear
+            g = math.sqrt(self.cfg.d_model) if self.cfg.xscaling else 1.0
+            self._sub_out = ((s["out.weight"] * g).contiguous(), (s["out.bias"] * g).contiguous())
+        return F.linear(flat, *self._sub_out)
 
     def positions(self, t: int) -> list:
         """W_pos applied to the relative encodings, per layer, for length t: [2t-1, d] each. Frozen per length
@@ -557,7 +590,7 @@ class FastConformerEncoder:
 
     def encode(self, feats: Tensor) -> Tensor:
         x = self.subsample(feats)
-        if self.cfg.xscaling:
+        if self.cfg.xscaling and not self.fused:  # the fused subsampling applies it in its output linear
             x = x * math.sqrt(self.cfg.d_model)
         pos = self.positions(x.shape[1])
         xq = None

@@ -259,3 +259,27 @@ def test_gemm_glu_contract_errors():
         lowbit.gemm(1, q, qs, w, 6, k, scale, None, torch.empty(4, 3, device="cuda"), None, glu=True, silu=True)
     with pytest.raises(ValueError):  # odd n
         lowbit.gemm(1, q, qs, w, 5, k, scale[:5], None, torch.empty(4, 3, device="cuda"), None, glu=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,frames", [(1, 1000), (2, 999), (3, 37)])
+@torch.inference_mode()
+def test_fused_subsampling_matches_pytorch(b, frames):
+    """kea_subsample_front + pointwise products + kea_dwconv2d_s2 + kea_bias_relu_flatten + output linear (x sqrt(d)
+    folded in) against PyTorch's convolution stack in FP64."""
+    cfg = E.EncoderConfig(layers=1)
+    w = E.synthetic_weights(cfg, seed=4)
+    enc = E.FastConformerEncoder(w, cfg, "cuda", parts=1)
+    feats = torch.randn(b, cfg.feat_in, frames, generator=torch.Generator().manual_seed(frames)).cuda()
+    got = enc._subsample_fused(feats).double()
+    s = {k: v.double() for k, v in enc.sub.items()}
+    c = cfg.sub_channels
+    x = feats.double().transpose(1, 2).unsqueeze(1)
+    x = F.relu(F.conv2d(x, s["conv.0.weight"], s["conv.0.bias"], stride=2, padding=1))
+    for i in (2, 5):
+        x = F.conv2d(x, s[f"conv.{i}.weight"], s[f"conv.{i}.bias"], stride=2, padding=1, groups=c)
+        x = F.relu(F.conv2d(x, s[f"conv.{i + 1}.weight"], s[f"conv.{i + 1}.bias"]))
+    bb, _, t, f = x.shape
+    ref = F.linear(x.transpose(1, 2).reshape(bb, t, c * f), s["out.weight"], s["out.bias"]) * math.sqrt(cfg.d_model)
+    assert got.shape == ref.shape
+    assert float((got - ref).abs().max() / ref.abs().max()) < 1e-5
