@@ -12,6 +12,7 @@
 #include <string>
 
 #include "kea_internal.h"
+#include "kea_wave.h"
 #include "../../include/kea_encoder.h"
 
 namespace {
@@ -19,16 +20,8 @@ namespace {
 constexpr int kQB = 8;        // query rows per workgroup
 constexpr int kMaxT = 256;    // longest sequence a workgroup holds
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
-    return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
+using kea::wave_max;
+using kea::wave_sum;
 
 // One workgroup (256 threads, 4 waves) = one (batch b, head h, block of kQB = 8 query rows); wave w owns query rows
 // 2w and 2w + 1. For query i and key j:
@@ -181,20 +174,16 @@ relpos_attention_kernel(const float *qkv, long long ld, const float *pos, long l
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// Xor-butterfly max / sum of R independent values over the 64 lanes of a wave (R chains interleaved).
+// Max / sum of R independent values over the 64 lanes of a wave (independent chains the scheduler interleaves).
 template <int R>
 __device__ __forceinline__ void wave_max_n(float *v) {
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-#pragma unroll
-        for (int r = 0; r < R; ++r) v[r] = fmaxf(v[r], __shfl_xor(v[r], off, 64));
+    for (int r = 0; r < R; ++r) v[r] = wave_max(v[r]);
 }
 template <int R>
 __device__ __forceinline__ void wave_sum_n(float *v) {
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-#pragma unroll
-        for (int r = 0; r < R; ++r) v[r] = v[r] + __shfl_xor(v[r], off, 64);
+    for (int r = 0; r < R; ++r) v[r] = wave_sum(v[r]);
 }
 
 // Matrix-core form of the same attention for T <= 128 (one workgroup = 16 query rows of one (b, h), NW waves), on

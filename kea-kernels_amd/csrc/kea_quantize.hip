@@ -12,8 +12,8 @@
 // chunks k = 4 * (th + 64 * WPR * i) + j: consecutive threads read consecutive 16-byte chunks (one float4 load each
 // when the row is contiguous and aligned) and store the 4 quantized bytes as one dword. The LayerNorm sums, the only
 // reductions that are not exact, use one fixed order that the CPU oracle restates: each thread sums its elements in
-// increasing k, a xor butterfly over the 64 lanes of each wave (offsets 32, 16, ..., 1), then the wave totals in wave
-// order. The max reductions are exact in any order.
+// increasing k, a xor butterfly over the 64 lanes of each wave (offsets 1, 2, 4, ..., 32; kea_wave.h), then the wave
+// totals in wave order. The max reductions are exact in any order.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -21,20 +21,13 @@
 
 #include "kea_epilogue.h"
 #include "kea_internal.h"
+#include "kea_wave.h"
 #include "../../include/kea_encoder.h"
 
 namespace {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
-    return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
+using kea::wave_max;
+using kea::wave_sum;
 
 __device__ __forceinline__ float load_x(const void *x, int dtype, long long i) {
     if (dtype == KEA_F16) return (float)(((const _Float16 *)x)[i]);

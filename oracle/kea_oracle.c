@@ -215,7 +215,7 @@ static float f16_to_f32(uint16_t h) {
 /*
  * The library's fixed LayerNorm summation order: a row is split over WPR wave64s (1 for k <= 256, else 4); thread th
  * of the row sums, in increasing k, its 4-element chunks k = 4 * (th + 64 * WPR * i) + j; each wave combines its 64
- * partial sums with a xor butterfly (offsets 32, 16, ..., 1); the wave totals are then added in wave order.
+ * partial sums with a xor butterfly (offsets 1, 2, 4, ..., 32); the wave totals are then added in wave order.
  */
 static float row_sum(const float *z, int64_t k) {
     const int wpr = k > 256 ? 4 : 1, tpr = 64 * wpr;
@@ -229,7 +229,7 @@ static float row_sum(const float *z, int64_t k) {
     float total = 0.f;
     for (int w = 0; w < wpr; ++w) {
         float *v = p + 64 * w;
-        for (int off = 32; off >= 1; off >>= 1) {
+        for (int off = 1; off <= 32; off <<= 1) {
             float nxt[64];
             for (int l = 0; l < 64; ++l) nxt[l] = v[l] + v[l ^ off];
             memcpy(v, nxt, sizeof(nxt));
