@@ -272,6 +272,10 @@ constexpr int kMaxStages = KEA_MAX_STAGES;
 #ifndef KEA_STAGE_K
 #define KEA_STAGE_K 256
 #endif
+// Tiles with P * RM at most this read a whole stage's LDS operands before its first MFMA (see compute below).
+#ifndef KEA_FULL_PRM
+#define KEA_FULL_PRM 2
+#endif
 __host__ __device__ constexpr StageShape stage_shape(int wbits, int parts, int rm, int rn, int wm, int wn) {
     const int nw = wm * wn, bm = wm * rm * 16, bn = wn * rn * 16;
     const int sw = KEA_STAGE_K / (wbits == 1 ? 128 : 64);
@@ -476,7 +480,7 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     };
 
     // One stage of MFMAs: straight-line code (no accumulator ever passes a control-flow merge; merges made the
-    // compiler emit AGPR copy chains). Operand reads from LDS run ahead of the MFMAs: narrow tiles (P * RM <= 3, few
+    // compiler emit AGPR copy chains). Operand reads from LDS run ahead of the MFMAs: narrow tiles (P * RM <= 2, few
     // MFMAs per k-step) issue every read of the stage before the first MFMA, so a stage pays one LDS latency instead
     // of one per k-step; wider tiles read k-step t + 1 while the MFMAs of step t run. MASKED (the last stage) zeroes
     // the weights at k >= kend: per 16-byte group of a lane's operand, or per byte for KTAIL.
@@ -484,7 +488,7 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
         constexpr bool MASKED = decltype(masked_tag)::value;
         const int8_t *buf = lds + (s % NS) * STAGE_BYTES;
         constexpr int STEPS = SW * KS;  // MFMA k-steps per stage
-        constexpr bool FULL = P * RM <= 3;
+        constexpr bool FULL = P * RM <= KEA_FULL_PRM;
         constexpr int ASLOTS = FULL ? STEPS : 2, WSLOTS = FULL ? SW : 2;
         v4i af[ASLOTS][P][RM];
         uint32_t wv[WSLOTS][RN];
@@ -845,15 +849,16 @@ FinishFn pick_finish(int parts) {
 
 // Tile and split choice: a pure function of (wbits, parts, m, n, k), fitted to MI355X sweeps of every tile x split
 // over BASELINE.json's shapes and the reference's tuned (N, K, M) points at P = 1 and 3 (the chosen configuration is
-// within 0.3% of the per-shape best summed over those 61 shapes). With P >= 2 the narrow 16x64 tile wins (its
-// register budget leaves room for co-resident workgroups); with P = 1 the 32x32 tile wins up to a few hundred rows,
-// then wide tiles take over as M grows.
+// within 0.3% of the per-shape best summed over those 61 shapes), re-checked with FP32 outputs at the encoder's
+// shapes (M = 125 and 1000). With P >= 2 the narrow 16x64 tile wins (its register budget leaves room for
+// co-resident workgroups) up to a few hundred rows, 32x128 from M = 512 at N >= 2048; with P = 1 the 32x32 tile wins
+// up to a few hundred rows, then 32x64 (N <= 1024) or 64x64 tiles take over as M grows.
 int choose_tile(int wbits, int parts, long long m, long long n, long long k) {
     (void)wbits; (void)k;
-    if (parts >= 2) return (m >= 320 && n >= 3072) ? 3 : 1;
+    if (parts >= 2) return (m >= 512 && n >= 2048) ? 9 : (m >= 320 && n >= 3072) ? 3 : 1;
     if (m <= 64) return 4;
     if (m < 512) return (n >= 4096 && m >= 192) ? 2 : 4;
-    return n <= 1024 ? 2 : (n >= 4096 ? 8 : 5);
+    return n <= 1024 ? 2 : 5;
 }
 
 // Split factor for split_k == 0: split K only for long K ranges (>= 2048) whose tiling leaves at most 64 workgroups,
