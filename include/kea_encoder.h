@@ -82,6 +82,14 @@ int kea_dwconv2d_s2(const float *x_dev, const float *in_bias_dev, const float *w
 int kea_bias_relu_flatten(const float *x_dev, const float *bias_dev, float *y_dev, int64_t batch, int64_t channels,
                           int64_t h, int64_t wd, void *stream);
 
+/* Normalised log-mel features from an STFT (the preprocessor of NeMo's AudioToMelSpectrogramPreprocessor, which
+ * the reference's encoder runs in front of its layers): spec interleaved complex [batch][bins][ld_t] (ld_t >= frames),
+ * fb [mels][bins] with row m nonzero only in [lo[m], hi[m]) (0 <= lo <= hi <= bins), y [batch][mels][frames] =
+ *   v = log(sum_k fb[m][k] * |spec[k][t]|^2 + log_eps);  y = (v - mean_t v) / (std_t v + std_eps)  (std: n - 1). */
+int kea_logmel_normalize(const float *spec_dev, int64_t batch, int64_t bins, int64_t frames, int64_t ld_t,
+                         const float *fb_dev, const int32_t *lo_dev, const int32_t *hi_dev, int64_t mels, float log_eps,
+                         float std_eps, float *y_dev, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -496,6 +496,47 @@ bias_relu_flatten_kernel(const float *x, const float *bias, float *y, int C, int
     y[idx] = fmaxf(x[((b * C + c) * H + t) * W + f] + bias[c], 0.f);
 }
 
+// Log-mel features with per-feature normalisation over time, one workgroup per (clip, mel bin):
+//   v[t] = log(sum_{k in [lo, hi)} fb[m][k] * (re^2 + im^2)[k][t] + log_eps)       (the filter's nonzero bins only)
+//   y[t] = (v[t] - mean) / (std + std_eps),  mean over the frames, std with the n - 1 divisor
+// spec: interleaved complex [B][bins][ld_t]; y: [B][mels][frames]. Thread th owns frames th, th + 256, ...: it writes
+// v, re-reads its own elements for the variance and the normalisation (no barrier between those passes).
+__global__ void __launch_bounds__(256)
+logmel_normalize_kernel(const float2 *spec, int bins, int frames, long long ld_t, const float *fb, const int *lo,
+                        const int *hi, int mels, float log_eps, float std_eps, float *y) {
+    __shared__ float red[2][4];
+    const int m = blockIdx.x, b = blockIdx.y, th = threadIdx.x, wave = th >> 6;
+    const float2 *sb = spec + (long long)b * bins * ld_t;
+    float *yr = y + ((long long)b * mels + m) * frames;
+    const int k0 = lo[m], k1 = hi[m];
+    float sum = 0.f;
+    for (int t = th; t < frames; t += 256) {
+        float acc = 0.f;
+        for (int k = k0; k < k1; ++k) {
+            const float2 c = sb[(long long)k * ld_t + t];
+            acc = __builtin_fmaf(fb[m * bins + k], c.x * c.x + c.y * c.y, acc);
+        }
+        const float v = logf(acc + log_eps);
+        yr[t] = v;
+        sum = sum + v;
+    }
+    sum = wave_sum(sum);
+    if ((th & 63) == 0) red[0][wave] = sum;
+    __syncthreads();
+    const float mean = ((red[0][0] + red[0][1]) + (red[0][2] + red[0][3])) / (float)frames;
+    float sq = 0.f;
+    for (int t = th; t < frames; t += 256) {
+        const float d = yr[t] - mean;
+        sq = __builtin_fmaf(d, d, sq);
+    }
+    sq = wave_sum(sq);
+    if ((th & 63) == 0) red[1][wave] = sq;
+    __syncthreads();
+    const float var = ((red[1][0] + red[1][1]) + (red[1][2] + red[1][3])) / (float)(frames > 1 ? frames - 1 : 1);
+    const float inv = 1.0f / (sqrtf(var) + std_eps);
+    for (int t = th; t < frames; t += 256) yr[t] = (yr[t] - mean) * inv;
+}
+
 }  // namespace
 
 extern "C" {
@@ -612,6 +653,23 @@ int kea_bias_relu_flatten(const float *x, const float *bias, float *y, int64_t b
                        (hipStream_t)stream, x, bias, y, (int)channels, (int)h, (int)wd, total);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return kea::fail((int)e, std::string("flatten launch failed: ") + hipGetErrorString(e));
+    return KEA_OK;
+}
+
+int kea_logmel_normalize(const float *spec, int64_t batch, int64_t bins, int64_t frames, int64_t ld_t,
+                         const float *fb, const int32_t *lo, const int32_t *hi, int64_t mels, float log_eps,
+                         float std_eps, float *y, void *stream) {
+    if (batch < 0 || batch > 65535 || bins < 1 || frames < 1 || ld_t < frames || mels < 1 || mels > 65535 ||
+        bins * ld_t > ((int64_t)1 << 40))
+        return kea::fail(KEA_EINVAL, "bad sizes");
+    if (batch == 0) return KEA_OK;
+    if (!spec || !fb || !lo || !hi || !y) return kea::fail(KEA_EINVAL, "null pointer");
+    if ((uintptr_t)spec & 7) return kea::fail(KEA_EALIGN, "spec must be 8-byte aligned (interleaved complex)");
+    hipLaunchKernelGGL(logmel_normalize_kernel, dim3((unsigned)mels, (unsigned)batch), dim3(256), 0,
+                       (hipStream_t)stream, (const float2 *)spec, (int)bins, (int)frames, (long long)ld_t, fb, lo, hi,
+                       (int)mels, log_eps, std_eps, y);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("logmel launch failed: ") + hipGetErrorString(e));
     return KEA_OK;
 }
 

@@ -163,12 +163,20 @@ def encoded_length(frames: int) -> int:
 
 class Preprocessor:
     """audio [B, S] FP32 -> normalised log-mel [B, n_mels, frames]: pre-emphasis, |STFT|^2 (Hann 400 / hop 160 /
-    n_fft 512, centred), mel projection, log(x + 2^-24), per-feature mean / std normalisation over time."""
+    n_fft 512, centred), mel projection, log(x + 2^-24), per-feature mean / std normalisation over time.
+    fused: everything after the STFT in one kernel (kea_logmel_normalize, each filter's nonzero bins only)."""
 
-    def __init__(self, cfg: EncoderConfig, device):
+    def __init__(self, cfg: EncoderConfig, device, *, fused: bool = False):
         self.cfg = cfg
+        self.fused = fused
         self.window = torch.hann_window(cfg.win_length, periodic=False, dtype=torch.float32, device=device)
-        self.fb = torch.from_numpy(mel_filterbank(cfg)).float().to(device)
+        fb = mel_filterbank(cfg)
+        self.fb = torch.from_numpy(fb).float().to(device)
+        nz = fb != 0
+        lo = np.where(nz.any(1), nz.argmax(1), 0)
+        hi = np.where(nz.any(1), fb.shape[1] - nz[:, ::-1].argmax(1), 0)
+        self.lo = torch.from_numpy(lo.astype(np.int32)).to(device)
+        self.hi = torch.from_numpy(hi.astype(np.int32)).to(device)
 
     def __call__(self, audio: Tensor) -> Tensor:
         cfg = self.cfg
@@ -176,6 +184,16 @@ class Preprocessor:
         spec = torch.stft(x, n_fft=cfg.n_fft, hop_length=cfg.hop_length, win_length=cfg.win_length,
                           window=self.window, center=True, pad_mode="constant", return_complex=True)
         frames = frames_for(cfg, audio.shape[1])
+        if self.fused:
+            spec = spec.contiguous()
+            b, bins, ld_t = spec.shape
+            y = torch.empty(b, cfg.feat_in, frames, device=audio.device, dtype=torch.float32)
+            rc = _hip.lib().kea_logmel_normalize(torch.view_as_real(spec).data_ptr(), b, bins, frames, ld_t,
+                                                 self.fb.data_ptr(), self.lo.data_ptr(), self.hi.data_ptr(),
+                                                 cfg.feat_in, 2.0 ** -24, 1e-5, y.data_ptr(),
+                                                 _hip.stream_handle(audio.device))
+            _hip.check(rc, "kea_logmel_normalize")
+            return y
         power = torch.view_as_real(spec[:, :, :frames]).pow(2).sum(-1)          # [B, bins, frames]
         mel = torch.matmul(self.fb, power)                                     # [B, mels, frames]
         logmel = torch.log(mel + 2.0 ** -24)
@@ -332,7 +350,7 @@ class FastConformerEncoder:
         self.device = device = torch.device(device)
         if device.type == "cuda" and device.index is None:
             self.device = device = torch.device("cuda", torch.cuda.current_device())
-        self.pre = Preprocessor(cfg, device)
+        self.pre = Preprocessor(cfg, device, fused=fused and not dense)
         dev = lambda t: t.to(device=device, dtype=torch.float32)  # noqa: E731
         p = "encoder.pre_encode."
         self.sub = {k[len(p):]: dev(v) for k, v in weights.items() if k.startswith(p)}

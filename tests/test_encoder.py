@@ -283,3 +283,24 @@ def test_fused_subsampling_matches_pytorch(b, frames):
     ref = F.linear(x.transpose(1, 2).reshape(bb, t, c * f), s["out.weight"], s["out.bias"]) * math.sqrt(cfg.d_model)
     assert got.shape == ref.shape
     assert float((got - ref).abs().max() / ref.abs().max()) < 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,samples", [(1, 160000), (3, 48000), (2, 16000)])
+@torch.inference_mode()
+def test_fused_logmel_matches_pytorch(b, samples):
+    """kea_logmel_normalize (each mel filter's nonzero bins, log, per-feature normalisation) against the PyTorch
+    preprocessor computed in FP64 after the same STFT."""
+    cfg = E.EncoderConfig()
+    audio = torch.randn(b, samples, generator=torch.Generator().manual_seed(samples)).cuda()
+    got = E.Preprocessor(cfg, "cuda", fused=True)(audio).double()
+    pre = E.Preprocessor(cfg, "cuda")
+    x = torch.cat([audio[:, :1], audio[:, 1:] - cfg.preemph * audio[:, :-1]], dim=1)
+    spec = torch.stft(x, n_fft=cfg.n_fft, hop_length=cfg.hop_length, win_length=cfg.win_length, window=pre.window,
+                      center=True, pad_mode="constant", return_complex=True)
+    frames = E.frames_for(cfg, samples)
+    power = torch.view_as_real(spec[:, :, :frames]).double().pow(2).sum(-1)
+    logmel = torch.log(torch.matmul(pre.fb.double(), power) + 2.0 ** -24)
+    ref = (logmel - logmel.mean(2, keepdim=True)) / (logmel.std(2, keepdim=True) + 1e-5)
+    assert got.shape == ref.shape
+    assert float((got - ref).abs().max()) < 1e-4
