@@ -405,13 +405,28 @@ template <int CG>
 __global__ void __launch_bounds__(256)
 subsample_front_kernel(const float *x, int T, int F, const float *w1, const float *b1, const float *w2,
                        const float *b2, float *y, int C, int T1, int F1, int T2, int F2) {
-    __shared__ float xt[4 * kSubTT + 3][132];   // input rows 4 t2a - 3 .. , columns -1 .. 130 (zero padded)
+    constexpr int XR = 4 * kSubTT + 3, XC = 132, XN = (XR * XC + 255) / 256;
+    __shared__ float xt[XR][XC];          // input rows 4 t2a - 3 .. , columns -1 .. 130 (zero padded)
+    __shared__ float4 wl[CG][5];          // per channel: w1[0..8], b1, w2[0..8], b2 (20 floats)
     const int b = blockIdx.z, c0 = blockIdx.y * CG, t2a = blockIdx.x * kSubTT;
     const int r0 = 4 * t2a - 3;
     const float *xb = x + (long long)b * F * T;
-    for (int idx = threadIdx.x; idx < (4 * kSubTT + 3) * 132; idx += 256) {
-        const int i = idx / 132, j = idx % 132, r = r0 + i, c = j - 1;
-        xt[i][j] = (r >= 0 && r < T && c >= 0 && c < F) ? xb[(long long)c * T + r] : 0.f;
+    {   // tile loads, consecutive threads along time (x is mel-major, time contiguous), all issued before the stores
+        float v[XN];
+#pragma unroll
+        for (int u = 0; u < XN; ++u) {
+            const int idx = threadIdx.x + 256 * u, j = idx / XR, i = idx % XR, r = r0 + i, c = j - 1;
+            v[u] = (idx < XR * XC && r >= 0 && r < T && c >= 0 && c < F) ? xb[(long long)c * T + r] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < XN; ++u) {
+            const int idx = threadIdx.x + 256 * u;
+            if (idx < XR * XC) xt[idx % XR][idx / XR] = v[u];
+        }
+    }
+    for (int idx = threadIdx.x; idx < CG * 20; idx += 256) {
+        const int cc = idx / 20, e = idx % 20, c = min(c0 + cc, C - 1);
+        ((float *)wl)[idx] = e < 9 ? w1[c * 9 + e] : e == 9 ? b1[c] : e < 19 ? w2[c * 9 + e - 10] : b2[c];
     }
     __syncthreads();
     const int t2 = t2a + threadIdx.x / 32, f2 = threadIdx.x % 32;
@@ -434,17 +449,19 @@ subsample_front_kernel(const float *x, int T, int F, const float *w1, const floa
             valid1[dy][dx] = r1 >= 0 && r1 < T1 && c1 >= 0 && c1 < F1;
         }
     const bool live = t2 < T2 && f2 < F2;
+#pragma unroll 2
     for (int cc = 0; cc < CG; ++cc) {
         const int c = c0 + cc;
         if (c >= C) break;
-        float wa[9], wb[9];
+        float wv[20];
 #pragma unroll
-        for (int k = 0; k < 9; ++k) {
-            wa[k] = w1[c * 9 + k];
-            wb[k] = w2[c * 9 + k];
+        for (int q = 0; q < 5; ++q) {
+            const float4 f4 = wl[cc][q];
+            wv[4 * q] = f4.x; wv[4 * q + 1] = f4.y; wv[4 * q + 2] = f4.z; wv[4 * q + 3] = f4.w;
         }
-        const float ba = b1[c];
-        float acc = b2[c];
+        const float *wa = wv, *wb = wv + 10;
+        const float ba = wv[9];
+        float acc = wv[19];
 #pragma unroll
         for (int dy = 0; dy < 3; ++dy)
 #pragma unroll
@@ -510,15 +527,35 @@ logmel_normalize_kernel(const float2 *spec, int bins, int frames, long long ld_t
     float *yr = y + ((long long)b * mels + m) * frames;
     const int k0 = lo[m], k1 = hi[m];
     float sum = 0.f;
-    for (int t = th; t < frames; t += 256) {
-        float acc = 0.f;
-        for (int k = k0; k < k1; ++k) {
-            const float2 c = sb[(long long)k * ld_t + t];
-            acc = __builtin_fmaf(fb[m * bins + k], c.x * c.x + c.y * c.y, acc);
+    for (int t0 = 0; t0 < frames; t0 += 1024) {   // 4 frames per thread per chunk; 4 bins x 4 frames loads in flight
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int k = k0; k < k1; k += 4) {
+            float2 c[4][4];
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = t0 + th + 256 * i;
+                    c[kk][i] = make_float2(0.f, 0.f);
+                    if (k + kk < k1 && t < frames) c[kk][i] = sb[(long long)(k + kk) * ld_t + t];
+                }
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const float w = k + kk < k1 ? fb[m * bins + k + kk] : 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[i] = __builtin_fmaf(w, c[kk][i].x * c[kk][i].x + c[kk][i].y * c[kk][i].y, acc[i]);
+            }
         }
-        const float v = logf(acc + log_eps);
-        yr[t] = v;
-        sum = sum + v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = t0 + th + 256 * i;
+            if (t < frames) {
+                const float v = logf(acc[i] + log_eps);
+                yr[t] = v;
+                sum = sum + v;
+            }
+        }
     }
     sum = wave_sum(sum);
     if ((th & 63) == 0) red[0][wave] = sum;
