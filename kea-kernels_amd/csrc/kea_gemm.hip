@@ -68,6 +68,7 @@ struct Params {
     float res_factor;
     int groups;     // per-group scales: G = ceil(K / ws_group) groups, alpha [N][G]
     int gp_shift;   // log2 of the padded group count held in LDS (a power of two >= the groups the stages span)
+    int ws_vec, bias_vec;  // 1: per-channel scales / bias allow aligned 4-element vector loads
 };
 
 using kea::combine;
@@ -191,12 +192,36 @@ __device__ __forceinline__ void load_row_scales(const Params &p, int m, EpiOpera
     for (int c = 0; c < 3; ++c) e.s[c] = c < P ? load_scalar(p.qs, p.qs_dtype, c * p.qs_stride + mm) : 0.f;
 }
 
-__device__ __forceinline__ void load_col_scales(const Params &p, int nb, EpiOperands &e, bool with_alpha = true) {
+// Four consecutive values of a per-column vector (f32 or f16) at nb..nb+3: one vector load when they are all in range
+// and the vector is aligned, else clamped scalar loads (the clamped values are never stored).
+__device__ __forceinline__ void load_col4(const void *v, int dtype, bool vec, int nb, int N, float *out) {
+    if (vec && nb + 3 < N) {
+        if (dtype == KEA_F16) {
+            const uint2 h = *(const uint2 *)((const _Float16 *)v + nb);
+            const _Float16 *hv = (const _Float16 *)&h;
+            out[0] = (float)hv[0]; out[1] = (float)hv[1]; out[2] = (float)hv[2]; out[3] = (float)hv[3];
+        } else {
+            const float4 f = *(const float4 *)((const float *)v + nb);
+            out[0] = f.x; out[1] = f.y; out[2] = f.z; out[3] = f.w;
+        }
+    } else {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int n = nb + r < p.N ? nb + r : p.N - 1;
-        e.alpha[r] = with_alpha ? load_scalar(p.ws, p.ws_dtype, n) : 0.f;
-        e.bias[r] = p.bias ? load_scalar(p.bias, p.bias_dtype, n) : 0.f;
+        for (int r = 0; r < 4; ++r) out[r] = load_scalar(v, dtype, nb + r < N ? nb + r : N - 1);
+    }
+}
+
+__device__ __forceinline__ void load_col_scales(const Params &p, int nb, EpiOperands &e, bool with_alpha = true) {
+    if (with_alpha) {
+        load_col4(p.ws, p.ws_dtype, p.ws_vec, nb, p.N, e.alpha);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) e.alpha[r] = 0.f;
+    }
+    if (p.bias) {
+        load_col4(p.bias, p.bias_dtype, p.bias_vec, nb, p.N, e.bias);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) e.bias[r] = 0.f;
     }
 }
 
@@ -1003,6 +1028,8 @@ static int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ld
     const int yv = glu ? 2 : 4;  // elements per vector store
     p.y_vec = y && (ldy % yv == 0) && ((uintptr_t)y % (yv * esz) == 0);
     p.acc_vec = acc_out && (acc_ld % 4 == 0) && ((uintptr_t)acc_out % 16 == 0);
+    p.ws_vec = ((uintptr_t)wscale % (ws_dtype == KEA_F16 ? 8 : 16)) == 0;
+    p.bias_vec = bias && ((uintptr_t)bias % (bias_dtype == KEA_F16 ? 8 : 16)) == 0;
 
     const Tile &t = kTiles[tile - 1];
     const int bm = t.wm * t.rm * 16, bn = t.wn * t.rn * 16;
@@ -1152,6 +1179,8 @@ int kea_lowbit_slices_finish(const int32_t *slices, int split, int parts, int64_
     const int esz = (y_dtype == KEA_F32) ? 4 : 2;
     p.y_vec = y && (ldy % 4 == 0) && ((uintptr_t)y % (4 * esz) == 0);
     p.acc_vec = acc_out && (acc_ld % 4 == 0) && ((uintptr_t)acc_out % 16 == 0);
+    p.ws_vec = ((uintptr_t)wscale % (ws_dtype == KEA_F16 ? 8 : 16)) == 0;
+    p.bias_vec = bias && ((uintptr_t)bias % (bias_dtype == KEA_F16 ? 8 : 16)) == 0;
     const long long work = m * cdivl(n, 4);
     hipLaunchKernelGGL(pick_finish(parts), dim3((unsigned)cdivl(work, 256)), dim3(256), 0, (hipStream_t)stream, p, split);
     hipError_t e = hipGetLastError();
