@@ -29,6 +29,15 @@ namespace {
 using kea::wave_max;
 using kea::wave_sum;
 
+// rint(z / s) with z / s the IEEE quotient, without a division per element: q = z * inv (inv = 1 / s, correctly
+// rounded) is corrected once with the residual, r = fma(-q, s, z), q' = fma(r, inv, q), which is the correctly rounded
+// quotient (Markstein's correction step for division with a fused multiply-add). Where the residual would underflow,
+// |z / s| < 1 / 4 and both round to 0.
+__device__ __forceinline__ float round_quotient(float z, float s, float inv) {
+    const float q = z * inv;
+    return rintf(fmaf(fmaf(-q, s, z), inv, q));
+}
+
 __device__ __forceinline__ float load_x(const void *x, int dtype, long long i) {
     if (dtype == KEA_F16) return (float)(((const _Float16 *)x)[i]);
     return ((const float *)x)[i];
@@ -51,8 +60,8 @@ __device__ __forceinline__ float row_reduce(float v, float (*red)[WPR], int slot
     }
 }
 
-// VPT: 4-element chunks per thread (K <= 256 * WPR * VPT). VEC: contiguous, 16-byte aligned rows (float4 loads) and
-// ldq % 4 == 0 (dword stores); otherwise element-wise access with any strides.
+// VPT: 4-element chunks per thread (K <= 256 * WPR * VPT). VEC: contiguous, 16-byte aligned rows and LayerNorm weights
+// (float4 loads), K % 4 == 0 and ldq % 4 == 0 (dword stores); otherwise element-wise access with any strides.
 template <int VPT, int WPR, bool VEC>
 __global__ void __launch_bounds__(256)
 quantize_kernel(const void *x, int x_dtype, long long xb, long long xt, long long xk, long long t, int M, int K,
@@ -69,13 +78,24 @@ quantize_kernel(const void *x, int x_dtype, long long xb, long long xt, long lon
     float lw[VPT][4], lb[VPT][4];
     if (nw) {
 #pragma unroll
-        for (int i = 0; i < VPT; ++i)
+        for (int i = 0; i < VPT; ++i) {
+            const int k0 = 4 * (th + TPR * i);
+            if constexpr (VEC) {  // K % 4 == 0: a chunk is inside the row or past it; one 16-byte load each
+                float4 w4 = make_float4(0.f, 0.f, 0.f, 0.f), b4 = w4;
+                if (k0 < K) {
+                    w4 = *(const float4 *)(nw + k0);
+                    b4 = *(const float4 *)(nb + k0);
+                }
+                lw[i][0] = w4.x; lw[i][1] = w4.y; lw[i][2] = w4.z; lw[i][3] = w4.w;
+                lb[i][0] = b4.x; lb[i][1] = b4.y; lb[i][2] = b4.z; lb[i][3] = b4.w;
+            } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int k = 4 * (th + TPR * i) + j;
-                lw[i][j] = k < K ? nw[k] : 0.f;
-                lb[i][j] = k < K ? nb[k] : 0.f;
+                for (int j = 0; j < 4; ++j) {
+                    lw[i][j] = k0 + j < K ? nw[k0 + j] : 0.f;
+                    lb[i][j] = k0 + j < K ? nb[k0 + j] : 0.f;
+                }
             }
+        }
     }
     float z[VPT][4];
 #pragma unroll
@@ -149,6 +169,7 @@ quantize_kernel(const void *x, int x_dtype, long long xb, long long xt, long lon
         } else if (th == 0) {
             ((float *)qs)[(long long)c * M + m] = s;
         }
+        const float inv = 1.0f / s;
         int8_t *row = q + ((long long)c * M + m) * ldq;
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
@@ -156,7 +177,7 @@ quantize_kernel(const void *x, int x_dtype, long long xb, long long xt, long lon
             uint32_t packed = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                float v = rintf(z[i][j] / s);
+                float v = round_quotient(z[i][j], s, inv);
                 v = fminf(fmaxf(v, -127.0f), 127.0f);
                 packed |= (uint32_t)(uint8_t)(int8_t)(int)v << (8 * j);
                 z[i][j] = z[i][j] - v * s;
@@ -189,6 +210,7 @@ __device__ __forceinline__ void quantize_parts(float (*z)[4], int K, int parts, 
         amax = row_reduce<WPR, true>(amax, red, 2 + c, wave);
         const float s = fmaxf(amax / 127.0f, 1.0e-30f);
         if (th == 0) qs[(long long)c * M + m] = s;
+        const float inv = 1.0f / s;
         int8_t *row = q + ((long long)c * M + m) * ldq;
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
@@ -196,7 +218,7 @@ __device__ __forceinline__ void quantize_parts(float (*z)[4], int K, int parts, 
             uint32_t packed = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                float v = rintf(z[i][j] / s);
+                float v = round_quotient(z[i][j], s, inv);
                 v = fminf(fmaxf(v, -127.0f), 127.0f);
                 packed |= (uint32_t)(uint8_t)(int8_t)(int)v << (8 * j);
                 z[i][j] = z[i][j] - v * s;
@@ -474,7 +496,8 @@ extern "C" int kea_quantize(const void *x, int x_dtype, int64_t xb, int64_t xt, 
     const int wpr = k > 256 ? 4 : 1;               // waves per row (the oracle restates this rule)
     const int vpt = (int)((k + 256 * wpr - 1) / (256 * wpr));
     const bool vec = xk == 1 && k % 4 == 0 && ldq % 4 == 0 && xb % 4 == 0 && xt % 4 == 0 &&
-                     ((uintptr_t)x % (4 * esz)) == 0 && ((uintptr_t)q % 4) == 0;
+                     ((uintptr_t)x % (4 * esz)) == 0 && ((uintptr_t)q % 4) == 0 &&
+                     (((uintptr_t)norm_w | (uintptr_t)norm_b) % 16) == 0;
     const dim3 grid((unsigned)((m + 4 / wpr - 1) / (4 / wpr))), block(256);
 #define KEA_Q(V, W)                                                                                                \
     do {                                                                                                           \
