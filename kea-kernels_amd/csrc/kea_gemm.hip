@@ -783,6 +783,9 @@ constexpr Tile kTiles[] = {
     {2, 4, 2, 2, "64x128 w2x2 r2x4"},  // 7
     {4, 2, 1, 4, "64x128 w1x4 r4x2"},  // 8
     {2, 2, 1, 4, "32x128 w1x4 r2x2"},  // 9
+    {2, 4, 2, 4, "64x256 w2x4 r2x4"},  // 10
+    {4, 2, 2, 4, "128x128 w2x4 r4x2"}, // 11
+    {1, 2, 2, 4, "32x128 w2x4 r1x2"},  // 12
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -821,6 +824,9 @@ KernelFn pick_tile(int id, bool sliced) {
         case 7: return pick_fit<WBITS, P, 2, 4, 2, 2>(sliced);
         case 8: return pick_fit<WBITS, P, 4, 2, 1, 4>(sliced);
         case 9: return pick_fit<WBITS, P, 2, 2, 1, 4>(sliced);
+        case 10: return pick_fit<WBITS, P, 2, 4, 2, 4>(sliced);
+        case 11: return pick_fit<WBITS, P, 4, 2, 2, 4>(sliced);
+        case 12: return pick_fit<WBITS, P, 1, 2, 2, 4>(sliced);
         default: return nullptr;
     }
 }
@@ -873,17 +879,31 @@ FinishFn pick_finish(int parts) {
 }
 
 // Tile and split choice: a pure function of (wbits, parts, m, n, k), fitted to MI355X sweeps of every tile x split
-// over BASELINE.json's shapes and the reference's tuned (N, K, M) points at P = 1 and 3 (the chosen configuration is
-// within 0.3% of the per-shape best summed over those 61 shapes), re-checked with FP32 outputs at the encoder's
-// shapes (M = 125 and 1000). With P >= 2 the narrow 16x64 tile wins (its register budget leaves room for
-// co-resident workgroups) up to a few hundred rows, 32x128 from M = 512 at N >= 2048; with P = 1 the 32x32 tile wins
-// up to a few hundred rows, then 32x64 (N <= 1024) or 64x64 tiles take over as M grows.
+// over BASELINE.json's shapes, the reference's tuned (N, K, M) points and the encoder's shapes at P = 1, 2 and 3 (HIP
+// graph replay, M from 1 to 1000). Small M wants many workgroups: the 16x64 (P >= 2) and 32x32 (P = 1) tiles, whose
+// register budgets leave room for co-resident workgroups. As M grows the activation tile, re-read once per column
+// tile, becomes the traffic that bounds a CU, so the winners widen in N: 32x64 / 64x64 at P = 1, and at P >= 2 (where
+// the activations are P times larger) the eight-wavefront 32x128 and 64x256 tiles, 10-17% faster than the
+// four-wavefront ones at M = 1000.
 int choose_tile(int wbits, int parts, long long m, long long n, long long k) {
     (void)wbits; (void)k;
-    if (parts >= 2) return (m >= 512 && n >= 2048) ? 9 : (m >= 320 && n >= 3072) ? 3 : 1;
+    if (parts >= 3) {
+        if (m >= 850) return n >= 4096 ? 10 : 12;
+        if (n <= 1024) return 1;
+        if (m < 320) return (n >= 4096 && m >= 192) ? 12 : 1;
+        if (m < 450) return n >= 3072 ? 3 : 1;
+        if (n >= 4096) return 12;
+        return (n >= 3072 || m >= 600) ? 3 : 12;
+    }
+    if (parts == 2) {
+        if (m >= 850 && n >= 4096) return 10;
+        if (m >= 192 && m < 320 && n >= 4096) return 12;
+        return (m >= 512 && n >= 2048) ? 9 : (m >= 320 && n >= 3072) ? 3 : 1;
+    }
     if (m <= 64) return 4;
-    if (m < 512) return (n >= 4096 && m >= 192) ? 2 : 4;
-    return n <= 1024 ? 2 : 5;
+    if (m < 512) return ((n >= 4096 && m >= 192) || (n >= 3072 && m >= 320)) ? 2 : 4;
+    if (m < 850) return n <= 1024 ? 4 : n >= 4096 ? 5 : m < 600 ? 2 : 5;
+    return n <= 1024 ? 2 : n >= 4096 ? 11 : 5;
 }
 
 // Split factor for split_k == 0: split K only for long K ranges (>= 2048) whose tiling leaves at most 64 workgroups,
