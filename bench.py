@@ -13,7 +13,7 @@ Prints one JSON line: value = int8 TOPS (2*M*N*K ops per step), `roofline` for t
 ops per launch / average launch time from HIP events on the launch stream), `encoder` = the metric's second part, ms
 per 10-s clip of the 24-layer synthetic encoder at batch 1 and 8, and `cpu_baseline` = the
 oracle's C port of the reference's b1_fallback arithmetic (unpack -> exact int32 dot -> FP32 epilogue -> fp16) timed on
-this host's cores. Other modes: --suite (configs 2-4 and the reference's tuned shapes), --encoder (config 5 with
+this host's cores. Other modes: --suite (configs 2-4 and the reference's tuned shapes), --case (one GEMM shape), --encoder (config 5 with
 accuracy against the FP32 dense twin), --copy-calibration (a plain copy for the PMC traffic calibration).
 """
 from __future__ import annotations
@@ -113,6 +113,47 @@ def gpu_bench(steps: int, warmup: int):
     return ms_per_step, eager_us, cfg, host
 
 
+def measured_peaks(reps: int = 5) -> dict:
+    """What this GPU sustains, for fractions against measured rather than published peaks: the dense int8 MFMA loop
+    of the library's probe (kea_probe_mfma_i8: 2048 workgroups of four waves, 8 independent 16x16x64 MFMA chains
+    each) and a 1 GiB device-to-device copy (read + write bytes). Best of `reps` event-timed launches each."""
+    import ctypes
+    import torch
+    from kea_kernels import _hip
+    L = _hip.lib()
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    blocks, iters = 2048, 2000
+    out = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    ops = L.kea_probe_mfma_i8_ops(blocks, iters)
+
+    def timed(fn):
+        best = float("inf")
+        for _ in range(reps + 1):  # the first launch warms up
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn()
+            b.record(stream)
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b) * 1e-3)
+        return best
+
+    def mfma():
+        rc = L.kea_probe_mfma_i8(blocks, iters, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"kea_probe_mfma_i8: {L.kea_last_error().decode()}")
+
+    t_mfma = timed(mfma)
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    t_copy = timed(lambda: dst.copy_(src))
+    nbytes = 2 * src.numel() * 4
+    del src, dst
+    return {"mfma_i8_tops": round(ops / t_mfma / 1e12, 1), "copy_gbs": round(nbytes / t_copy / 1e9, 1),
+            "method": "int8 MFMA loop (2048 WGs x 4 waves x 2000 x 8 v_mfma_i32_16x16x64_i8) and a 1 GiB "
+                      "device-to-device copy (read + write bytes), best of 5"}
+
+
 def cpu_baseline(host, seconds: float = 10.0):
     """The oracle's C port of b1_fallback on the same workload, repeated for about `seconds` on this host's cores."""
     import numpy as np
@@ -153,8 +194,11 @@ REF_SHAPES = [(n, k, m) for n, k in [(1024, 1024), (1024, 4096), (2048, 1024), (
               for m in (38, 126, 256, 368)]  # kk/binary/configs.py:17-36 (RTX 5090 timings, three parts, FP32 out)
 
 
-def _suite_case(wbits, parts, m, n, k, *, scale_dtype, out_dtype, seed, reps=200, ws_group=0):
-    """Per-launch microseconds of the library's default configuration, inputs resident, HIP-graph replay."""
+def _suite_case(wbits, parts, m, n, k, *, scale_dtype, out_dtype, seed, reps=200, ws_group=0, cold=False):
+    """Per-launch microseconds of the library's default configuration, inputs resident, HIP-graph replay.
+
+    cold: every launch reads its own copy of the weights and activations, cycling through at least 768 MiB of
+    copies (three times the 256 MB last-level cache), so no launch finds its operands in a cache."""
     import torch
     from kea_kernels import formats, lowbit
     from kea_kernels.binary import bits, kernels
@@ -173,33 +217,49 @@ def _suite_case(wbits, parts, m, n, k, *, scale_dtype, out_dtype, seed, reps=200
     alpha = (torch.rand(*shape, generator=g) * 0.09 + 0.01).to(scale_dtype).to(dev)
     y = torch.empty(m, n, dtype=out_dtype, device=dev)
     stream = torch.cuda.Stream(dev)
+    copies = 1
+    if cold:
+        per_copy = words.numel() * words.element_size() + q.numel()
+        copies = -(-(3 << 28) // per_copy)
+        operands = [(q.clone(), words.clone()) for _ in range(copies)]
+    else:
+        operands = [(q, words)]
 
-    def step():
-        lowbit.gemm(wbits, q, qs, words, n, k, alpha, None, y, None, ws_group=ws_group)
+    def step(i=0):
+        qi, wi = operands[i % copies]
+        lowbit.gemm(wbits, qi, qs, wi, n, k, alpha, None, y, None, ws_group=ws_group)
 
     with torch.cuda.stream(stream):
         step()
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        for _ in range(100):
-            step()
+    graphs = []
+    for g0 in range(0, max(copies, 100), 100):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(g0, g0 + 100):
+                step(i)
+        graphs.append(graph)
+    passes = max(1, reps // (100 * len(graphs)))
     with torch.cuda.stream(stream):
-        graph.replay()
+        for graph in graphs:
+            graph.replay()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
-        for _ in range(reps // 100):
-            graph.replay()
+        for _ in range(passes):
+            for graph in graphs:
+                graph.replay()
         b.record(stream)
         torch.cuda.synchronize()
-    us = a.elapsed_time(b) * 1000 / (reps // 100 * 100)
+    us = a.elapsed_time(b) * 1000 / (passes * 100 * len(graphs))
+    del operands
     esz = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
     ops = 2 * m * n * k * parts
     nbytes = (m * k * parts + n * (-(-k * wbits // 8)) + esz[scale_dtype] * (alpha.numel() + parts * m)
               + esz[out_dtype] * m * n)
     t_roof = max(ops / (PEAK_INT8_TOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9))
-    return {"wbits": wbits, "parts": parts, "M": m, "N": n, "K": k, "ws_group": ws_group, "us": round(us, 3),
+    return {"wbits": wbits, "parts": parts, "M": m, "N": n, "K": k, "ws_group": ws_group, "cold": cold,
+            "us": round(us, 3),
             "tops": round(ops / us / 1e6, 2), "gbs": round(nbytes / us / 1e3, 1),
             "bound": "mfma" if ops / (PEAK_INT8_TOPS * 1e12) >= nbytes / (PEAK_HBM_GBS * 1e9) else "hbm",
             "roofline_frac": round(t_roof / (us * 1e-6), 4)}
@@ -216,10 +276,11 @@ def suite() -> None:
     cases += [("config4", w, 1, m, n, k, f16, f16) for w in (1, 2) for m in (1, 4, 16)
               for n, k in [(2560, 640), (1030, 640)]]
     cases += [("config4", w, 1, 16, 1024, 4096, f16, f16) for w in (1, 2)]
+    cases += [(name + "_cold", *rest) for name, *rest in cases if name == "config4"]
     cases += [("refshape_x3", w, 3, m, n, k, f32, f32) for w in (1, 2) for n, k, m in REF_SHAPES]
     for i, (name, w, p, m, n, k, sd, od) in enumerate(cases):
         row = _suite_case(w, p, m, n, k, scale_dtype=sd, out_dtype=od, seed=i,
-                          ws_group=128 if name.endswith("group128") else 0)
+                          ws_group=128 if name.endswith("group128") else 0, cold=name.endswith("_cold"))
         print(json.dumps({"case": name, **row}), flush=True)
 
 
@@ -278,6 +339,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-encoder", action="store_true",
                     help="skip the config-5 encoder figures (ms per 10-s clip) of the headline line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-peaks", action="store_true",
+                    help="skip the measured-peak microbenchmarks (int8 MFMA loop, 1 GiB copy)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (5 times); the known byte count "
                          "calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
@@ -289,9 +352,19 @@ def main(argv=None) -> int:
                     help="--encoder: skip the FP32 dense comparison (profiles then hold only the quantized encoder)")
     ap.add_argument("--suite", action="store_true",
                     help="only time BASELINE.json configs 2-4 and the reference's tuned shapes (one JSON line each)")
+    ap.add_argument("--case", default=None, metavar="BITS,P,M,N,K",
+                    help="only time one GEMM shape (fp16 scales and output, library-chosen configuration) for "
+                         "--steps launches; used for the rocprofv3 counter passes of the larger configs")
     args = ap.parse_args(argv)
     if args.suite:
         suite()
+        return 0
+    if args.case:
+        w, p, m, n, k = (int(v) for v in args.case.split(","))
+        import torch
+        row = _suite_case(w, p, m, n, k, scale_dtype=torch.float16, out_dtype=torch.float16, seed=0,
+                          reps=max(100, args.steps // 100 * 100))
+        print(json.dumps({"case": "gemm", **row}), flush=True)
         return 0
     if args.encoder:
         for case in args.encoder_cases.split(","):
@@ -345,6 +418,12 @@ def main(argv=None) -> int:
                      "algorithmic_bytes": BYTES, "ops": OPS},
         "eager_launch_us": round(eager_us, 3),
     }
+    if not args.no_peaks:
+        peaks = measured_peaks()
+        measured = peaks["mfma_i8_tops"] if bound == "mfma" else peaks["copy_gbs"]
+        line["roofline"]["measured_peak"] = measured
+        line["roofline"]["frac_of_measured"] = round(achieved / measured, 5)
+        line["measured_peaks"] = peaks
     if not args.no_encoder:
         # the metric's second part: ms per 10-s clip of the 24-layer encoder (config 5), one int8 part, HIP graph
         enc = {f"batch{b}": encoder_bench(b, 1, check_dense=False) for b in (1, 8)}

@@ -20,8 +20,12 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "kea_kernels" / "lib" / "libkea_hip.so"
-SOURCES = ["kea_gemm.hip", "kea_quantize.hip", "kea_encoder.hip", "kea_layout.cpp"]
+SOURCES = ["kea_gemm.hip", "kea_quantize.hip", "kea_encoder.hip", "kea_probe.hip", "kea_layout.cpp"]
 ARCH = "gfx950"
+# Per-source flags. The probe's loop keeps eight MFMA accumulators live across iterations; in the accumulator
+# (AGPR) form the register allocator shuffles them with accvgpr moves every iteration, which would be measured as
+# matrix-core time, so it selects the VGPR form of the MFMAs.
+SOURCE_FLAGS = {"kea_probe.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def hipcc() -> str:
@@ -38,7 +42,7 @@ def flags() -> list[str]:
 
 
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *flags()]
+    cmd = [hipcc(), *flags(), *SOURCE_FLAGS.get(src.name, [])]
     if src.suffix == ".cpp":
         cmd += ["-x", "c++"]  # host-only translation unit
     cmd += ["-c", str(src), "-o", str(obj)]
