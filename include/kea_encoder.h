@@ -29,6 +29,29 @@ int kea_relpos_attention(const float *qkv_dev, int64_t ld, const float *pos_dev,
                          const float *bias_u_dev, const float *bias_v_dev, float *out_dev, int64_t ldo,
                          int64_t batch, int64_t t, int heads, int head_dim, float scale, void *stream);
 
+/* kea_relpos_attention with a workspace that lets small grids split every (clip, query tile, head) over two key
+ * halves on two workgroups. Each half stores its unnormalised partial output O_s and its rows' softmax statistics
+ * (m_s, l_s) in the workspace; a second launch merges them into out:
+ *   out = (O0 exp(m0 - m) + O1 exp(m1 - m)) / (l0 exp(m0 - m) + l1 exp(m1 - m)),  m = max(m0, m1),
+ * which equals the unsplit attention up to FP32 rounding. With out == NULL the merge is left to
+ * kea_attention_merge_quantize, which quantizes the merged rows directly. kea_relpos_attention_workspace gives the
+ * workspace size: 0 where the split does not apply (t > 128, an odd number of 16-key tiles, or a grid that already
+ * fills the GPU); there workspace may be NULL, out is required and the call equals kea_relpos_attention. Same
+ * reference function as kea_relpos_attention (kk/ternary/fused_kernels.py:163-240). */
+int64_t kea_relpos_attention_workspace(int64_t batch, int64_t t, int heads);
+int kea_relpos_attention_ws(const float *qkv_dev, int64_t ld, const float *pos_dev, int64_t ldp,
+                            const float *bias_u_dev, const float *bias_v_dev, float *out_dev, int64_t ldo,
+                            int64_t batch, int64_t t, int heads, int head_dim, float scale, void *workspace_dev,
+                            int64_t workspace_bytes, void *stream);
+
+/* The P-part int8 quantization (as kea_quantize, f32 scales, no LayerNorm) of the attention output that a
+ * kea_relpos_attention_ws call with out == NULL left as two halves in `workspace_dev`: bitwise what kea_quantize
+ * gives on that call's merged out, without writing it. The same batch, t and heads as that call (the split must
+ * apply); q [parts][batch * t][ldq] (zero padded past heads * 128), qs [parts][batch * t]. The quantizer in front of
+ * the attention output projection (kk/ternary/row_fusion.py:121-152 quantizes the attention output for it). */
+int kea_attention_merge_quantize(const void *workspace_dev, int64_t workspace_bytes, int64_t batch, int64_t t,
+                                 int heads, int parts, int8_t *q_dev, int64_t ldq, float *qs_dev, void *stream);
+
 /* GLU + depthwise convolution (BatchNorm folded into w and bias by the caller):
  *   y[(b*T + t)*ldy + c] = bias[c] + sum_{j<kernel} w[c*kernel + j] * glu(b, t + j - kernel/2, c)
  *   glu(b, t, c) = x[(b*T + t)*ldx + c] * sigmoid(x[(b*T + t)*ldx + channels + c]), 0 outside [0, T).

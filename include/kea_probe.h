@@ -14,7 +14,8 @@ extern "C" {
 
 /* Dense int8 matrix-core loop: `blocks` workgroups of four wave64s, each wave issuing `iters` rounds of eight
  * independent v_mfma_i32_16x16x64_i8 (32768 int8 ops each) on register operands, then one int32 per thread to
- * `out` (blocks * 256 ints, so the work is not dead code). Ops per launch: blocks * 4 * iters * 8 * 32768.
+ * `out` (blocks * 256 ints: the wrapping sum of the thread's accumulator elements, so the work is not dead code and
+ * its result can be checked). Ops per launch: blocks * 4 * iters * 8 * 32768.
  * blocks in [1, 65536], iters in [1, 1 << 20]. */
 int kea_probe_mfma_i8(int64_t blocks, int64_t iters, int32_t *out, void *stream);
 

@@ -12,6 +12,7 @@
 #include <string>
 
 #include "kea_internal.h"
+#include "kea_merge.h"
 #include "kea_wave.h"
 #include "../../include/kea_encoder.h"
 
@@ -203,36 +204,41 @@ __device__ __forceinline__ void wave_sum_n(float *v) {
 // Every wave's score tiles (content tiles w, w + NW, ..., then position tiles w, w + NW, ...) run as one list whose
 // next operand loads are issued before the current tile's MFMAs; the V operands are loaded at the start and consumed
 // last. 8 waves halve a workgroup's serial MFMA work for grids too small to fill the CUs (batch 1).
-template <int NKT, int NW>
+template <int NKT, int NW, int SPLIT>
 __global__ void __launch_bounds__(NW * 64)
 relpos_attention_mfma_kernel(const float *qkv, long long ld, const float *pos, long long ldp, const float *bias_u,
-                             const float *bias_v, float *out, long long ldo, int T, int H, float scale) {
+                             const float *bias_v, float *out, long long ldo, int T, int H, float scale,
+                             kea::SplitWs ws) {
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
-    constexpr int DK = 128, KP = 16 * NKT, NPT = NKT + 1, KS = KP / 4, RPW = 16 / NW, VC = 128 / NW / 16;
+    static_assert(SPLIT == 1 || (SPLIT == 2 && NKT % 2 == 0), "two key halves need an even number of key tiles");
+    constexpr int NKS = NKT / SPLIT;  // key tiles of this workgroup
+    constexpr int DK = 128, KP = 16 * NKS, NPT = NKS + 1, KS = KP / 4, RPW = 16 / NW, VC = 128 / NW / 16;
     constexpr int SP = KP + 4, BP = 16 * NPT + 4;  // padded LDS row strides (floats)
-    constexpr int NC = (NKT + NW - 1) / NW, NPOS = (NPT + NW - 1) / NW, NTASK = NC + NPOS;  // tiles per wave (max)
-    constexpr int QP = DK + 4;
+    constexpr int NC = (NKS + NW - 1) / NW, NPOS = (NPT + NW - 1) / NW, NTASK = NC + NPOS;  // tiles per wave (max)
+    constexpr int QP = DK + 4, KPL = (KP + 63) / 64;  // keys per lane in the softmax
     __shared__ __attribute__((aligned(16))) float Sc[16 * SP];
     __shared__ __attribute__((aligned(16))) float Bd[16 * BP];
     __shared__ __attribute__((aligned(16))) float Qu[16 * QP];
     __shared__ __attribute__((aligned(16))) float Qv[16 * QP];
+    __shared__ float row_m[16], row_l[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, g = lane >> 4;
-    // blockIdx.x is the head: consecutive workgroups go to different XCDs, so the query tiles of one head share an
-    // XCD and its L2 serves their K, V and position rows after the first fetch
-    const int b = blockIdx.z, h = blockIdx.x, i0 = blockIdx.y * 16;
+    // blockIdx.x is the head: consecutive workgroups go to different XCDs, so the query tiles (and key halves) of one
+    // head share an XCD and its L2 serves their K, V and position rows after the first fetch
+    const int b = blockIdx.z, h = blockIdx.x, qt = blockIdx.y / SPLIT, half = blockIdx.y % SPLIT, i0 = qt * 16;
+    const int j0 = half * KP;  // first key of this workgroup
     const float *qbase = qkv + (long long)b * T * ld + (long long)h * DK;
     const float *kbase = qbase + (long long)H * DK, *vbase = qbase + 2LL * H * DK;
 
     // This wave's score tiles: task i < nc is content tile wave + NW i, then position tile wave + NW (i - nc).
     // DEPTH operand buffers: every tile's loads up front with 8 waves (at most 3 tiles a wave), one ahead with 4.
     constexpr int DEPTH = NW == 8 ? NTASK : 2;
-    const int nc = max(NKT - wave + NW - 1, 0) / NW, npos = max(NPT - wave + NW - 1, 0) / NW;
-    const int rbase = T - 1 - (i0 + 15);  // relative row of band position 0
+    const int nc = max(NKS - wave + NW - 1, 0) / NW, npos = max(NPT - wave + NW - 1, 0) / NW;
+    const int rbase = T - 1 - (i0 + 15) + j0;  // relative row of this workgroup's band position 0
     float kb[DEPTH][32];
     auto load_task = [&](int i, float *dst) {
         const bool content = i < nc;
         const int tile = wave + NW * (content ? i : i - nc);
-        const int row = content ? tile * 16 + li : rbase + tile * 16 + li;
+        const int row = content ? j0 + tile * 16 + li : rbase + tile * 16 + li;
         const bool valid = i < nc + npos && (content ? row < T : (row >= 0 && row <= 2 * T - 2));
         const float *src = content ? kbase + (long long)row * ld : pos + (long long)row * ldp + (long long)h * DK;
 #pragma unroll
@@ -246,11 +252,11 @@ relpos_attention_mfma_kernel(const float *qkv, long long ld, const float *pos, l
     for (int i = 0; i < DEPTH; ++i)
         if (i < NTASK) load_task(i, kb[i]);
 
-    // V operands of the output phase: V[KS g + s][(128 / NW) wave + VC li .. + VC - 1] (zero for keys >= T)
+    // V operands of the output phase: V[j0 + KS g + s][(128 / NW) wave + VC li .. + VC - 1] (zero for keys >= T)
     float vr[KS][VC];
 #pragma unroll
     for (int st = 0; st < KS; ++st) {
-        const int j = KS * g + st;
+        const int j = j0 + KS * g + st;
         const float *src = vbase + (long long)j * ld + (128 / NW) * wave + VC * li;
         if constexpr (VC == 2) {
             float2 v = make_float2(0.f, 0.f);
@@ -303,18 +309,19 @@ relpos_attention_mfma_kernel(const float *qkv, long long ld, const float *pos, l
     }
     __syncthreads();
 
-    // softmax: wave w owns rows RPW w .. RPW w + RPW - 1 (reduced together); lane takes keys lane, lane + 64
+    // softmax over this workgroup's keys: wave w owns rows RPW w .. RPW w + RPW - 1 (reduced together); lane takes
+    // keys lane, lane + 64. One workgroup per row normalises; a key half keeps exp(s - max) and the row statistics.
     {
-        float sv[RPW][2], mx[RPW], sum[RPW];
+        float sv[RPW][KPL], mx[RPW], sum[RPW];
 #pragma unroll
         for (int rr = 0; rr < RPW; ++rr) {
             const int i = RPW * wave + rr;
             mx[rr] = -INFINITY;
 #pragma unroll
-            for (int n = 0; n < 2; ++n) {
+            for (int n = 0; n < KPL; ++n) {
                 const int j = lane + 64 * n;
                 sv[rr][n] = -INFINITY;
-                if (j < KP && j < T) sv[rr][n] = (Sc[i * SP + j] + Bd[i * BP + j + 15 - i]) * scale;
+                if (j < KP && j0 + j < T) sv[rr][n] = (Sc[i * SP + j] + Bd[i * BP + j + 15 - i]) * scale;
                 mx[rr] = fmaxf(mx[rr], sv[rr][n]);
             }
         }
@@ -323,7 +330,7 @@ relpos_attention_mfma_kernel(const float *qkv, long long ld, const float *pos, l
         for (int rr = 0; rr < RPW; ++rr) {
             sum[rr] = 0.f;
 #pragma unroll
-            for (int n = 0; n < 2; ++n) {
+            for (int n = 0; n < KPL; ++n) {
                 sv[rr][n] = expf(sv[rr][n] - mx[rr]);
                 sum[rr] = sum[rr] + sv[rr][n];
             }
@@ -332,11 +339,15 @@ relpos_attention_mfma_kernel(const float *qkv, long long ld, const float *pos, l
 #pragma unroll
         for (int rr = 0; rr < RPW; ++rr) {
             const int i = RPW * wave + rr;
-            const float inv = 1.0f / sum[rr];
+            const float inv = SPLIT == 1 ? 1.0f / sum[rr] : 1.0f;
 #pragma unroll
-            for (int n = 0; n < 2; ++n) {
+            for (int n = 0; n < KPL; ++n) {
                 const int j = lane + 64 * n;
-                if (j < KP) Sc[i * SP + j] = sv[rr][n] * inv;
+                if (j < KP) Sc[i * SP + j] = SPLIT == 1 ? sv[rr][n] * inv : sv[rr][n];
+            }
+            if (SPLIT > 1 && lane == 0) {
+                row_m[i] = mx[rr];
+                row_l[i] = sum[rr];
             }
         }
     }
@@ -358,14 +369,29 @@ relpos_attention_mfma_kernel(const float *qkv, long long ld, const float *pos, l
         for (int c = 0; c < VC; ++c) acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[st][c], pa[st], acc[c], 0, 0, 0);
     // lane holds rows j = 4 g + r for query q = li: column (128 / NW) w + VC (4 g + r) + c
     const int t = i0 + li;
-    if (t < T) {
-        float *o = out + ((long long)b * T + t) * ldo + (long long)h * DK + (128 / NW) * wave + 4 * VC * g;
-        if constexpr (VC == 2) {
-            *(float4 *)o = make_float4(acc[0][0], acc[VC - 1][0], acc[0][1], acc[VC - 1][1]);
-            *(float4 *)(o + 4) = make_float4(acc[0][2], acc[VC - 1][2], acc[0][3], acc[VC - 1][3]);
-        } else {
-            *(float4 *)o = make_float4(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
+    const long long col = (long long)h * DK + (128 / NW) * wave + 4 * VC * g;
+    float o[4 * VC];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < VC; ++c) o[VC * r + c] = acc[c][r];
+    if constexpr (SPLIT > 1) {
+        // this half's unnormalised partial and its rows' statistics; the consumer merges the halves
+        if (t < T) {
+            const long long rows = (long long)gridDim.z * T, row = (long long)b * T + t, hd = (long long)H * DK;
+            float *po = ws.o + ((long long)half * rows + row) * hd + col;
+#pragma unroll
+            for (int v = 0; v < VC; ++v)
+                *(float4 *)(po + 4 * v) = make_float4(o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]);
+            if (wave == 0 && g == 0)
+                *(float2 *)(ws.ml + (((long long)half * rows + row) * H + h) * 2) = make_float2(row_m[li], row_l[li]);
         }
+        return;
+    }
+    if (t < T) {
+        float *dst = out + ((long long)b * T + t) * ldo + col;
+#pragma unroll
+        for (int v = 0; v < VC; ++v) *(float4 *)(dst + 4 * v) = make_float4(o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]);
     }
 }
 
@@ -574,46 +600,85 @@ logmel_normalize_kernel(const float2 *spec, int bins, int frames, long long ld_t
     for (int t = th; t < frames; t += 256) yr[t] = (yr[t] - mean) * inv;
 }
 
-}  // namespace
+using kea::attention_splits;
 
-extern "C" {
+int64_t split_ws_bytes(int64_t batch, int64_t t, int heads) { return 4 * kea::split_ws_floats(batch * t, heads); }
 
-int kea_relpos_attention(const float *qkv, int64_t ld, const float *pos, int64_t ldp, const float *bias_u,
-                         const float *bias_v, float *out, int64_t ldo, int64_t batch, int64_t t, int heads,
-                         int head_dim, float scale, void *stream) {
-    if (batch < 0 || t < 1 || heads < 1 || head_dim != 128)
+// out[row][k] = the merged halves; one thread per four features.
+__global__ void __launch_bounds__(256)
+attention_merge_kernel(kea::SplitWs ws, long long rows, int heads, float *out, long long ldo) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x, per_row = (long long)heads * 32;
+    if (idx >= rows * per_row) return;
+    const long long row = idx / per_row;
+    const int k = (int)(idx - row * per_row) * 4;
+    float v[4];
+    kea::merged4(ws, rows, heads, row, k, v);
+    *(float4 *)(out + row * ldo + k) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+int attention(const float *qkv, int64_t ld, const float *pos, int64_t ldp, const float *bias_u, const float *bias_v,
+              float *out, int64_t ldo, int64_t batch, int64_t t, int heads, int head_dim, float scale, void *ws,
+              int64_t ws_bytes, void *stream) {
+    if (batch < 0 || t < 1 || heads < 1 || head_dim != 128 || batch > 65535 || heads > 65535)
         return kea::fail(KEA_EINVAL, "bad sizes (head_dim must be 128)");
     if (t > kMaxT) return kea::fail(KEA_EINVAL, "sequence longer than 256 frames: use the unfused attention");
     if (batch == 0) return KEA_OK;
-    if (!qkv || !pos || !bias_u || !bias_v || !out) return kea::fail(KEA_EINVAL, "null pointer");
-    if (ld < 3LL * heads * head_dim || ldp < (int64_t)heads * head_dim || ldo < (int64_t)heads * head_dim)
+    const bool split = ws && attention_splits(batch, t, heads);
+    if (!qkv || !pos || !bias_u || !bias_v || (!out && !split)) return kea::fail(KEA_EINVAL, "null pointer");
+    if (ld < 3LL * heads * head_dim || ldp < (int64_t)heads * head_dim || (out && ldo < (int64_t)heads * head_dim))
         return kea::fail(KEA_EINVAL, "leading dimension too small");
     if (((uintptr_t)qkv | (uintptr_t)pos | (uintptr_t)out | (uintptr_t)bias_u | (uintptr_t)bias_v) & 15 ||
         (ld | ldp | ldo) & 3)
         return kea::fail(KEA_EALIGN, "qkv, pos, out and the biases need 16-byte aligned rows");
     if (t <= 128) {
         const int nkt = (int)((t + 15) / 16);
-        const dim3 grid((unsigned)heads, (unsigned)((t + 15) / 16), (unsigned)batch);
+        kea::SplitWs sw{nullptr, nullptr};
+        if (split) {
+            if (ws_bytes < split_ws_bytes(batch, t, heads))
+                return kea::fail(KEA_ESPACE, "attention workspace too small: need " +
+                                                 std::to_string(split_ws_bytes(batch, t, heads)) + " bytes");
+            if ((uintptr_t)ws & 15) return kea::fail(KEA_EALIGN, "attention workspace must be 16-byte aligned");
+            sw = kea::split_ws(ws, batch * t, heads);
+        }
+        const dim3 grid((unsigned)heads, (unsigned)(nkt * (split ? 2 : 1)), (unsigned)batch);
         void (*fn)(const float *, long long, const float *, long long, const float *, const float *, float *,
-                   long long, int, int, float) = nullptr;
+                   long long, int, int, float, kea::SplitWs) = nullptr;
         // 8 waves per workgroup when the grid leaves CUs idle (fewer workgroups than the 256 CUs)
         const bool wide = (long long)grid.x * grid.y * grid.z < 256;
-#define KEA_ATT(N) fn = wide ? relpos_attention_mfma_kernel<N, 8> : relpos_attention_mfma_kernel<N, 4>
-        switch (nkt) {
-            case 1: KEA_ATT(1); break;
-            case 2: KEA_ATT(2); break;
-            case 3: KEA_ATT(3); break;
-            case 4: KEA_ATT(4); break;
-            case 5: KEA_ATT(5); break;
-            case 6: KEA_ATT(6); break;
-            case 7: KEA_ATT(7); break;
-            default: KEA_ATT(8); break;
+#define KEA_ATT(N) fn = wide ? relpos_attention_mfma_kernel<N, 8, 1> : relpos_attention_mfma_kernel<N, 4, 1>
+#define KEA_ATT2(N) fn = relpos_attention_mfma_kernel<N, 8, 2>
+        if (split) {
+            switch (nkt) {
+                case 2: KEA_ATT2(2); break;
+                case 4: KEA_ATT2(4); break;
+                case 6: KEA_ATT2(6); break;
+                default: KEA_ATT2(8); break;
+            }
+        } else {
+            switch (nkt) {
+                case 1: KEA_ATT(1); break;
+                case 2: KEA_ATT(2); break;
+                case 3: KEA_ATT(3); break;
+                case 4: KEA_ATT(4); break;
+                case 5: KEA_ATT(5); break;
+                case 6: KEA_ATT(6); break;
+                case 7: KEA_ATT(7); break;
+                default: KEA_ATT(8); break;
+            }
         }
 #undef KEA_ATT
-        hipLaunchKernelGGL(fn, grid, dim3(wide ? 512 : 256), 0, (hipStream_t)stream, qkv, (long long)ld, pos,
-                           (long long)ldp, bias_u, bias_v, out, (long long)ldo, (int)t, heads, scale);
+#undef KEA_ATT2
+        hipLaunchKernelGGL(fn, grid, dim3(wide || split ? 512 : 256), 0, (hipStream_t)stream, qkv, (long long)ld, pos,
+                           (long long)ldp, bias_u, bias_v, out, (long long)ldo, (int)t, heads, scale, sw);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return kea::fail((int)e, std::string("attention launch failed: ") + hipGetErrorString(e));
+        if (split && out) {
+            const long long rows = batch * t, work = rows * heads * 32;
+            hipLaunchKernelGGL(attention_merge_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0,
+                               (hipStream_t)stream, sw, rows, heads, out, (long long)ldo);
+            e = hipGetLastError();
+            if (e != hipSuccess) return kea::fail((int)e, std::string("merge launch failed: ") + hipGetErrorString(e));
+        }
         return KEA_OK;
     }
     const int nk = (int)((t + 63) / 64), kp = 64 * nk;
@@ -630,6 +695,29 @@ int kea_relpos_attention(const float *qkv, int64_t ld, const float *pos, int64_t
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return kea::fail((int)e, std::string("attention launch failed: ") + hipGetErrorString(e));
     return KEA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kea_relpos_attention(const float *qkv, int64_t ld, const float *pos, int64_t ldp, const float *bias_u,
+                         const float *bias_v, float *out, int64_t ldo, int64_t batch, int64_t t, int heads,
+                         int head_dim, float scale, void *stream) {
+    return attention(qkv, ld, pos, ldp, bias_u, bias_v, out, ldo, batch, t, heads, head_dim, scale, nullptr, 0,
+                     stream);
+}
+
+int64_t kea_relpos_attention_workspace(int64_t batch, int64_t t, int heads) {
+    if (batch < 1 || t < 1 || heads < 1 || !attention_splits(batch, t, heads)) return 0;
+    return split_ws_bytes(batch, t, heads);
+}
+
+int kea_relpos_attention_ws(const float *qkv, int64_t ld, const float *pos, int64_t ldp, const float *bias_u,
+                            const float *bias_v, float *out, int64_t ldo, int64_t batch, int64_t t, int heads,
+                            int head_dim, float scale, void *workspace, int64_t workspace_bytes, void *stream) {
+    return attention(qkv, ld, pos, ldp, bias_u, bias_v, out, ldo, batch, t, heads, head_dim, scale, workspace,
+                     workspace_bytes, stream);
 }
 
 int kea_glu_dwconv(const float *x, int64_t ldx, const float *w, const float *bias, float *y, int64_t ldy,

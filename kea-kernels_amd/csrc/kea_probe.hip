@@ -27,10 +27,12 @@ __global__ void __launch_bounds__(256) mfma_i8_loop(int iters, int32_t *out) {
 #pragma unroll
         for (int c = 0; c < kProbeChains; ++c) acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[c], 0, 0, 0);
     }
-    int32_t s = 0;
+    uint32_t s = 0;  // wrapping sum
 #pragma unroll
-    for (int c = 0; c < kProbeChains; ++c) s += acc[c][0] + acc[c][1] + acc[c][2] + acc[c][3];
-    out[(int64_t)blockIdx.x * 256 + threadIdx.x] = s;
+    for (int c = 0; c < kProbeChains; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s += (uint32_t)acc[c][r];
+    out[(int64_t)blockIdx.x * 256 + threadIdx.x] = (int32_t)s;
 }
 
 bool probe_args_ok(int64_t blocks, int64_t iters) {

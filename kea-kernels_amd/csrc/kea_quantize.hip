@@ -21,6 +21,7 @@
 
 #include "kea_epilogue.h"
 #include "kea_internal.h"
+#include "kea_merge.h"
 #include "kea_wave.h"
 #include "../../include/kea_encoder.h"
 
@@ -293,6 +294,29 @@ norm_quantize_kernel(const float *x, long long ldx, int M, int K, const float *w
     quantize_parts<VPT, WPR>(z, K, parts, q, ldq, qs, M, m, th, red[rl], wave);
 }
 
+// The P-part quantization of the attention output rows that the key-split attention left as two halves: the merge
+// of kea_merge.h (the same bits the split attention's merge kernel writes), then quantize_parts. WPR waves per row
+// with the quantizer's rule (K = heads * 128).
+template <int VPT, int WPR>
+__global__ void __launch_bounds__(256)
+attention_merge_quantize_kernel(kea::SplitWs ws, long long rows, int heads, int parts, int8_t *q, long long ldq,
+                                float *qs) {
+    constexpr int RPB = 4 / WPR, TPR = 64 * WPR;
+    __shared__ float red[RPB][5][WPR];
+    const int th = threadIdx.x % TPR, rl = threadIdx.x / TPR, wave = th >> 6;
+    const long long m = (long long)blockIdx.x * RPB + rl;
+    if (m >= rows) return;  // whole rows leave together: the row's barriers stay matched
+    const int K = heads * 128;
+    float z[VPT][4];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int k0 = 4 * (th + TPR * i);
+        if (k0 < K) kea::merged4(ws, rows, heads, m, k0, z[i]);
+        else z[i][0] = z[i][1] = z[i][2] = z[i][3] = 0.f;
+    }
+    quantize_parts<VPT, WPR>(z, K, parts, q, ldq, qs, (int)rows, (int)m, th, red[rl], wave);
+}
+
 // GLU + depthwise convolution (as glu_dwconv_kernel, same operation order), SiLU, then the P-part quantization of the
 // row: the middle of the convolution module fused with the quantizer of the second pointwise convolution. One
 // workgroup (4 waves) per token row; thread th holds the channel chunks 4 * (th + 256 i) .. + 3 (C % 4 == 0).
@@ -549,6 +573,38 @@ extern "C" int kea_norm_quantize(const float *x, int64_t ldx, int64_t m, int64_t
 #undef KEA_NQ
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return kea::fail((int)e, std::string("norm_quantize launch failed: ") + hipGetErrorString(e));
+    return KEA_OK;
+}
+
+extern "C" int kea_attention_merge_quantize(const void *workspace, int64_t workspace_bytes, int64_t batch, int64_t t,
+                                            int heads, int parts, int8_t *q, int64_t ldq, float *qs, void *stream) {
+    if (parts < 1 || parts > 3) return kea::fail(KEA_EINVAL, "parts must be 1, 2 or 3");
+    if (batch < 1 || t < 1 || heads < 1 || heads > 32 || batch > 65535)
+        return kea::fail(KEA_EINVAL, "bad sizes (heads <= 32)");
+    if (!kea::attention_splits(batch, t, heads))
+        return kea::fail(KEA_EINVAL, "the key-split attention does not apply to this shape: no halves to merge");
+    const long long rows = batch * t, k = (long long)heads * 128;
+    if (rows > INT32_MAX) return kea::fail(KEA_EINVAL, "too many rows");
+    if (workspace_bytes < 4 * kea::split_ws_floats(rows, heads))
+        return kea::fail(KEA_ESPACE, "attention workspace too small");
+    if (ldq < k) return kea::fail(KEA_EINVAL, "leading dimension too small");
+    if (!workspace || !q || !qs) return kea::fail(KEA_EINVAL, "null pointer");
+    if ((uintptr_t)workspace & 15 || ((uintptr_t)q | (uintptr_t)ldq) & 3)
+        return kea::fail(KEA_EALIGN, "workspace needs 16-byte alignment, q rows 4-byte alignment");
+    const kea::SplitWs sw = kea::split_ws(const_cast<void *>(workspace), rows, heads);
+    const int wpr = k > 256 ? 4 : 1, vpt = (int)((k + 256 * wpr - 1) / (256 * wpr));
+    const dim3 grid((unsigned)((rows + 4 / wpr - 1) / (4 / wpr))), block(256);
+    hipStream_t st = (hipStream_t)stream;
+#define KEA_MQ(V, W)                                                                                             \
+    hipLaunchKernelGGL((attention_merge_quantize_kernel<V, W>), grid, block, 0, st, sw, rows, heads, parts, q,     \
+                       (long long)ldq, qs)
+    if (wpr == 1) KEA_MQ(1, 1);
+    else if (vpt <= 1) KEA_MQ(1, 4);
+    else if (vpt <= 2) KEA_MQ(2, 4);
+    else KEA_MQ(4, 4);
+#undef KEA_MQ
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("merge_quantize launch failed: ") + hipGetErrorString(e));
     return KEA_OK;
 }
 

@@ -50,6 +50,10 @@ SIGNATURES = {
     "kea_quantize": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _f32, _i32, _vp, _i64,
                             _vp, _i32, _vp]),
     "kea_relpos_attention": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _f32, _vp]),
+    "kea_relpos_attention_workspace": (_i64, [_i64, _i64, _i32]),
+    "kea_relpos_attention_ws": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _f32, _vp,
+                                       _i64, _vp]),
+    "kea_attention_merge_quantize": (_i32, [_vp, _i64, _i64, _i64, _i32, _i32, _vp, _i64, _vp, _vp]),
     "kea_glu_dwconv": (_i32, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
     "kea_norm_quantize": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _f32, _vp, _i64, _vp, _vp, _f32, _i32, _vp, _i64,
                                  _vp, _vp]),

@@ -222,19 +222,50 @@ def rel_shift(x: Tensor) -> Tensor:
 
 # --- fused HIP kernels (include/kea_encoder.h) ----------------------------------------------------------------------
 
-def relpos_attention(qkv: Tensor, pos: Tensor, bias_u: Tensor, bias_v: Tensor, heads: int) -> Tensor:
+def attention_workspace(batch: int, t: int, heads: int, device) -> Tensor | None:
+    """A zero-filled workspace for relpos_attention's key-split form at this shape, or None where it does not apply
+    (kea_relpos_attention_workspace). Reusable by every later call of the same shape that does not overlap it: the
+    kernel leaves its counters at zero."""
+    nbytes = _hip.lib().kea_relpos_attention_workspace(batch, t, heads)
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device) if nbytes > 0 else None
+
+
+def relpos_attention(qkv: Tensor, pos: Tensor, bias_u: Tensor, bias_v: Tensor, heads: int, *,
+                     workspace: Tensor | None = None, merged: bool = True) -> Tensor | None:
     """qkv [B, T, 3d] (rows contiguous), pos [2T-1, d] (W_pos of the relative encodings), biases [H, dk] ->
-    attention output [B, T, d] (kea_relpos_attention)."""
+    attention output [B, T, d] (kea_relpos_attention). With `workspace` (from attention_workspace) small grids split
+    the keys over two workgroups (kea_relpos_attention_ws); merged=False then leaves the two halves in the workspace
+    for attention_merge_quantize and returns None."""
     b, t, three_d = qkv.shape
     d = three_d // 3
-    out = torch.empty(b, t, d, device=qkv.device, dtype=torch.float32)
+    if not merged and workspace is None:
+        raise ValueError("merged=False needs the key-split workspace")
+    out = torch.empty(b, t, d, device=qkv.device, dtype=torch.float32) if merged else None
     if qkv.stride(2) != 1 or pos.stride(1) != 1 or qkv.stride(0) != t * qkv.stride(1):
         raise ValueError("qkv and pos need contiguous rows")
-    rc = _hip.lib().kea_relpos_attention(qkv.data_ptr(), qkv.stride(1), pos.data_ptr(), pos.stride(0),
-                                         bias_u.data_ptr(), bias_v.data_ptr(), out.data_ptr(), d, b, t, heads,
-                                         d // heads, 1.0 / math.sqrt(d // heads), _hip.stream_handle(qkv.device))
+    args = (qkv.data_ptr(), qkv.stride(1), pos.data_ptr(), pos.stride(0), bias_u.data_ptr(), bias_v.data_ptr(),
+            _hip.ptr(out), d, b, t, heads, d // heads, 1.0 / math.sqrt(d // heads))
+    if workspace is None:
+        rc = _hip.lib().kea_relpos_attention(*args, _hip.stream_handle(qkv.device))
+    else:
+        rc = _hip.lib().kea_relpos_attention_ws(*args, workspace.data_ptr(), workspace.numel(),
+                                                _hip.stream_handle(qkv.device))
     _hip.check(rc, "kea_relpos_attention")
     return out
+
+
+def attention_merge_quantize(workspace: Tensor, batch: int, t: int, heads: int, parts: int) -> tuple[Tensor, Tensor]:
+    """The P-part quantization (f32 scales) of the attention output a relpos_attention(..., merged=False) call left
+    in `workspace`: bitwise lowbit.quantize of the merged output (kea_attention_merge_quantize). Returns q int8
+    [parts, B*T, ldq] (zero padded to ldq = round_up(heads * 128, 16)) and qs [parts, B*T]."""
+    m, k = batch * t, heads * 128
+    ldq = -(-k // 16) * 16
+    q = torch.empty(parts, m, ldq, device=workspace.device, dtype=torch.int8)
+    qs = torch.empty(parts, m, device=workspace.device, dtype=torch.float32)
+    rc = _hip.lib().kea_attention_merge_quantize(workspace.data_ptr(), workspace.numel(), batch, t, heads, parts,
+                                                 q.data_ptr(), ldq, qs.data_ptr(), _hip.stream_handle(workspace.device))
+    _hip.check(rc, "kea_attention_merge_quantize")
+    return q, qs
 
 
 def glu_dwconv(x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
@@ -356,6 +387,7 @@ class FastConformerEncoder:
         self.sub = {k[len(p):]: dev(v) for k, v in weights.items() if k.startswith(p)}
         self.layers = []
         self._pos_cache: dict = {}
+        self._att_ws: dict = {}  # (batch, t) -> key-split attention workspace (or None)
         shapes = quantized_shapes(cfg)
         quantized = {}
         for layer in range(cfg.layers):
@@ -505,12 +537,30 @@ class FastConformerEncoder:
             self._pos_cache[t] = hit
         return hit
 
+    def _attention_ws(self, b: int, t: int) -> Tensor | None:
+        """The key-split attention workspace of this shape (None where the split does not apply), allocated on the
+        first forward of the shape (the eager warm-up, before any graph capture)."""
+        key = (b, t)
+        if key not in self._att_ws:
+            self._att_ws[key] = attention_workspace(b, t, self.cfg.heads, self.device)
+        return self._att_ws[key]
+
+    def _attention_quantized(self, qkv: Tensor, pos: Tensor, u: Tensor, v_bias: Tensor) -> tuple[Tensor, Tensor]:
+        """The attention output as the P-part input of the output projection. Where the key split applies its two
+        halves are merged inside the quantizer (the merged FP32 output is never written)."""
+        b, t, _ = qkv.shape
+        ws = self._attention_ws(b, t) if self.cfg.d_model // self.cfg.heads == 128 else None
+        if ws is None:
+            return self._quantize(self.attention(qkv, pos, u, v_bias))
+        relpos_attention(qkv, pos, u, v_bias, self.cfg.heads, workspace=ws, merged=False)
+        return attention_merge_quantize(ws, b, t, self.cfg.heads, self.parts)
+
     def attention(self, qkv: Tensor, pos: Tensor, u: Tensor, v_bias: Tensor) -> Tensor:
         b, t, _ = qkv.shape
         h = self.cfg.heads
         dk = self.cfg.d_model // h
         if self.fused and t <= 256 and dk == 128:
-            return relpos_attention(qkv, pos, u, v_bias, h)
+            return relpos_attention(qkv, pos, u, v_bias, h, workspace=self._attention_ws(b, t))
         pos_t = pos.view(2 * t - 1, h, dk).permute(1, 2, 0).contiguous()  # [H, dk, 2t-1]
         q, k, v = qkv.view(b, t, 3, h, dk).unbind(2)
         qu = (q + u).transpose(1, 2).contiguous()                                   # [B, H, T, dk]
@@ -574,8 +624,8 @@ class FastConformerEncoder:
         y = self._gemm(pre + "feed_forward1.linear1", *xq, m, silu=True)
         xq = self._block(pre + "feed_forward1.linear2", *self._quantize(y), x, 0.5, norm=fp["norm_self_att"])
         qkv = self._gemm(pre + "self_attn.qkv", *xq, m).view(b, t, -1)
-        att = self.attention(qkv, pos, fp["u"], fp["v"])
-        xq = self._block(pre + "self_attn.linear_out", *self._quantize(att), x, 1.0, norm=fp["norm_conv"])
+        xq = self._block(pre + "self_attn.linear_out", *self._attention_quantized(qkv, pos, fp["u"], fp["v"]), x, 1.0,
+                         norm=fp["norm_conv"])
         u = self._gemm(pre + "conv.pointwise_conv1", *xq, m, glu=True).view(b, t, -1)   # GLU in the epilogue
         xq = self._block(pre + "conv.pointwise_conv2", *dwconv_quantize(u, fp["dw_w"], fp["dw_b"], self.parts),
                          x, 1.0, norm=fp["norm_feed_forward2"])

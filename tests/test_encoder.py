@@ -11,6 +11,7 @@ import torch
 import torch.nn.functional as F
 
 from kea_kernels import encoder as E
+from oracle import oracle as O
 
 
 def test_rel_shift_matches_the_relative_index():
@@ -99,6 +100,77 @@ def test_encoder_graph_replays_equal_eager():
         torch.cuda.synchronize()
         torch.testing.assert_close(got, eager, rtol=0, atol=0)
         _ = enc(audio)  # eager work between replays
+
+
+def _attention_inputs(b, t, h=8, dk=128):
+    g = torch.Generator().manual_seed(b * 1000 + t)
+    qkv = torch.randn(b, t, 3 * h * dk, generator=g)
+    pos = torch.randn(2 * t - 1, h * dk, generator=g)
+    u, v = torch.randn(h, dk, generator=g) * 0.1, torch.randn(h, dk, generator=g) * 0.1
+    return qkv, pos, u, v
+
+
+def _attention_fp64(qkv, pos, u, v, h=8, dk=128):
+    b, t, _ = qkv.shape
+    q, k, vv = qkv.double().view(b, t, 3, h, dk).unbind(2)
+    qu = (q + u.double()).transpose(1, 2)
+    qv = (q + v.double()).transpose(1, 2)
+    ac = qu @ k.permute(0, 2, 3, 1)
+    bd = E.rel_shift(qv @ pos.double().view(2 * t - 1, h, dk).permute(1, 2, 0))
+    a = torch.softmax((ac + bd) / math.sqrt(dk), dim=-1)
+    return (a @ vv.transpose(1, 2)).transpose(1, 2).reshape(b, t, h * dk)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,t", [(1, 125), (1, 32), (2, 96), (1, 64), (2, 128), (1, 17)])
+@torch.inference_mode()
+def test_key_split_attention_matches_fp64(b, t):
+    """The key-split form (two workgroups per (clip, query tile, head), halves merged by a second launch): the same
+    FP64 bar as the unsplit kernel, the same result on repeated calls over one workspace, and within FP32 rounding of
+    the unsplit kernel."""
+    h = 8
+    qkv, pos, u, v = _attention_inputs(b, t)
+    ws = E.attention_workspace(b, t, h, "cuda")
+    assert ws is not None and ws.numel() > 0
+    dq, dp, du, dv = qkv.cuda(), pos.cuda(), u.cuda(), v.cuda()
+    ref = _attention_fp64(qkv, pos, u, v)
+    outs = [E.relpos_attention(dq, dp, du, dv, h, workspace=ws) for _ in range(2)]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    got = outs[0].cpu().double()
+    assert float((got - ref).abs().max() / ref.abs().max()) < 2e-6
+    unsplit = E.relpos_attention(dq, dp, du, dv, h).cpu().double()
+    assert float((got - unsplit).abs().max() / ref.abs().max()) < 2e-6
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,t,parts", [(1, 125, 1), (1, 125, 3), (2, 64, 2), (1, 17, 1)])
+@torch.inference_mode()
+def test_attention_merge_quantize_is_the_quantizer_of_the_merged_output(b, t, parts):
+    """Quantizing the two halves directly (the merged rows are never written) gives bitwise what the library's
+    quantizer and the oracle give on the merged output."""
+    h = 8
+    qkv, pos, u, v = _attention_inputs(b, t)
+    ws = E.attention_workspace(b, t, h, "cuda")
+    dq, dp, du, dv = qkv.cuda(), pos.cuda(), u.cuda(), v.cuda()
+    assert E.relpos_attention(dq, dp, du, dv, h, workspace=ws, merged=False) is None
+    q, qs = E.attention_merge_quantize(ws, b, t, h, parts)
+    merged = E.relpos_attention(dq, dp, du, dv, h, workspace=ws)  # same halves, merged by the merge kernel
+    lq, lqs, _ = E.lowbit.quantize(merged, (merged.stride(0), merged.stride(1), 1, t), b * t, h * 128, parts)
+    torch.cuda.synchronize()
+    assert torch.equal(q, lq) and torch.equal(qs, lqs)
+    rq, rqs = O.quantize(merged.cpu().numpy().reshape(b * t, h * 128), parts, ldq=q.shape[2])
+    assert np.array_equal(q.cpu().numpy(), rq) and np.array_equal(qs.cpu().numpy(), rqs)
+
+
+@pytest.mark.gpu
+def test_key_split_applies_only_to_small_even_grids():
+    L = E._hip.lib()
+    assert L.kea_relpos_attention_workspace(1, 125, 8) > 0
+    assert L.kea_relpos_attention_workspace(8, 125, 8) == 0      # 512 workgroups already fill the GPU
+    assert L.kea_relpos_attention_workspace(1, 40, 8) == 0       # three 16-key tiles
+    assert L.kea_relpos_attention_workspace(1, 200, 8) == 0      # the long-sequence kernel
+    assert E.attention_workspace(8, 125, 8, "cuda") is None
 
 
 @pytest.mark.gpu
