@@ -3,6 +3,7 @@ against its FP32 dense twin on the GPU (relative Frobenius error bars per part c
 from __future__ import annotations
 
 import copy
+import ctypes
 import math
 
 import numpy as np
@@ -163,14 +164,25 @@ def test_attention_merge_quantize_is_the_quantizer_of_the_merged_output(b, t, pa
     assert np.array_equal(q.cpu().numpy(), rq) and np.array_equal(qs.cpu().numpy(), rqs)
 
 
-@pytest.mark.gpu
 def test_key_split_applies_only_to_small_even_grids():
+    """Host-side rule and contract checks of the key-split attention (nothing is launched)."""
     L = E._hip.lib()
-    assert L.kea_relpos_attention_workspace(1, 125, 8) > 0
+    rows = 125
+    assert L.kea_relpos_attention_workspace(1, 125, 8) == 4 * (2 * rows * 8 * 128 + 2 * rows * 8 * 2)
+    assert L.kea_relpos_attention_workspace(2, 128, 8) > 0       # 2 x 8 x 8 x 2 = 256 workgroups
     assert L.kea_relpos_attention_workspace(8, 125, 8) == 0      # 512 workgroups already fill the GPU
     assert L.kea_relpos_attention_workspace(1, 40, 8) == 0       # three 16-key tiles
     assert L.kea_relpos_attention_workspace(1, 200, 8) == 0      # the long-sequence kernel
     assert E.attention_workspace(8, 125, 8, "cuda") is None
+    need = L.kea_relpos_attention_workspace(1, 125, 8)
+    q = ctypes.c_void_p(16)
+    assert L.kea_attention_merge_quantize(q, need, 1, 125, 8, 4, q, 1024, q, None) == -1            # parts
+    assert L.kea_attention_merge_quantize(q, need, 8, 125, 8, 1, q, 1024, q, None) == -1            # no split
+    assert L.kea_attention_merge_quantize(q, need - 4, 1, 125, 8, 1, q, 1024, q, None) == -4        # workspace
+    assert L.kea_attention_merge_quantize(q, need, 1, 125, 8, 1, q, 1000, q, None) == -1            # ldq < k
+    assert L.kea_attention_merge_quantize(ctypes.c_void_p(8), need, 1, 125, 8, 1, q, 1024, q, None) == -2
+    assert L.kea_relpos_attention_ws(q, 3072, q, 1024, q, q, q, 1024, 1, 125, 8, 128, 1.0, q, need - 4, None) == -4
+    assert L.kea_relpos_attention_ws(q, 3072, q, 1024, q, q, None, 1024, 8, 125, 8, 128, 1.0, None, 0, None) == -1
 
 
 @pytest.mark.gpu
