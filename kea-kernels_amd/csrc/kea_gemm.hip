@@ -19,10 +19,10 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <type_traits>
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <type_traits>
 
 #include "kea_epilogue.h"
 #include "kea_internal.h"
@@ -247,6 +247,32 @@ __device__ __forceinline__ void epilogue4(const Params &p, int m, int nb, const 
 #pragma unroll
         for (int c = 0; c < P; ++c)
             store_int4(p.acc + ((long long)c * p.M + m) * p.acc_ld + nb, p.acc_vec, nb, p.N, a[c]);
+    }
+}
+
+// epilogue4 for a plain output (no GLU pairs, no raw accumulators) of compile-time dtype DT whose 4 columns are all
+// inside N with a vector-aligned y: the same values, one vector store, no per-lane selection.
+template <int P, int DT>
+__device__ __forceinline__ void epilogue4_full(const Params &p, int m, int nb, const int (*a)[4],
+                                               const EpiOperands &e) {
+    float v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        int ar[3] = {a[0][r], P > 1 ? a[1][r] : 0, P > 2 ? a[2][r] : 0};
+        v[r] = finish(combine<P>(ar, e.s, p.flags), e.alpha[r], p.bias != nullptr, e.bias[r], p.flags);
+        if (p.res) v[r] = e.res[r] + v[r] * p.res_factor;
+    }
+    const long long off = (long long)m * p.ldy + nb;
+    if constexpr (DT == KEA_F32) {
+        *(float4 *)((float *)p.y + off) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+        uint16_t h[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h[r] = DT == KEA_F16 ? to_f16_bits(v[r]) : to_bf16_bits(v[r]);
+        uint2 packed;
+        packed.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+        packed.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+        *(uint2 *)((uint16_t *)p.y + off) = packed;
     }
 }
 
@@ -679,39 +705,59 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     compute(nst - 1, masked_t{});
 
     // ---- epilogue: the MFMA result row is the weight row n, the column the activation row m ----
+    // DT >= 0: the output dtype as a compile-time constant; then 16x16 tiles wholly inside [M, N) take a path without
+    // per-lane bounds or dtype selection (the tile test is wave-uniform). DT < 0: the general epilogue.
+    auto epilogue = [&](auto dt_tag) {
+        constexpr int DT = decltype(dt_tag)::value;
 #pragma unroll
-    for (int i = 0; i < RM; ++i) {
-        const int m = m0 + (wm * RM + i) * 16 + (lane & 15);
-        if (m >= p.M) continue;
+        for (int i = 0; i < RM; ++i) {
+            const int mt = m0 + (wm * RM + i) * 16, m = mt + (lane & 15);
+            if (m >= p.M) continue;
 #pragma unroll
-        for (int jn = 0; jn < RN; ++jn) {
-            const int nb = n0 + (wn * RN + jn) * 16 + (lane >> 4) * 4;
-            if (nb >= p.N) continue;
-            int a[P][4];
-#pragma unroll
-            for (int c = 0; c < P; ++c)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) a[c][r] = acc[c][i][jn][r];
-            if constexpr (SLICED) {
+            for (int jn = 0; jn < RN; ++jn) {
+                const int nt = n0 + (wn * RN + jn) * 16, nb = nt + (lane >> 4) * 4;
+                if (nb >= p.N) continue;
+                int a[P][4];
 #pragma unroll
                 for (int c = 0; c < P; ++c)
-                    store_int4(p.slices + (((long long)blockIdx.z * P + c) * p.M + m) * p.N + nb, p.slice_vec, nb,
-                               p.N, a[c]);
-            } else {
-                EpiOperands e = cols[jn];
 #pragma unroll
-                for (int c = 0; c < 3; ++c) e.s[c] = rows[i].s[c];
-                if constexpr (RES_PREFETCH) {
+                    for (int r = 0; r < 4; ++r) a[c][r] = acc[c][i][jn][r];
+                if constexpr (SLICED) {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) e.res[r] = resv[i][jn][r];
+                    for (int c = 0; c < P; ++c)
+                        store_int4(p.slices + (((long long)blockIdx.z * P + c) * p.M + m) * p.N + nb, p.slice_vec,
+                                   nb, p.N, a[c]);
                 } else {
-                    load_residual(p, m, nb, e.res);
+                    EpiOperands e = cols[jn];
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) e.s[c] = rows[i].s[c];
+                    if constexpr (RES_PREFETCH) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) e.res[r] = resv[i][jn][r];
+                    } else {
+                        load_residual(p, m, nb, e.res);
+                    }
+                    if constexpr (GQ > 0) {
+                        epilogue4_groups<P>(p, m, nb, a, racc[i][jn], e);
+                    } else if constexpr (DT >= 0) {
+                        if (mt + 16 <= p.M && nt + 16 <= p.N) {
+                            epilogue4_full<P, DT>(p, m, nb, a, e);
+                            continue;
+                        }
+                        epilogue4<P>(p, m, nb, a, e);
+                    } else {
+                        epilogue4<P>(p, m, nb, a, e);
+                    }
                 }
-                if constexpr (GQ > 0) epilogue4_groups<P>(p, m, nb, a, racc[i][jn], e);
-                else epilogue4<P>(p, m, nb, a, e);
             }
         }
-    }
+    };
+    // plain outputs (no GLU pairs, no raw accumulators, vector-aligned y) branch once on the dtype
+    const bool plain = !SLICED && GQ == 0 && p.y && !p.acc && !(p.flags & KEA_FLAG_GLU) && p.y_vec;
+    if (plain && p.y_dtype == KEA_F16) epilogue(std::integral_constant<int, KEA_F16>{});
+    else if (plain && p.y_dtype == KEA_BF16) epilogue(std::integral_constant<int, KEA_BF16>{});
+    else if (plain && p.y_dtype == KEA_F32) epilogue(std::integral_constant<int, KEA_F32>{});
+    else epilogue(std::integral_constant<int, -1>{});
 }
 
 // Split-K finish: slices [S][P][M][N] summed in slice order (exact int32), then the epilogue of 4 columns.
