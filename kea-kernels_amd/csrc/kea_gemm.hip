@@ -953,17 +953,21 @@ int choose_tile(int wbits, int parts, long long m, long long n, long long k) {
 }
 
 // Split factor for split_k == 0: split K only for long K ranges (>= 2048) whose tiling leaves at most 64 workgroups,
-// by powers of two up to 8 slices and 256 workgroups; the split's second launch costs more than it saves otherwise.
+// by powers of two up to 8 slices and 256 workgroups (ternary, one part, K >= 4096: up to 128 workgroups, 512 after
+// the split); the split's second launch costs more than it saves otherwise.
 int choose_split(int wbits, int parts, long long m, long long n, long long k, int id) {
     const Tile &t = kTiles[id - 1];
     const long long bm = t.wm * t.rm * 16, bn = t.wn * t.rn * 16;
     const long long wgs = cdivl(m, bm) * cdivl(n, bn);
     const long long J = wbits == 1 ? cdivl(k, 128) : cdivl(k, 64);
     const long long quads = cdivl(J, 4);
-    (void)parts;
-    if (k < 2048 || wgs > 64) return 1;
+    // Ternary weights at one part and K >= 4096 carry twice the weight bytes per k: there four slices of a
+    // 128-workgroup tiling still pay (config 2: 8.1 -> 7.7 us); elsewhere a tiling above 64 workgroups runs unsplit.
+    const bool wide = wbits == 2 && parts == 1 && k >= 4096 && wgs <= 128;
+    if (k < 2048 || (wgs > 64 && !wide)) return 1;
+    const long long cap = wide ? 512 : 256;
     long long s = 1;
-    while (s * 2 <= std::min<long long>(8, quads) && wgs * s * 2 <= 256) s *= 2;
+    while (s * 2 <= std::min<long long>(8, quads) && wgs * s * 2 <= cap) s *= 2;
     return (int)s;
 }
 
