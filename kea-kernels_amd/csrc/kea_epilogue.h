@@ -27,7 +27,17 @@ __device__ __forceinline__ float combine(const int *a, const float *s, int flags
     }
 }
 
-// Weight scale and bias, then the optional SiLU (kk/binary/kernels.py:73-93).
+// Weight scale and bias, then the optional SiLU (kk/binary/kernels.py:73-93): bias ? fma(r, alpha, bias) : r * alpha.
+// Both forms are one fma here: `b` is the bias, or kNoBias (-0.0f) for none, and fma(r, alpha, -0) is bitwise r * alpha
+// (the exact product plus -0 is the exact product, also when that is +0, -0, a denormal, an infinity or a NaN).
+constexpr float kNoBias = -0.0f;
+__device__ __forceinline__ float finish(float r, float alpha, float b, int flags) {
+    r = __builtin_fmaf(r, alpha, b);
+    if (flags & KEA_FLAG_SILU) r = r / (1.0f + expf(-r));
+    return r;
+}
+// The same value with the two cases as written (a select between the fma and the product). Small GEMM tiles keep
+// this form: their launches measured about 1% faster with it (instruction layout), the values are identical.
 __device__ __forceinline__ float finish(float r, float alpha, bool has_bias, float b, int flags) {
     r = has_bias ? __builtin_fmaf(r, alpha, b) : r * alpha;
     if (flags & KEA_FLAG_SILU) r = r / (1.0f + expf(-r));

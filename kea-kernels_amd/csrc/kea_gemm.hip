@@ -73,6 +73,7 @@ struct Params {
 
 using kea::combine;
 using kea::finish;
+using kea::kNoBias;
 using kea::load_scalar;
 
 // 1-bit: plane (4h + d) of a native word -> four int8 weights. Stored bits are inverted signs, so after the mask
@@ -221,7 +222,7 @@ __device__ __forceinline__ void load_col_scales(const Params &p, int nb, EpiOper
         load_col4(p.bias, p.bias_dtype, p.bias_vec, nb, p.N, e.bias);
     } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) e.bias[r] = 0.f;
+        for (int r = 0; r < 4; ++r) e.bias[r] = kNoBias;
     }
 }
 
@@ -251,20 +252,25 @@ __device__ __forceinline__ void epilogue4(const Params &p, int m, int nb, const 
 }
 
 // epilogue4 for a plain output (no GLU pairs, no raw accumulators) of compile-time dtype DT whose 4 columns are all
-// inside N with a vector-aligned y: the same values, one vector store, no per-lane selection.
-template <int P, int DT>
-__device__ __forceinline__ void epilogue4_full(const Params &p, int m, int nb, const int (*a)[4],
+// inside N with a vector-aligned y: the same values, one vector store at yrow + nb (yrow: the row's first element),
+// no per-lane selection. RES: the residual is applied (Params::res is set).
+template <int P, int DT, bool RES, bool SMALL>
+__device__ __forceinline__ void epilogue4_full(const Params &p, void *yrow, int nb, const int (*a)[4],
                                                const EpiOperands &e) {
     float v[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         int ar[3] = {a[0][r], P > 1 ? a[1][r] : 0, P > 2 ? a[2][r] : 0};
-        v[r] = finish(combine<P>(ar, e.s, p.flags), e.alpha[r], p.bias != nullptr, e.bias[r], p.flags);
-        if (p.res) v[r] = e.res[r] + v[r] * p.res_factor;
+        if constexpr (SMALL) {
+            v[r] = finish(combine<P>(ar, e.s, p.flags), e.alpha[r], p.bias != nullptr, e.bias[r], p.flags);
+            if (p.res) v[r] = e.res[r] + v[r] * p.res_factor;
+        } else {
+            v[r] = finish(combine<P>(ar, e.s, p.flags), e.alpha[r], e.bias[r], p.flags);
+            if constexpr (RES) v[r] = e.res[r] + v[r] * p.res_factor;
+        }
     }
-    const long long off = (long long)m * p.ldy + nb;
     if constexpr (DT == KEA_F32) {
-        *(float4 *)((float *)p.y + off) = make_float4(v[0], v[1], v[2], v[3]);
+        *(float4 *)((float *)yrow + nb) = make_float4(v[0], v[1], v[2], v[3]);
     } else {
         uint16_t h[4];
 #pragma unroll
@@ -272,7 +278,7 @@ __device__ __forceinline__ void epilogue4_full(const Params &p, int m, int nb, c
         uint2 packed;
         packed.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
         packed.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
-        *(uint2 *)((uint16_t *)p.y + off) = packed;
+        *(uint2 *)((uint16_t *)yrow + nb) = packed;
     }
 }
 
@@ -707,12 +713,15 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     // ---- epilogue: the MFMA result row is the weight row n, the column the activation row m ----
     // DT >= 0: the output dtype as a compile-time constant; then 16x16 tiles wholly inside [M, N) take a path without
     // per-lane bounds or dtype selection (the tile test is wave-uniform). DT < 0: the general epilogue.
-    auto epilogue = [&](auto dt_tag) {
+    constexpr bool SMALL = RM * RN <= 2;
+    auto epilogue = [&](auto dt_tag, auto res_tag) {
         constexpr int DT = decltype(dt_tag)::value;
+        constexpr bool RES = decltype(res_tag)::value;
 #pragma unroll
         for (int i = 0; i < RM; ++i) {
             const int mt = m0 + (wm * RM + i) * 16, m = mt + (lane & 15);
             if (m >= p.M) continue;
+            void *yrow = (int8_t *)p.y + (long long)m * p.ldy * (DT == KEA_F32 ? 4 : 2);
 #pragma unroll
             for (int jn = 0; jn < RN; ++jn) {
                 const int nt = n0 + (wn * RN + jn) * 16, nb = nt + (lane >> 4) * 4;
@@ -741,7 +750,7 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
                         epilogue4_groups<P>(p, m, nb, a, racc[i][jn], e);
                     } else if constexpr (DT >= 0) {
                         if (mt + 16 <= p.M && nt + 16 <= p.N) {
-                            epilogue4_full<P, DT>(p, m, nb, a, e);
+                            epilogue4_full<P, DT, RES, SMALL>(p, yrow, nb, a, e);
                             continue;
                         }
                         epilogue4<P>(p, m, nb, a, e);
@@ -754,10 +763,29 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     };
     // plain outputs (no GLU pairs, no raw accumulators, vector-aligned y) branch once on the dtype
     const bool plain = !SLICED && GQ == 0 && p.y && !p.acc && !(p.flags & KEA_FLAG_GLU) && p.y_vec;
-    if (plain && p.y_dtype == KEA_F16) epilogue(std::integral_constant<int, KEA_F16>{});
-    else if (plain && p.y_dtype == KEA_BF16) epilogue(std::integral_constant<int, KEA_BF16>{});
-    else if (plain && p.y_dtype == KEA_F32) epilogue(std::integral_constant<int, KEA_F32>{});
-    else epilogue(std::integral_constant<int, -1>{});
+    using kRes = std::true_type;
+    using kNoRes = std::false_type;
+    // Tiles of one or two 16x16 blocks per wave (the small-M shapes) keep one epilogue copy per dtype with the
+    // residual and bias tested at run time: separate copies measured slower there (config 1: 4.13 vs 4.27 us).
+    if constexpr (SMALL) {
+        if (plain && p.y_dtype == KEA_F16) epilogue(std::integral_constant<int, KEA_F16>{}, kNoRes{});
+        else if (plain && p.y_dtype == KEA_BF16) epilogue(std::integral_constant<int, KEA_BF16>{}, kNoRes{});
+        else if (plain && p.y_dtype == KEA_F32) epilogue(std::integral_constant<int, KEA_F32>{}, kNoRes{});
+        else epilogue(std::integral_constant<int, -1>{}, kNoRes{});
+        return;
+    }
+    if (plain && p.y_dtype == KEA_F16) {
+        if (p.res) epilogue(std::integral_constant<int, KEA_F16>{}, kRes{});
+        else epilogue(std::integral_constant<int, KEA_F16>{}, kNoRes{});
+    } else if (plain && p.y_dtype == KEA_BF16) {
+        if (p.res) epilogue(std::integral_constant<int, KEA_BF16>{}, kRes{});
+        else epilogue(std::integral_constant<int, KEA_BF16>{}, kNoRes{});
+    } else if (plain && p.y_dtype == KEA_F32) {
+        if (p.res) epilogue(std::integral_constant<int, KEA_F32>{}, kRes{});
+        else epilogue(std::integral_constant<int, KEA_F32>{}, kNoRes{});
+    } else {
+        epilogue(std::integral_constant<int, -1>{}, kNoRes{});
+    }
 }
 
 // Split-K finish: slices [S][P][M][N] summed in slice order (exact int32), then the epilogue of 4 columns.

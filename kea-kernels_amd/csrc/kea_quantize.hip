@@ -482,8 +482,8 @@ __global__ void __launch_bounds__(256) row_epilogue_kernel(RowParams rp) {
                 const int ar[3] = {a[i][0][e], P > 1 ? a[i][P > 1 ? 1 : 0][e] : 0,
                                    P > 2 ? a[i][P > 2 ? 2 : 0][e] : 0};
                 const float alpha = kea::load_scalar(rp.ws, rp.ws_dtype, n0 + e);
-                const float b = rp.bias ? kea::load_scalar(rp.bias, rp.bias_dtype, n0 + e) : 0.f;
-                float v = kea::finish(kea::combine<P>(ar, s, rp.flags), alpha, rp.bias != nullptr, b, rp.flags);
+                const float b = rp.bias ? kea::load_scalar(rp.bias, rp.bias_dtype, n0 + e) : kea::kNoBias;
+                float v = kea::finish(kea::combine<P>(ar, s, rp.flags), alpha, b, rp.flags);
                 if (rp.res) v = res[e] + v * rp.factor;
                 z[i][e] = v;
             }
