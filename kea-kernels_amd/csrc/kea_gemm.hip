@@ -293,7 +293,7 @@ __device__ __forceinline__ void epilogue4_groups(const Params &p, int m, int nb,
         for (int r = 0; r < 4; ++r) {
             float x = racc[r];
             if (p.bias) x = x + e.bias[r];
-            if (p.flags & KEA_FLAG_SILU) x = x / (1.0f + expf(-x));
+            if (p.flags & KEA_FLAG_SILU) x = kea::silu_epilogue(x);
             if (p.res) x = e.res[r] + x * p.res_factor;
             v[r] = x;
         }

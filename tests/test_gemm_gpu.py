@@ -174,10 +174,10 @@ def test_silu_epilogue_within_tolerance(out_dtype):
     assert_parity(case, y, acc, out_dtype=out_dtype, silu=True)
 
 
-@pytest.mark.parametrize("wbits", [1, 2])
+@pytest.mark.parametrize("wbits,parts", [(1, 2), (2, 2), (1, 1), (2, 1)])
 @torch.inference_mode()
-def test_every_tile_gives_identical_results(wbits):
-    case = Case(wbits, 2, 70, 200, 1152, seed=31, bias=True)
+def test_every_tile_gives_identical_results(wbits, parts):
+    case = Case(wbits, parts, 70, 200, 1152, seed=31 + parts, bias=True)
     ref = None
     for tile in range(1, kernels.tile_count() + 1):
         y, acc = case.run(config=kernels.GemmConfig(tile=tile, split=1))
