@@ -11,6 +11,8 @@
  *   - Functions return KEA_OK (0) on success, a negative KEA_E* code for a contract violation (nothing is
  *     launched), or a positive hipError_t when the HIP runtime refused a launch. kea_last_error() returns a
  *     thread-local message describing the last failure of the calling thread.
+ *   - A call whose grid would exceed one dispatch (2^32 work-items along a grid dimension) fails with KEA_EINVAL
+ *     ("too large for one launch") instead of being truncated: split it along M (or N for the GEMM).
  *
  * Reference interfaces replaced (paths relative to the reference checkout, kk/ = src/kea_kernels/):
  *   kea_lowbit_gemm    <- the NVRTC kernel entry `b1_dot_*` (kk/binary/kernels.py:556-565) launched by

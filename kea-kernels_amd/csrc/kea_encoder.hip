@@ -683,6 +683,7 @@ int attention(const float *qkv, int64_t ld, const float *pos, int64_t ldp, const
     }
     const int nk = (int)((t + 63) / 64), kp = 64 * nk;
     const size_t lds = sizeof(float) * (size_t)(2 * kQB * head_dim + kQB * kp + (kQB - 1 + kp) * (head_dim + 4));
+    if (!kea::fits_dispatch((t + kQB - 1) / kQB, 256)) return kea::fail(KEA_EINVAL, "too large for one launch");
     const dim3 grid((unsigned)((t + kQB - 1) / kQB), (unsigned)heads, (unsigned)batch);
     auto fn = nk == 1 ? relpos_attention_kernel<128, 1> : nk == 2 ? relpos_attention_kernel<128, 2>
             : nk == 3 ? relpos_attention_kernel<128, 3> : relpos_attention_kernel<128, 4>;
@@ -760,6 +761,7 @@ int kea_dwconv2d_s2(const float *x, const float *in_bias, const float *w, const 
     if (!x || !w || !bias || !y) return kea::fail(KEA_EINVAL, "null pointer");
     const int h2 = (int)((h - 1) / 2 + 1), w2 = (int)((wd - 1) / 2 + 1);
     const long long total = batch * channels * (long long)h2 * w2;
+    if (!kea::fits_dispatch((total + 255) / 256, 256)) return kea::fail(KEA_EINVAL, "too large for one launch");
     hipLaunchKernelGGL(dwconv_s2_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x,
                        in_bias, w, bias, y, (int)channels, (int)h, (int)wd, h2, w2, total);
     hipError_t e = hipGetLastError();
@@ -774,6 +776,7 @@ int kea_bias_relu_flatten(const float *x, const float *bias, float *y, int64_t b
     if (batch == 0) return KEA_OK;
     if (!x || !bias || !y) return kea::fail(KEA_EINVAL, "null pointer");
     const long long total = batch * channels * h * wd;
+    if (!kea::fits_dispatch((total + 255) / 256, 256)) return kea::fail(KEA_EINVAL, "too large for one launch");
     hipLaunchKernelGGL(bias_relu_flatten_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, x, bias, y, (int)channels, (int)h, (int)wd, total);
     hipError_t e = hipGetLastError();

@@ -1148,6 +1148,9 @@ static int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ld
         if (lds_bytes > kLdsBudget)
             return kea::fail(KEA_EINVAL, "too many weight-scale groups for one workgroup's LDS: use a larger ws_group");
     }
+    if (!kea::fits_dispatch(cdivl(n, bn), t.wm * t.wn * 64) ||
+        (s > 1 && !kea::fits_dispatch(cdivl(m * cdivl(n, 4), 256), 256)))
+        return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N or M");
     dim3 grid((unsigned)cdivl(n, bn), (unsigned)cdivl(m, bm), (unsigned)s);
     dim3 block(t.wm * t.wn * 64);
     hipStream_t st = (hipStream_t)stream;
@@ -1234,6 +1237,8 @@ int kea_lowbit_gemm_slices(int wbits, const int8_t *q, int64_t part_stride, int6
     const StageShape shape = stage_shape(wbits, parts, t.rm, t.rn, t.wm, t.wn);
     const int nst = (int)cdivl(words_per_wg, shape.sw);
     const int lds_bytes = std::min(shape.ns, nst) * shape.stage_bytes;
+    if (!kea::fits_dispatch(cdivl(n, bn), t.wm * t.wn * 64))
+        return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N");
     KernelFn fn = pick_kernel(wbits, parts, tile, true, false);
     if (lds_bytes > 65536) {
         hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
@@ -1280,6 +1285,8 @@ int kea_lowbit_slices_finish(const int32_t *slices, int split, int parts, int64_
     p.ws_vec = ((uintptr_t)wscale % (ws_dtype == KEA_F16 ? 8 : 16)) == 0;
     p.bias_vec = bias && ((uintptr_t)bias % (bias_dtype == KEA_F16 ? 8 : 16)) == 0;
     const long long work = m * cdivl(n, 4);
+    if (!kea::fits_dispatch(cdivl(work, 256), 256))
+        return kea::fail(KEA_EINVAL, "too large for one launch: split the call along M");
     hipLaunchKernelGGL(pick_finish(parts), dim3((unsigned)cdivl(work, 256)), dim3(256), 0, (hipStream_t)stream, p, split);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return kea::fail((int)e, std::string("finish launch failed: ") + hipGetErrorString(e));

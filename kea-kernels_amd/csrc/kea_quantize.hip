@@ -522,6 +522,7 @@ extern "C" int kea_quantize(const void *x, int x_dtype, int64_t xb, int64_t xt, 
     const bool vec = xk == 1 && k % 4 == 0 && ldq % 4 == 0 && xb % 4 == 0 && xt % 4 == 0 &&
                      ((uintptr_t)x % (4 * esz)) == 0 && ((uintptr_t)q % 4) == 0 &&
                      (((uintptr_t)norm_w | (uintptr_t)norm_b) % 16) == 0;
+    if (!kea::fits_dispatch((m + 4 / wpr - 1) / (4 / wpr), 256)) return kea::fail(KEA_EINVAL, "too large for one launch: split the call along M");
     const dim3 grid((unsigned)((m + 4 / wpr - 1) / (4 / wpr))), block(256);
 #define KEA_Q(V, W)                                                                                                \
     do {                                                                                                           \
@@ -560,6 +561,7 @@ extern "C" int kea_norm_quantize(const float *x, int64_t ldx, int64_t m, int64_t
          (uintptr_t)norm1_b) & 15 || (ldx | ldo) & 3 || ((uintptr_t)q | (uintptr_t)ldq) & 3)
         return kea::fail(KEA_EALIGN, "rows and norm weights need 16-byte alignment, q rows 4-byte alignment");
     const int wpr = k > 256 ? 4 : 1, vpt = (int)((k + 256 * wpr - 1) / (256 * wpr));
+    if (!kea::fits_dispatch((m + 4 / wpr - 1) / (4 / wpr), 256)) return kea::fail(KEA_EINVAL, "too large for one launch: split the call along M");
     const dim3 grid((unsigned)((m + 4 / wpr - 1) / (4 / wpr))), block(256);
     hipStream_t st = (hipStream_t)stream;
 #define KEA_NQ(V, W)                                                                                             \
@@ -593,6 +595,7 @@ extern "C" int kea_attention_merge_quantize(const void *workspace, int64_t works
         return kea::fail(KEA_EALIGN, "workspace needs 16-byte alignment, q rows 4-byte alignment");
     const kea::SplitWs sw = kea::split_ws(const_cast<void *>(workspace), rows, heads);
     const int wpr = k > 256 ? 4 : 1, vpt = (int)((k + 256 * wpr - 1) / (256 * wpr));
+    if (!kea::fits_dispatch((rows + 4 / wpr - 1) / (4 / wpr), 256)) return kea::fail(KEA_EINVAL, "too large for one launch: split the call along M");
     const dim3 grid((unsigned)((rows + 4 / wpr - 1) / (4 / wpr))), block(256);
     hipStream_t st = (hipStream_t)stream;
 #define KEA_MQ(V, W)                                                                                             \
@@ -621,6 +624,7 @@ static int dwconv_quantize(bool glu, const float *x, int64_t ldx, const float *w
     if (((uintptr_t)x | (uintptr_t)bias) & 15 || ldx & 3 || ((uintptr_t)q | (uintptr_t)ldq) & 3)
         return kea::fail(KEA_EALIGN, "x rows and bias need 16-byte alignment, q rows 4-byte alignment");
     const int vpt = (int)((channels + 1023) / 1024);
+    if (!kea::fits_dispatch(t, 256)) return kea::fail(KEA_EINVAL, "too large for one launch: split the call along T");
     const dim3 grid((unsigned)t, (unsigned)batch), block(256);
     hipStream_t st = (hipStream_t)stream;
 #define KEA_GQ(V, W, G)                                                                                          \
@@ -690,6 +694,7 @@ extern "C" int kea_row_epilogue(const int32_t *slices, int split, int parts, int
     rp.nw = norm_w; rp.nb = norm_b; rp.eps = eps;
     rp.qparts = q_parts; rp.q = q; rp.ldq = ldq; rp.qsc = q_scales;
     const int wpr = n > 256 ? 4 : 1, vpt = (int)((n + 256 * wpr - 1) / (256 * wpr));
+    if (!kea::fits_dispatch((m + 4 / wpr - 1) / (4 / wpr), 256)) return kea::fail(KEA_EINVAL, "too large for one launch: split the call along M");
     const dim3 grid((unsigned)((m + 4 / wpr - 1) / (4 / wpr))), block(256);
     hipStream_t st = (hipStream_t)stream;
 #define KEA_RE(P_, V, W) hipLaunchKernelGGL((row_epilogue_kernel<P_, V, W>), grid, block, 0, st, rp)

@@ -134,6 +134,31 @@ def test_gemm_argument_validation_happens_before_any_launch():
     assert call(**base, ws_group=100) == -1
 
 
+def test_grids_past_one_dispatch_are_refused_before_any_launch():
+    """A dispatch holds each grid dimension as a 32-bit work-item count; launches past it would be truncated and
+    leave outputs unwritten, so the entry points refuse them (the checks run before any HIP call: the fake device
+    pointers below are never dereferenced)."""
+    L = _hip.lib()
+    fake, big = 4096, 2**31 - 1
+    # GEMM: N = 2^31 - 1 needs > 2^32 work-items along N for every tile
+    rc = L.kea_lowbit_gemm(1, fake, 0, 1024, 1, fake, 0, 0, fake, big, 1024, fake, 0, 0, None, 0, fake, 1, big,
+                           None, 0, 128, 0, 1, 0, None, 0, None)
+    assert rc == -1 and "too large for one launch" in _hip.last_error()
+    # the same N with M = 0 is an empty call, not an error
+    assert L.kea_lowbit_gemm(1, fake, 0, 1024, 1, fake, 0, 0, fake, big, 1024, fake, 0, 0, None, 0, fake, 1, big,
+                             None, 0, 0, 0, 1, 0, None, 0, None) == 0
+    # split-K finish over M x N / 4 lanes
+    rc = L.kea_lowbit_slices_finish(fake, 2, 1, big, 4096, fake, 0, 0, fake, 0, None, 0, fake, 1, 4096, None, 0, 0,
+                                    None)
+    assert rc == -1 and "too large for one launch" in _hip.last_error()
+    # per-token quantizer: one workgroup per row at K > 256
+    rc = L.kea_quantize(fake, 0, 0, 1024, 1, big, big, 1024, 1, None, None, 1e-5, 0, fake, 1024, fake, 0, None)
+    assert rc == -1 and "too large for one launch" in _hip.last_error()
+    # the boundary: 2^24 rows of 256 work-items are one past the 32-bit count
+    assert L.kea_quantize(fake, 0, 0, 1024, 1, 2**24, 2**24, 1024, 1, None, None, 1e-5, 0, fake, 1024, fake, 0,
+                          None) == -1
+
+
 def test_tile_and_split_tables_are_pure_functions():
     L = _hip.lib()
     for (m, n, k) in [(128, 4096, 1024), (1000, 3072, 1024), (1, 2560, 640), (16, 1024, 4096)]:
