@@ -21,6 +21,19 @@ def _on(device: torch.device, *tensors: Tensor | None) -> None:
             raise ValueError(f"tensor on {t.device}, expected {device}")
 
 
+def _check_words(words: Tensor, n: int, k: int, wbits: int) -> None:
+    """The kernels read the whole native layout of an n x k matrix: refuse a buffer that does not hold it."""
+    if wbits not in (1, 2):
+        raise ValueError(f"wbits must be 1 or 2, got {wbits}")
+    L = _hip.lib()
+    need = (L.kea_b1_native_words if wbits == 1 else L.kea_t2_native_words)(n, k)
+    if need <= 0:
+        raise ValueError(f"bad weight shape {n} x {k}")
+    if not words.is_contiguous() or words.numel() * words.element_size() < 4 * need:
+        raise ValueError(f"words must be a contiguous buffer of the {need} native words of a {n} x {k} "
+                         f"{wbits}-bit matrix")
+
+
 def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscale: Tensor, bias: Tensor | None,
          y: Tensor | None = None, acc_out: Tensor | None = None, *, m: int | None = None, silu: bool = False,
          order: int = 0, config=None, ws_group: int = 0, residual: Tensor | None = None,
@@ -39,10 +52,13 @@ def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscal
         raise ValueError("q rows must be contiguous with row stride ldq")
     if qs.dim() != 2 or qs.shape[0] != parts or qs.shape[1] < m or qs.stride(1) != 1 or qs.dtype not in _SCALE_DTYPES:
         raise ValueError(f"qs must be f32/f16 [{parts}, >= {m}] with unit column stride")
-    if wscale.dtype not in _SCALE_DTYPES or not wscale.is_contiguous():
-        raise ValueError("weight scales must be contiguous f32 or f16")
+    groups = -(-k // ws_group) if ws_group > 0 else 1
+    if wscale.dtype not in _SCALE_DTYPES or not wscale.is_contiguous() or wscale.numel() < n * groups:
+        raise ValueError(f"weight scales must be contiguous f32 or f16 [{n}]" +
+                         (f" x {groups} groups" if ws_group > 0 else ""))
     if bias is not None and (bias.dtype not in _SCALE_DTYPES or not bias.is_contiguous() or bias.numel() != n):
         raise ValueError("bias must be contiguous f32 or f16 [N]")
+    _check_words(words, n, k, wbits)
     if y is None and acc_out is None:
         raise ValueError("nothing to compute: y and acc_out are both None")
     ny = n // 2 if glu else n
@@ -96,6 +112,7 @@ def gemm_slices(wbits: int, q: Tensor, words: Tensor, n: int, k: int, slices: Te
     if (slices.dtype != torch.int32 or slices.dim() != 4 or tuple(slices.shape[1:]) != (parts, m, n)
             or not slices.is_contiguous()):
         raise ValueError(f"slices must be contiguous int32 [S, {parts}, {m}, {n}]")
+    _check_words(words, n, k, wbits)
     _on(q.device, words, slices)
     tile = 0 if config is None or not hasattr(config, "tile") else int(config.tile)
     rc = _hip.lib().kea_lowbit_gemm_slices(wbits, q.data_ptr(), q.stride(0), ldq, parts, words.data_ptr(), n, k, m,

@@ -338,3 +338,30 @@ def test_product_path_has_no_cpu_fallback():
     y = torch.empty(4, 16)
     with pytest.raises((RuntimeError, ValueError, OSError)):
         lowbit.gemm(1, q, qs, words, 16, 16, torch.ones(16), None, y)
+
+
+def test_gemm_refuses_short_weight_and_scale_buffers():
+    """The launcher checks, before any C call, that the weight words hold the whole native layout of an n x k
+    matrix and that the weight scales cover every output column (and group): a short buffer would be read past its
+    end by the kernel."""
+    from kea_kernels import lowbit
+    m, n, k = 4, 64, 256
+    q = torch.zeros(1, m, k, dtype=torch.int8)
+    qs = torch.ones(1, m, dtype=torch.float16)
+    y = torch.empty(m, n, dtype=torch.float16)
+    for wbits in (1, 2):
+        words = torch.zeros(kernels.native_words(n, k, wbits), dtype=torch.int32)
+        alpha = torch.ones(n, dtype=torch.float16)
+        with pytest.raises(ValueError, match="native words"):
+            lowbit.gemm(wbits, q, qs, words[:-1], n, k, alpha, None, y)
+        with pytest.raises(ValueError, match="native words"):
+            lowbit.gemm(wbits, q, qs, words.view(-1, 4).t(), n, k, alpha, None, y)  # not contiguous
+        with pytest.raises(ValueError, match="weight scales"):
+            lowbit.gemm(wbits, q, qs, words, n, k, alpha[:-1], None, y)
+        with pytest.raises(ValueError, match="groups"):
+            lowbit.gemm(wbits, q, qs, words, n, k, alpha, None, y, ws_group=128)  # needs [n, 2]
+        slices = torch.empty(2, 1, m, n, dtype=torch.int32)
+        with pytest.raises(ValueError, match="native words"):
+            lowbit.gemm_slices(wbits, q, words[:-4], n, k, slices)
+    with pytest.raises(ValueError, match="wbits"):
+        lowbit.gemm(3, q, qs, words, n, k, alpha, None, y)
