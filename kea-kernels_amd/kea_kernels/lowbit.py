@@ -221,6 +221,17 @@ def quantize(x: Tensor, rows: tuple, m: int, k: int, parts: int, *, norm=None, i
     if input_activation not in ("", "silu"):
         raise ValueError(f"unsupported input activation {input_activation!r}")
     xb, xt, xk, t = rows
+    if m > 0:
+        if min(xb, xt, xk) < 0 or t < 1 or k < 1:
+            raise ValueError(f"row addressing {rows} needs non-negative strides, T >= 1 and k >= 1")
+        # the furthest element any row reads: the last row, or the last row of the last full batch before it
+        b_last, r_last = divmod(m - 1, t)
+        far = b_last * xb + r_last * xt
+        if b_last >= 1:
+            far = max(far, (b_last - 1) * xb + (t - 1) * xt)
+        far += (k - 1) * xk
+        if x.storage_offset() + far >= x.untyped_storage().nbytes() // x.element_size():
+            raise ValueError(f"rows {rows} x {m} rows x {k} features reach past the end of x's storage")
     ldq = round_up(k, 16) if ldq is None else ldq
     q = torch.empty(parts, m, ldq, device=x.device, dtype=torch.int8)
     qs = torch.empty(parts, m, device=x.device, dtype=qs_dtype)

@@ -365,3 +365,22 @@ def test_gemm_refuses_short_weight_and_scale_buffers():
             lowbit.gemm_slices(wbits, q, words[:-4], n, k, slices)
     with pytest.raises(ValueError, match="wbits"):
         lowbit.gemm(3, q, qs, words, n, k, alpha, None, y)
+
+
+def test_quantize_refuses_rows_past_the_input_storage():
+    """kea_quantize reads row r at x + (r // T) * XB + (r % T) * XT + kk * XK: the launcher refuses an addressing
+    whose furthest element lies past x's storage (or negative strides) before any C call."""
+    from kea_kernels import lowbit
+    x = torch.zeros(2, 5, 64)  # B = 2, T = 5, K = 64
+    rows = (x.stride(0), x.stride(1), x.stride(2), 5)
+    with pytest.raises(ValueError, match="past the end"):
+        lowbit.quantize(x, rows, 11, 64, 1)  # an 11th row
+    with pytest.raises(ValueError, match="past the end"):
+        lowbit.quantize(x, rows, 10, 65, 1)  # a 65th feature
+    with pytest.raises(ValueError, match="past the end"):
+        lowbit.quantize(x[1:], (320, 64, 1, 5), 6, 64, 1)  # the second batch's rows 0-4, then a missing batch
+    with pytest.raises(ValueError, match="non-negative"):
+        lowbit.quantize(x, (x.stride(0), -64, 1, 5), 10, 64, 1)
+    # a view's storage offset counts: the second batch alone has room for 5 rows, not 6
+    with pytest.raises(ValueError, match="past the end"):
+        lowbit.quantize(x[1], (0, 64, 1, 6), 6, 64, 1)
