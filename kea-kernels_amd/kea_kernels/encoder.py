@@ -222,6 +222,21 @@ def rel_shift(x: Tensor) -> Tensor:
 
 # --- fused HIP kernels (include/kea_encoder.h) ----------------------------------------------------------------------
 
+def _f32(name: str, t: Tensor | None, device, numel: int | None = None) -> None:
+    """The kernels read FP32 parameters as dense arrays of a known length on the launch device."""
+    if t is None:
+        return
+    if t.dtype != torch.float32 or t.device != device or not t.is_contiguous() or \
+            (numel is not None and t.numel() != numel):
+        what = f" of {numel} elements" if numel is not None else ""
+        raise ValueError(f"{name} must be a contiguous FP32 tensor{what} on {device}")
+
+
+def _f32_rows(name: str, t: Tensor, device) -> None:
+    if t.dtype != torch.float32 or t.device != device:
+        raise ValueError(f"{name} must be FP32 on {device}")
+
+
 def attention_workspace(batch: int, t: int, heads: int, device) -> Tensor | None:
     """A zero-filled workspace for relpos_attention's key-split form at this shape, or None where it does not apply
     (kea_relpos_attention_workspace). Reusable by every later call of the same shape that does not overlap it: the
@@ -243,6 +258,14 @@ def relpos_attention(qkv: Tensor, pos: Tensor, bias_u: Tensor, bias_v: Tensor, h
     out = torch.empty(b, t, d, device=qkv.device, dtype=torch.float32) if merged else None
     if qkv.stride(2) != 1 or pos.stride(1) != 1 or qkv.stride(0) != t * qkv.stride(1):
         raise ValueError("qkv and pos need contiguous rows")
+    if three_d % 3 or d % heads:
+        raise ValueError(f"qkv width {three_d} is not 3 x heads x head_dim for {heads} heads")
+    if pos.dim() != 2 or pos.shape[0] < 2 * t - 1 or pos.shape[1] < d:
+        raise ValueError(f"pos must be [>= {2 * t - 1}, >= {d}] (relative positions t-1 .. -(t-1))")
+    _f32_rows("qkv", qkv, qkv.device)
+    _f32_rows("pos", pos, qkv.device)
+    _f32("bias_u", bias_u, qkv.device, d)
+    _f32("bias_v", bias_v, qkv.device, d)
     args = (qkv.data_ptr(), qkv.stride(1), pos.data_ptr(), pos.stride(0), bias_u.data_ptr(), bias_v.data_ptr(),
             _hip.ptr(out), d, b, t, heads, d // heads, 1.0 / math.sqrt(d // heads))
     if workspace is None:
@@ -274,6 +297,9 @@ def glu_dwconv(x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
     c, kw = two_c // 2, weight.shape[-1]
     if x.stride(2) != 1 or x.stride(0) != t * x.stride(1) or not weight.is_contiguous():
         raise ValueError("x needs contiguous rows and a contiguous weight")
+    _f32_rows("x", x, x.device)
+    _f32("weight", weight, x.device, c * kw)
+    _f32("bias", bias, x.device, c)
     y = torch.empty(b, t, c, device=x.device, dtype=torch.float32)
     rc = _hip.lib().kea_glu_dwconv(x.data_ptr(), x.stride(1), weight.data_ptr(), _hip.ptr(bias), y.data_ptr(), c,
                                    b, t, c, kw, _hip.stream_handle(x.device))
@@ -289,6 +315,12 @@ def norm_quantize(x: Tensor, norm0, norm1, parts: int, *, out: Tensor | None = N
     ldq = lowbit.round_up(k, 16)
     if not x.is_contiguous() or (out is not None and (not out.is_contiguous() or out.shape != x.shape)):
         raise ValueError("x and out must be contiguous [B, T, K]")
+    _f32_rows("x", x, x.device)
+    if out is not None:
+        _f32_rows("out", out, x.device)
+    for name, v in (("norm0.weight", norm0.weight), ("norm0.bias", norm0.bias), ("norm1.weight", norm1.weight),
+                    ("norm1.bias", norm1.bias)):
+        _f32(name, v, x.device, k)
     out = torch.empty_like(x) if out is None else out
     q = torch.empty(parts, m, ldq, device=x.device, dtype=torch.int8)
     qs = torch.empty(parts, m, device=x.device, dtype=torch.float32)
@@ -307,6 +339,9 @@ def glu_dwconv_quantize(x: Tensor, weight: Tensor, bias: Tensor | None, parts: i
     c, kw = two_c // 2, weight.shape[-1]
     if x.stride(2) != 1 or x.stride(0) != t * x.stride(1) or not weight.is_contiguous():
         raise ValueError("x needs contiguous rows and a contiguous weight")
+    _f32_rows("x", x, x.device)
+    _f32("weight", weight, x.device, c * kw)
+    _f32("bias", bias, x.device, c)
     ldq = lowbit.round_up(c, 16)
     q = torch.empty(parts, b * t, ldq, device=x.device, dtype=torch.int8)
     qs = torch.empty(parts, b * t, device=x.device, dtype=torch.float32)
@@ -323,6 +358,9 @@ def dwconv_quantize(u: Tensor, weight: Tensor, bias: Tensor | None, parts: int) 
     kw = weight.shape[-1]
     if u.stride(2) != 1 or u.stride(0) != t * u.stride(1) or not weight.is_contiguous():
         raise ValueError("u needs contiguous rows and a contiguous weight")
+    _f32_rows("u", u, u.device)
+    _f32("weight", weight, u.device, c * kw)
+    _f32("bias", bias, u.device, c)
     ldq = lowbit.round_up(c, 16)
     q = torch.empty(parts, b * t, ldq, device=u.device, dtype=torch.int8)
     qs = torch.empty(parts, b * t, device=u.device, dtype=torch.float32)

@@ -388,3 +388,36 @@ def test_fused_logmel_matches_pytorch(b, samples):
     ref = (logmel - logmel.mean(2, keepdim=True)) / (logmel.std(2, keepdim=True) + 1e-5)
     assert got.shape == ref.shape
     assert float((got - ref).abs().max()) < 1e-4
+
+
+def test_fused_launchers_check_parameters_before_any_call():
+    """The encoder's fused-kernel launchers refuse, before any C call, parameters the kernels would read past: a
+    depthwise weight or bias not of C x KW / C elements, positions shorter than 2T - 1 rows, head biases not of d
+    elements, LayerNorm parameters not of K elements, and non-FP32 inputs."""
+    from kea_kernels import encoder as E
+    c, kw, t = 4, 9, 4
+    x = torch.zeros(1, t, 2 * c)
+    u = torch.zeros(1, t, c)
+    w, b = torch.zeros(c, 1, kw), torch.zeros(c)
+    for fn, inp in ((E.glu_dwconv, x), (lambda *a: E.glu_dwconv_quantize(*a, 1), x),
+                    (lambda *a: E.dwconv_quantize(*a, 1), u)):
+        with pytest.raises(ValueError, match="weight"):
+            fn(inp, torch.zeros(c - 1, 1, kw), b)
+        with pytest.raises(ValueError, match="bias"):
+            fn(inp, w, torch.zeros(c + 1))
+        with pytest.raises(ValueError, match="FP32"):
+            fn(inp.half(), w, b)
+    heads, d = 2, 256
+    qkv, pos = torch.zeros(1, t, 3 * d), torch.zeros(2 * t - 1, d)
+    bu = bv = torch.zeros(heads, d // heads)
+    with pytest.raises(ValueError, match="pos"):
+        E.relpos_attention(qkv, pos[:-1], bu, bv, heads)
+    with pytest.raises(ValueError, match="bias_u"):
+        E.relpos_attention(qkv, pos, bu[:1], bv, heads)
+    with pytest.raises(ValueError, match="heads"):
+        E.relpos_attention(qkv, pos, bu, bv, 3)
+    with pytest.raises(ValueError, match="qkv"):
+        E.relpos_attention(qkv.half(), pos, bu, bv, heads)
+    ln_k, ln_short = torch.nn.LayerNorm(d), torch.nn.LayerNorm(d - 1)
+    with pytest.raises(ValueError, match="norm1.weight"):
+        E.norm_quantize(torch.zeros(1, t, d), ln_k, ln_short, 1)
