@@ -101,7 +101,7 @@ def gpu_bench(steps: int, warmup: int):
     ms = start.elapsed_time(end)
     ms_per_step = ms / steps
 
-    # eager launch rate through the Python operator (host launch path included), for DESIGN.md only
+    # eager launch rate through the Python operator (host launch path included): reported beside the headline
     with torch.cuda.stream(stream):
         t0 = time.perf_counter()
         for _ in range(200):
@@ -381,8 +381,8 @@ def main(argv=None) -> int:
         print(json.dumps({"copy_bytes": src.numel() * 4, "launches": 5}), flush=True)
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path (the GEMM shards by clip; see "
-              "DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path (data-parallel serving would "
+              "shard by clip, one process per GPU). Run with --gpus 1.", file=sys.stderr)
         return 2
     if args.steps < 1:
         print("--steps must be >= 1", file=sys.stderr)
