@@ -197,6 +197,26 @@ def test_strided_output_rows_and_acc_only():
     assert_parity(case, None, acc)
 
 
+@pytest.mark.parametrize("wbits,k,split", [(1, 384, 1), (2, 384, 1), (1, 2048, 4), (2, 2048, 4)])
+@torch.inference_mode()
+def test_leading_rows_of_a_taller_q(wbits, k, split):
+    """m below q's row count, three parts: the part planes sit rows * ldq apart (a gap after each part's m rows) and
+    the scale rows `rows` apart. The m output rows match the oracle on the first m activation rows, bit for bit,
+    unsplit and split, and the output rows past m stay untouched."""
+    case = Case(wbits, 3, 40, 96, k, seed=45)
+    m, n = 25, 96
+    y = torch.full((40, n), float("nan"), device=DEV, dtype=torch.float16)
+    acc = torch.full((3, m, n), -7, device=DEV, dtype=torch.int32)
+    lowbit.gemm(wbits, case.dq, case.dqs, case.words, n, k, case.dalpha, None, y, acc, m=m,
+                config=kernels.GemmConfig(0, split))
+    torch.cuda.synchronize()
+    ref_acc = case.oracle_acc()[:, :m]
+    assert np.array_equal(acc.cpu().numpy(), ref_acc)
+    ref = O.epilogue(ref_acc, case.qs.float().numpy()[:, :m], case.alpha.float().numpy(), None)
+    assert np.array_equal(_gpu_bits(y[:m].cpu(), torch.float16), _bits(ref, torch.float16))
+    assert torch.isnan(y[m:]).all()
+
+
 @torch.inference_mode()
 def test_zero_rows_is_a_no_op():
     case = Case(1, 1, 4, 64, 128, seed=1)
