@@ -157,6 +157,18 @@ def test_output_and_scale_dtypes(out_dtype, scale_dtype):
     assert_parity(case, y, acc, out_dtype=out_dtype)
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("wbits,p", [(1, 1), (2, 3)])
+@torch.inference_mode()
+def test_split_k_finish_with_bias_and_output_dtypes(out_dtype, wbits, p):
+    """Split K = 4: the int32 slices are summed and finished by the separate epilogue kernel, which applies the bias
+    and writes f32 / bf16 (order 1 at three parts) bit for bit as the oracle."""
+    case = Case(wbits, p, 45, 300, 2048, seed=60 + p, scale_dtype=torch.float32, bias=True)
+    order = 1 if p == 3 else 0
+    y, acc = case.run(out_dtype=out_dtype, order=order, config=kernels.GemmConfig(0, 4))
+    assert_parity(case, y, acc, out_dtype=out_dtype, order=order)
+
+
 @pytest.mark.parametrize("wbits", [1, 2])
 @pytest.mark.parametrize("k", [1, 15, 17, 300, 1100])
 @torch.inference_mode()
