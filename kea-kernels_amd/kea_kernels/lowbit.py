@@ -7,6 +7,8 @@ reference does for its L2 workspace, kk/binary/layer.py:194-195) and enqueues ke
 """
 from __future__ import annotations
 
+import functools
+
 import torch
 from torch import Tensor
 
@@ -21,12 +23,17 @@ def _on(device: torch.device, *tensors: Tensor | None) -> None:
             raise ValueError(f"tensor on {t.device}, expected {device}")
 
 
+@functools.lru_cache(maxsize=256)
+def _native_words(wbits: int, n: int, k: int) -> int:
+    L = _hip.lib()
+    return (L.kea_b1_native_words if wbits == 1 else L.kea_t2_native_words)(n, k)
+
+
 def _check_words(words: Tensor, n: int, k: int, wbits: int) -> None:
     """The kernels read the whole native layout of an n x k matrix: refuse a buffer that does not hold it."""
     if wbits not in (1, 2):
         raise ValueError(f"wbits must be 1 or 2, got {wbits}")
-    L = _hip.lib()
-    need = (L.kea_b1_native_words if wbits == 1 else L.kea_t2_native_words)(n, k)
+    need = _native_words(wbits, n, k)
     if need <= 0:
         raise ValueError(f"bad weight shape {n} x {k}")
     if not words.is_contiguous() or words.numel() * words.element_size() < 4 * need:
