@@ -238,9 +238,10 @@ def _f32_rows(name: str, t: Tensor, device) -> None:
 
 
 def attention_workspace(batch: int, t: int, heads: int, device) -> Tensor | None:
-    """A zero-filled workspace for relpos_attention's key-split form at this shape, or None where it does not apply
-    (kea_relpos_attention_workspace). Reusable by every later call of the same shape that does not overlap it: the
-    kernel leaves its counters at zero."""
+    """A workspace for relpos_attention's key-split form at this shape, or None where it does not apply
+    (kea_relpos_attention_workspace). Each call writes both halves' partial outputs and row statistics before they
+    are merged, so the buffer is reusable by every later call of the same shape that does not overlap it (it is
+    zero-filled once here, which no call relies on)."""
     nbytes = _hip.lib().kea_relpos_attention_workspace(batch, t, heads)
     return torch.zeros(nbytes, dtype=torch.uint8, device=device) if nbytes > 0 else None
 
