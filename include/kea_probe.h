@@ -22,6 +22,28 @@ int kea_probe_mfma_i8(int64_t blocks, int64_t iters, int32_t *out, void *stream)
 /* The ops one kea_probe_mfma_i8 launch performs (0 for arguments it would reject). */
 int64_t kea_probe_mfma_i8_ops(int64_t blocks, int64_t iters);
 
+/* Launch floors of a GEMM-shaped grid: (n / bn) x (m / bm) workgroups of 256 threads, one per bm x bn output tile of
+ * an m x n x k low-bit GEMM, as kea_lowbit_gemm launches them. What each workgroup does:
+ *   KEA_PROBE_EMPTY    nothing (the dispatch and completion cost of the grid);
+ *   KEA_PROBE_LOADS    copies its tile's operand bytes into LDS - the bm activation rows of a (int8 [m][k], bm * k
+ *                      bytes) and the native 1-bit words of its bn weight columns (w, bn * k / 8 bytes) - every copy
+ *                      issued before the first wait, then waits for all of them;
+ *   KEA_PROBE_STORES   writes its bm x bn fp16 tile of y ([m][ldy]) with 8-byte stores (zeros);
+ *   KEA_PROBE_LOADS | KEA_PROBE_STORES  both, the stored values read back from the loaded bytes.
+ * Requirements: bm, bn multiples of 16 in [16, 256]; m, n multiples of bm, bn (<= 2^20); k a multiple of 128
+ * (<= 65536); bm * k + bn * k / 8 <= 160 KiB when loading; a, w 16-byte aligned; y 8-byte aligned, ldy >= n,
+ * ldy % 4 == 0. */
+/* Keeps the stream busy for `ns` nanoseconds (one wavefront spinning on the device's constant-rate wall clock, so
+ * it always ends): enqueued in front of a timed region, it lets the host finish submitting the region's work before
+ * the region's start event executes, so host submission latency stays out of the measurement. ns in [0, 1e8]. */
+int kea_probe_spin(int64_t ns, void *stream);
+
+#define KEA_PROBE_EMPTY 0
+#define KEA_PROBE_LOADS 1
+#define KEA_PROBE_STORES 2
+int kea_probe_floor(int kind, int64_t m, int64_t n, int64_t k, int bm, int bn, const int8_t *a, const uint32_t *w,
+                    uint16_t *y, int64_t ldy, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

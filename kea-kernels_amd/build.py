@@ -20,7 +20,9 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "kea_kernels" / "lib" / "libkea_hip.so"
-SOURCES = ["kea_gemm.hip", "kea_quantize.hip", "kea_encoder.hip", "kea_probe.hip", "kea_layout.cpp"]
+SOURCES = ["kea_gemm_ring_w1.hip", "kea_gemm_ring_w2.hip", "kea_gemm_wsplit_p1.hip", "kea_gemm_wsplit_p2.hip",
+           "kea_gemm_wsplit_p3.hip", "kea_gemm.hip", "kea_gemm_wsplit.hip", "kea_quantize.hip", "kea_encoder.hip",
+           "kea_probe.hip", "kea_layout.cpp"]
 ARCH = "gfx950"
 # Per-source flags. The probe's loop keeps eight MFMA accumulators live across iterations; in the accumulator
 # (AGPR) form the register allocator shuffles them with accvgpr moves every iteration, which would be measured as

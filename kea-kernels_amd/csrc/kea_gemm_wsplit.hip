@@ -1,0 +1,29 @@
+// Launcher of the wave-split low-bit GEMM (kernel instances: kea_gemm_wsplit_p1.hip .. _p3.hip).
+#include <hip/hip_runtime.h>
+
+#include "kea_gemm_wsplit.h"
+
+namespace kea {
+
+hipError_t wsplit_launch(const Params &p, int wbits, int parts, int tile, int s, int splits, bool sliced,
+                         hipStream_t stream) {
+    const WsplitTile &t = kWsplitTiles[tile];
+    // unmasked vector loads need whole k-step ranges in every workgroup and complete weight quads (or one word)
+    const int ksteps = (p.K + 63) / 64, words = wbits == 1 ? s / 2 : s;
+    const bool ragged = (p.K % 64) != 0 || ksteps % (t.nw * s) != 0 || (words > 1 && p.J % 4 != 0);
+    const WsplitFn fn = parts == 1 ? wsplit_pick_p1(wbits, tile, s, sliced, ragged)
+                      : parts == 2 ? wsplit_pick_p2(wbits, tile, s, sliced, ragged)
+                                   : wsplit_pick_p3(wbits, tile, s, sliced, ragged);
+    if (!fn) return hipErrorInvalidDeviceFunction;
+    const int lds = wsplit_lds_bytes(parts, t);
+    if (lds > 65536) {
+        const hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e != hipSuccess) return e;
+    }
+    const dim3 grid((unsigned)((p.N + t.nt * 16 - 1) / (t.nt * 16)), (unsigned)((p.M + t.rm * 16 - 1) / (t.rm * 16)),
+                    (unsigned)splits);
+    hipLaunchKernelGGL(fn, grid, dim3(t.nw * 64), lds, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace kea

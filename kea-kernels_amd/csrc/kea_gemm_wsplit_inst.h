@@ -1,0 +1,317 @@
+// Instances of the wave-split GEMM kernel for one activation part count (KEA_WSPLIT_P), included by
+// kea_gemm_wsplit_p1.hip .. _p3.hip so the part counts compile in parallel.
+//
+// Wave-split low-bit GEMM for small M on MI355X (gfx950): the same contract and epilogue as the LDS-ring kernel of
+// kea_gemm.hip (kk/binary/kernels.py:134-565, kk/ternary/fused_kernels.py:53-120), organised for launches whose time
+// is set by memory latency rather than by matrix-core throughput.
+//
+// One workgroup owns a BM x BN output tile (BM = 16 * RM rows, BN = 16 * NT columns) and a range of NW * S k-steps of
+// 64; wave w of its NW waves takes the S consecutive k-steps [w * S, (w + 1) * S) of that range. Each wave:
+//   * issues every load it needs at once, before any wait: its activation fragments (one 16-byte load per lane per
+//     k-step, the MFMA operand layout of 16 rows x 64 k), its weight words (one 32-bit word per lane per native word:
+//     2 k-steps at 1 bit, 1 at 2 bits; four consecutive words of a lane come with one 128-bit load) and the epilogue's
+//     scales (raw 32-bit words whose conversion waits until the epilogue);
+//   * expands each weight word once (v_and_b32 + v_perm_b32 per 4 weights) and feeds it to the RM row blocks x P parts
+//     of v_mfma_i32_16x16x64_i8, with the weights as the A operand (a lane ends with 4 consecutive columns of a row);
+//   * writes its int32 partial tile to LDS. After one barrier the tile's 16x16 blocks are shared out over the waves,
+//     each block summed over the NW partials in wave order (integer addition: exact) and finished by the epilogue.
+// Activations at k >= the end of the K range are zeroed at load, so the (valid, never garbage) weight words there
+// contribute nothing; rows past M are clamped to row M - 1 and columns past N to the last n-tile, and neither is
+// stored. SLICED: blockIdx.z is a K slice of steps_per_slice k-steps whose exact int32 sums go to the slices
+// [S][P][M][N] instead of the epilogue (the finish kernel adds them in slice order).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <type_traits>
+
+#include "kea_gemm_wsplit.h"
+
+#ifndef KEA_WSPLIT_P
+#error "define KEA_WSPLIT_P (1, 2 or 3) before including kea_gemm_wsplit_inst.h"
+#endif
+
+namespace {
+
+using namespace kea;
+
+// The aligned 32-bit word holding element i of an f32 or f16 vector (f16: the half is selected at conversion time).
+// The word lies inside the 4-byte block of an in-bounds element, so it never reaches past a page the vector touches.
+__device__ __forceinline__ uint32_t load_raw(const void *v, bool f16, long long i) {
+    const long long off = f16 ? (i * 2) & ~3LL : i * 4;
+    return *(const uint32_t *)((const char *)v + off);
+}
+__device__ __forceinline__ float raw_to_f32(uint32_t raw, bool f16, long long i) {
+    const float h = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw >> ((i & 1) * 16)));
+    return f16 ? h : __builtin_bit_cast(float, raw);
+}
+
+// RAGGED = false: the host guarantees that every wave's K range is whole (K % 64 == 0, the workgroup's range a
+// multiple of NW * S k-steps) and that its weight words lie in complete quads (J % 4 == 0 or one word per wave), so
+// every load is an unmasked vector load. RAGGED = true: loads from clamped addresses, masked to zero at k >= kend
+// (per byte, so K % 16 != 0 is covered).
+template <int WBITS, int P, int RM, int NT, int NW, int S, bool SLICED, bool RAGGED>
+__global__ void __launch_bounds__(NW * 64) wsplit_kernel(Params p) {
+    static_assert(WBITS == 2 || S % 2 == 0, "1-bit waves take whole words (two k-steps each)");
+    constexpr int KSW = WBITS == 1 ? 2 : 1;       // k-steps per native word
+    constexpr int WPW = S / KSW;                  // words per lane per n-tile for one wave
+    constexpr int BM = RM * 16, BN = NT * 16;
+    constexpr int NB = RM * NT;                   // 16x16 blocks of the tile
+    constexpr int UB = (NB + NW - 1) / NW;        // blocks one wave finishes
+    constexpr int PART = P * RM * NT * 256;       // int32 of one wave's partial tile in LDS
+    extern __shared__ __attribute__((aligned(16))) int32_t red[];  // [NW][P][RM][NT][64 lanes][4]
+
+    // The parameters the loads need, all read before the first load is issued: one kernel-argument round trip.
+    const int8_t *const q = p.q;
+    const uint32_t *const w = p.w;
+    const void *const qs = p.qs, *const ws = p.ws, *const bias = p.bias;
+    const long long part_stride = p.part_stride, ldq = p.ldq, qs_stride = p.qs_stride;
+    const int M = p.M, N = p.N, K = p.K, J = p.J, NTILES = p.NT, sps = p.steps_per_slice;
+    const bool qs16 = p.qs_dtype == KEA_F16, ws16 = p.ws_dtype == KEA_F16, b16 = p.bias_dtype == KEA_F16;
+    asm volatile("" ::"s"(q), "s"(w), "s"(qs), "s"(ws), "s"(bias), "s"(part_stride), "s"(ldq), "s"(qs_stride),
+                 "s"(M), "s"(N), "s"(K), "s"(J), "s"(NTILES), "s"(sps), "s"(p.qs_dtype), "s"(p.ws_dtype),
+                 "s"(p.bias_dtype));
+
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    const int ksteps = (K + 63) >> 6;
+    const int sa = SLICED ? (int)blockIdx.z * sps : 0;
+    const int sb = SLICED ? min(ksteps, sa + sps) : ksteps;
+    const int s0 = sa + wave * S;                 // this wave's first k-step
+    const int kend = min(K, sb * 64);
+
+    // ---- loads: weights, activations, epilogue scales, all issued before the first wait ----
+    uint32_t wv[NT][WPW];
+    {
+        const int j0 = s0 / KSW;
+#pragma unroll
+        for (int jn = 0; jn < NT; ++jn) {
+            const int t = min((n0 >> 4) + jn, NTILES - 1);
+            const uint32_t *tb = w + (long long)t * J * 64;
+            if constexpr (WPW == 1 || RAGGED) {
+                // general addressing: a short last quad has lane stride wq < 4; words past J load any valid word
+                // (their activations are zero)
+#pragma unroll
+                for (int u = 0; u < WPW; ++u) {
+                    const int j = min(j0 + u, J - 1), jq = j & ~3;
+                    const int wq = min(4, J - jq);
+                    wv[jn][u] = tb[jq * 64 + lane * wq + (j & 3)];
+                }
+            } else if constexpr (WPW == 2) {
+                const uint2 v = ((const uint2 *)(tb + (j0 >> 2) * 256 + lane * 4))[(j0 >> 1) & 1];
+                wv[jn][0] = v.x; wv[jn][1] = v.y;
+            } else {
+#pragma unroll
+                for (int g = 0; g < WPW / 4; ++g) {
+                    const uint4 v = *(const uint4 *)(tb + ((j0 >> 2) + g) * 256 + lane * 4);
+                    wv[jn][4 * g] = v.x; wv[jn][4 * g + 1] = v.y; wv[jn][4 * g + 2] = v.z; wv[jn][4 * g + 3] = v.w;
+                }
+            }
+        }
+    }
+    v4i af[P][RM][S];
+    {
+        const int kl = (lane >> 4) * 16;          // this lane's 16 bytes of each k-step
+#pragma unroll
+        for (int c = 0; c < P; ++c)
+#pragma unroll
+            for (int i = 0; i < RM; ++i) {
+                const int m = min(m0 + i * 16 + (lane & 15), M - 1);
+                const int8_t *row = q + c * part_stride + (long long)m * ldq;
+#pragma unroll
+                for (int t = 0; t < S; ++t) {
+                    const int k = (s0 + t) * 64 + kl;
+                    if constexpr (!RAGGED) {
+                        af[c][i][t] = *(const v4i *)(row + k);
+                    } else {
+                        // k < kend <= K <= ldq with ldq % 16 == 0: the 16 bytes lie in the row; else load the row start
+                        v4i v = *(const v4i *)(row + (k < kend ? k : 0));
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) {
+                            const int valid = kend - (k + 4 * d);  // bytes at k >= kend must not contribute
+                            const uint32_t keep =
+                                valid >= 4 ? 0xFFFFFFFFu : (valid <= 0 ? 0u : (1u << (8 * valid)) - 1u);
+                            v[d] = (int)((uint32_t)v[d] & keep);
+                        }
+                        af[c][i][t] = v;
+                    }
+                }
+            }
+    }
+    // epilogue scales of the blocks this wave finishes: raw words now, converted in the epilogue
+    uint32_t rs[UB][3], ra[UB][4], rb[UB][4];
+    if constexpr (!SLICED) {
+#pragma unroll
+        for (int u = 0; u < UB; ++u) {
+            const int b = min(wave + NW * u, NB - 1);
+            const int i = b / NT, jn = b - (b / NT) * NT;
+            const int m = min(m0 + i * 16 + (lane & 15), M - 1);
+#pragma unroll
+            for (int c = 0; c < 3; ++c) rs[u][c] = c < P ? load_raw(qs, qs16, c * qs_stride + m) : 0u;
+            const int nb = n0 + jn * 16 + (lane >> 4) * 4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ra[u][r] = load_raw(ws, ws16, min(nb + r, N - 1));
+            if (bias) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) rb[u][r] = load_raw(bias, b16, min(nb + r, N - 1));
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) rb[u][r] = 0u;
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first instruction that waits
+
+    // ---- MFMAs: straight-line code over the wave's S k-steps ----
+    v4i acc[P][RM][NT];
+#pragma unroll
+    for (int c = 0; c < P; ++c)
+#pragma unroll
+        for (int i = 0; i < RM; ++i)
+#pragma unroll
+            for (int jn = 0; jn < NT; ++jn) acc[c][i][jn] = (v4i){0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+        const int u = t / KSW, h = t % KSW;
+#pragma unroll
+        for (int jn = 0; jn < NT; ++jn) {
+            const uint32_t w32 = wv[jn][u];
+            v4i bf;
+            if constexpr (WBITS == 1) {
+                if (h == 0) {
+                    bf[0] = b1_expand<0>(w32); bf[1] = b1_expand<1>(w32); bf[2] = b1_expand<2>(w32); bf[3] = b1_expand<3>(w32);
+                } else {
+                    bf[0] = b1_expand<4>(w32); bf[1] = b1_expand<5>(w32); bf[2] = b1_expand<6>(w32); bf[3] = b1_expand<7>(w32);
+                }
+            } else {
+                const uint32_t w4 = w32 >> 4;
+                bf[0] = t2_lo(w32); bf[1] = t2_hi(w32); bf[2] = t2_lo(w4); bf[3] = t2_hi(w4);
+            }
+#pragma unroll
+            for (int c = 0; c < P; ++c)
+#pragma unroll
+                for (int i = 0; i < RM; ++i)
+                    acc[c][i][jn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af[c][i][t], acc[c][i][jn], 0, 0, 0);
+        }
+    }
+
+    // ---- exact reduction over the waves through LDS ----
+    {
+        int32_t *mine = red + wave * PART;
+#pragma unroll
+        for (int c = 0; c < P; ++c)
+#pragma unroll
+            for (int i = 0; i < RM; ++i)
+#pragma unroll
+                for (int jn = 0; jn < NT; ++jn) *(v4i *)(mine + ((c * RM + i) * NT + jn) * 256 + lane * 4) = acc[c][i][jn];
+    }
+    __syncthreads();
+
+    // ---- epilogue: block b = wave + NW * u of the tile ----
+    const bool plain = !SLICED && p.y && !p.acc && !p.res && !(p.flags & KEA_FLAG_GLU) && p.y_vec;
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+        const int b = wave + NW * u;
+        if (b >= NB) break;  // wave-uniform
+        const int i = b / NT, jn = b - (b / NT) * NT;
+        int a[P][4];
+#pragma unroll
+        for (int c = 0; c < P; ++c) {
+            const int32_t *src = red + ((c * RM + i) * NT + jn) * 256 + lane * 4;
+            v4i sum = *(const v4i *)src;
+#pragma unroll
+            for (int v = 1; v < NW; ++v) sum += *(const v4i *)(src + v * PART);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) a[c][r] = sum[r];
+        }
+        const int mt = m0 + i * 16, m = mt + (lane & 15);
+        const int nt = n0 + jn * 16, nb = nt + (lane >> 4) * 4;
+        if (m >= M || nb >= N) continue;
+        if constexpr (SLICED) {
+#pragma unroll
+            for (int c = 0; c < P; ++c)
+                store_int4(p.slices + (((long long)blockIdx.z * P + c) * M + m) * N + nb, p.slice_vec, nb, N, a[c]);
+        } else {
+            EpiOperands e;
+#pragma unroll
+            for (int c = 0; c < 3; ++c) e.s[c] = c < P ? raw_to_f32(rs[u][c], qs16, c * qs_stride + m) : 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int n = min(nb + r, N - 1);
+                e.alpha[r] = raw_to_f32(ra[u][r], ws16, n);
+                e.bias[r] = bias ? raw_to_f32(rb[u][r], b16, n) : kNoBias;
+            }
+            load_residual(p, m, nb, e.res);
+            if (plain && mt + 16 <= M && nt + 16 <= N) {
+                if (p.y_dtype == KEA_F16) {
+                    epilogue4_full<P, KEA_F16, false, true>(p, (uint16_t *)p.y + (long long)m * p.ldy, nb, a, e);
+                } else if (p.y_dtype == KEA_BF16) {
+                    epilogue4_full<P, KEA_BF16, false, true>(p, (uint16_t *)p.y + (long long)m * p.ldy, nb, a, e);
+                } else {
+                    epilogue4_full<P, KEA_F32, false, true>(p, (float *)p.y + (long long)m * p.ldy, nb, a, e);
+                }
+            } else {
+                epilogue4<P>(p, m, nb, a, e);
+            }
+        }
+    }
+}
+
+// Instances exist only for register budgets that fit (kea::wsplit_fits, checked by the host before any launch).
+template <int WBITS, int P, int RM, int NT, int NW, int S, bool SLICED, bool RAGGED>
+WsplitFn pick_fit() {
+    constexpr int words = WBITS == 1 ? S / 2 : S;
+    constexpr int regs = P * RM * S * 4 + NT * words + P * RM * NT * 4;
+    if constexpr (regs <= (NW == 4 ? 320 : 160) && NW * P * RM * NT * 1024 <= 160 * 1024)
+        return wsplit_kernel<WBITS, P, RM, NT, NW, S, SLICED, RAGGED>;
+    else
+        return nullptr;
+}
+
+template <int WBITS, int P, int RM, int NT, int NW, bool SLICED, bool RAGGED>
+WsplitFn pick_s(int s) {
+    switch (s) {
+        case 2: return pick_fit<WBITS, P, RM, NT, NW, 2, SLICED, RAGGED>();
+        case 4: return pick_fit<WBITS, P, RM, NT, NW, 4, SLICED, RAGGED>();
+        case 8: return pick_fit<WBITS, P, RM, NT, NW, 8, SLICED, RAGGED>();
+        default: return pick_fit<WBITS, P, RM, NT, NW, 16, SLICED, RAGGED>();
+    }
+}
+
+template <int WBITS, int P, bool SLICED, bool RAGGED>
+WsplitFn pick_tile(int tile, int s) {
+    switch (tile) {
+        case 0: return pick_s<WBITS, P, 1, 8, 4, SLICED, RAGGED>(s);
+        case 1: return pick_s<WBITS, P, 2, 4, 4, SLICED, RAGGED>(s);
+        case 2: return pick_s<WBITS, P, 1, 4, 4, SLICED, RAGGED>(s);
+        case 3: return pick_s<WBITS, P, 1, 8, 8, SLICED, RAGGED>(s);
+        case 4: return pick_s<WBITS, P, 2, 4, 8, SLICED, RAGGED>(s);
+        case 5: return pick_s<WBITS, P, 1, 2, 4, SLICED, RAGGED>(s);
+        case 6: return pick_s<WBITS, P, 2, 8, 4, SLICED, RAGGED>(s);
+        default: return pick_s<WBITS, P, 1, 4, 8, SLICED, RAGGED>(s);
+    }
+}
+
+template <int WBITS, int P>
+WsplitFn pick_flags(int tile, int s, bool sliced, bool ragged) {
+    if (sliced) return ragged ? pick_tile<WBITS, P, true, true>(tile, s) : pick_tile<WBITS, P, true, false>(tile, s);
+    return ragged ? pick_tile<WBITS, P, false, true>(tile, s) : pick_tile<WBITS, P, false, false>(tile, s);
+}
+
+}  // namespace
+
+namespace kea {
+
+#if KEA_WSPLIT_P == 1
+WsplitFn wsplit_pick_p1(int wbits, int tile, int s, bool sliced, bool ragged) {
+#elif KEA_WSPLIT_P == 2
+WsplitFn wsplit_pick_p2(int wbits, int tile, int s, bool sliced, bool ragged) {
+#else
+WsplitFn wsplit_pick_p3(int wbits, int tile, int s, bool sliced, bool ragged) {
+#endif
+    return wbits == 1 ? pick_flags<1, KEA_WSPLIT_P>(tile, s, sliced, ragged)
+                      : pick_flags<2, KEA_WSPLIT_P>(tile, s, sliced, ragged);
+}
+
+}  // namespace kea

@@ -1,4 +1,5 @@
-// Measurement helpers (include/kea_probe.h): a dense int8 matrix-core loop that measures the sustained MFMA rate.
+// Measurement helpers (include/kea_probe.h): a dense int8 matrix-core loop that measures the sustained MFMA rate, and
+// the launch floors of a GEMM-shaped grid (an empty kernel, and kernels that only move a GEMM tile's bytes).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -39,6 +40,69 @@ bool probe_args_ok(int64_t blocks, int64_t iters) {
     return blocks >= 1 && blocks <= 65536 && iters >= 1 && iters <= (1 << 20);
 }
 
+// ---- launch floors ------------------------------------------------------------------------------------------------
+// One workgroup of 256 threads per BM x BN output tile of an M x N x K GEMM, as the GEMM launches them. The data
+// kinds move exactly one GEMM tile's operand bytes: the BM activation rows (BM * K bytes) and the BN weight columns'
+// native 1-bit words (BN * K / 8 bytes, one contiguous range per tile) by direct global -> LDS copies, all issued
+// before the first wait; and/or the tile's fp16 outputs (BM * BN * 2 bytes) by 8-byte stores.
+struct FloorArgs {
+    const int8_t *a;
+    const uint8_t *w;
+    uint16_t *y;
+    long long ldy;
+    int k, bm, bn;
+    int a_units, w_units;  // 16-byte units per tile
+};
+
+typedef __attribute__((address_space(1))) const void *gptr_t;
+typedef __attribute__((address_space(3))) void *lptr_t;
+
+template <int KIND>
+__global__ void __launch_bounds__(256) floor_kernel(FloorArgs f) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    if constexpr (KIND == KEA_PROBE_EMPTY) {
+        return;
+    } else {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const int n0 = blockIdx.x * f.bn, m0 = blockIdx.y * f.bm;
+        if constexpr (KIND & KEA_PROBE_LOADS) {
+            const int row_units = f.k / 16;
+            const int8_t *abase = f.a + (long long)m0 * f.k;
+            const uint8_t *wbase = f.w + (long long)n0 * (f.k / 8);
+            // unit u of the tile: activation units first, then weight units; a wave's 64 lanes fill 1 KiB of LDS
+            for (int base = wave * 64; base < f.a_units + f.w_units; base += 256) {
+                const int u = base + lane;
+                if (u < f.a_units) {
+                    const int r = u / row_units, c = u - r * row_units;
+                    __builtin_amdgcn_global_load_lds((gptr_t)(abase + (long long)r * f.k + c * 16),
+                                                     (lptr_t)(lds + base * 16), 16, 0, 0);
+                } else if (u < f.a_units + f.w_units) {
+                    __builtin_amdgcn_global_load_lds((gptr_t)(wbase + (long long)(u - f.a_units) * 16),
+                                                     (lptr_t)(lds + base * 16), 16, 0, 0);
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0);  // every copy landed (vmcnt, expcnt, lgkmcnt all 0)
+            __syncthreads();
+        }
+        if constexpr (KIND & KEA_PROBE_STORES) {
+            const int groups = f.bn / 4, total = f.bm * groups;
+            const int lds_words = (f.a_units + f.w_units) * 2;  // 8-byte words in LDS (data kinds with loads)
+            for (int g = threadIdx.x; g < total; g += 256) {
+                const int r = g / groups, c = (g - r * groups) * 4;
+                uint2 v = make_uint2(0u, 0u);
+                if constexpr (KIND & KEA_PROBE_LOADS) v = ((const uint2 *)lds)[g % lds_words];
+                *(uint2 *)(f.y + (long long)(m0 + r) * f.ldy + n0 + c) = v;
+            }
+        }
+    }
+}
+
+// Spins one wavefront on the constant-rate wall clock (s_memrealtime) until `ticks` have passed: always ends.
+__global__ void __launch_bounds__(64) spin_kernel(unsigned long long ticks) {
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(4);
+}
+
 }  // namespace
 
 extern "C" {
@@ -56,6 +120,53 @@ int kea_probe_mfma_i8(int64_t blocks, int64_t iters, int32_t *out, void *stream)
     hipLaunchKernelGGL(mfma_i8_loop, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (int)iters, out);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_mfma_i8: ") + hipGetErrorString(e));
+    return 0;
+}
+
+int kea_probe_spin(int64_t ns, void *stream) {
+    if (ns < 0 || ns > 100000000LL) return kea::fail(KEA_EINVAL, "kea_probe_spin: ns must be in [0, 1e8]");
+    int dev = 0, khz = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
+    if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_spin: ") + hipGetErrorString(e));
+    if (khz <= 0) return kea::fail(KEA_ENODEV, "kea_probe_spin: the device reports no wall-clock rate");
+    const unsigned long long ticks = (unsigned long long)(ns * (long long)khz / 1000000LL);
+    hipLaunchKernelGGL(spin_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, ticks);
+    e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_spin: ") + hipGetErrorString(e));
+    return 0;
+}
+
+int kea_probe_floor(int kind, int64_t m, int64_t n, int64_t k, int bm, int bn, const int8_t *a, const uint32_t *w,
+                    uint16_t *y, int64_t ldy, void *stream) {
+    if (kind < KEA_PROBE_EMPTY || kind > (KEA_PROBE_LOADS | KEA_PROBE_STORES))
+        return kea::fail(KEA_EINVAL, "kea_probe_floor: kind must be 0 (empty), 1 (loads), 2 (stores) or 3 (both)");
+    if (bm < 16 || bm > 256 || bm % 16 || bn < 16 || bn > 256 || bn % 16)
+        return kea::fail(KEA_EINVAL, "kea_probe_floor: bm and bn must be multiples of 16 in [16, 256]");
+    if (m < bm || n < bn || k < 128 || m % bm || n % bn || k % 128 || m > (1 << 20) || n > (1 << 20) || k > (1 << 16))
+        return kea::fail(KEA_EINVAL, "kea_probe_floor: m, n must be multiples of bm, bn (<= 2^20) and k a multiple of "
+                                     "128 (<= 65536)");
+    const long long a_units = (long long)bm * k / 16, w_units = (long long)bn * k / 128;
+    const long long lds = (kind & KEA_PROBE_LOADS) ? (a_units + w_units) * 16 : 0;
+    if (lds > 160 * 1024) return kea::fail(KEA_EINVAL, "kea_probe_floor: bm * k + bn * k / 8 exceeds 160 KiB of LDS");
+    if ((kind & KEA_PROBE_LOADS) && (!a || !w || ((uintptr_t)a & 15) || ((uintptr_t)w & 15)))
+        return kea::fail(KEA_EINVAL, "kea_probe_floor: loads need 16-byte aligned a [m, k] and w (native words)");
+    if ((kind & KEA_PROBE_STORES) && (!y || ((uintptr_t)y & 7) || ldy < n || ldy % 4))
+        return kea::fail(KEA_EINVAL, "kea_probe_floor: stores need an 8-byte aligned fp16 y [m, ldy >= n], ldy % 4 == 0");
+    FloorArgs f = {a, (const uint8_t *)w, y, (long long)ldy, (int)k, bm, bn, (int)a_units, (int)w_units};
+    const dim3 grid((unsigned)(n / bn), (unsigned)(m / bm));
+    hipStream_t st = (hipStream_t)stream;
+    void (*fn)(FloorArgs) = kind == KEA_PROBE_EMPTY ? floor_kernel<KEA_PROBE_EMPTY>
+                          : kind == KEA_PROBE_LOADS ? floor_kernel<KEA_PROBE_LOADS>
+                          : kind == KEA_PROBE_STORES ? floor_kernel<KEA_PROBE_STORES>
+                                                     : floor_kernel<KEA_PROBE_LOADS | KEA_PROBE_STORES>;
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_floor: ") + hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(fn, grid, dim3(256), (size_t)lds, st, f);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_floor: ") + hipGetErrorString(e));
     return 0;
 }
 

@@ -88,6 +88,42 @@ def test_quantized_encoder_matches_dense_fp32(parts, tol):
     assert rel < tol, rel
 
 
+@pytest.fixture(scope="module")
+def config5_weights():
+    """The 24-layer synthetic model of BASELINE.json config 5 (random init, seed 5 as bench.py uses)."""
+    cfg = E.EncoderConfig()
+    return cfg, E.synthetic_weights(cfg, seed=5)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("parts,tol", [(1, 5e-2), (3, 5e-6)])
+@torch.inference_mode()
+def test_config5_full_encoder_matches_dense_fp32(config5_weights, parts, tol):
+    """Config 5 at its workload: 10 s of 16 kHz noise -> log-mel (1000 frames) -> 8x subsampling (125 frames) -> 24
+    FastConformer layers, batch 1 and batch 8, every linear 1-bit with P int8 activation parts, run as the HIP graph
+    the benchmark times. Bar: relative Frobenius error against the same model with FP32 dense linears. One int8
+    part carries ~2^-8 relative error per linear (the reference's one-part linear bar is 2e-2,
+    tests/test_kernels_gpu.py:47-57); through 24 residual layers the measured error is 3.0-3.2e-2, so the bar is
+    5e-2. Three parts carry ~2^-24 per linear, at the FP32 rounding of the dense twin itself (measured 7-10e-7): the
+    bar is 5e-6."""
+    cfg, w = config5_weights
+    assert cfg.layers == 24 and cfg.d_model == 1024
+    dense = E.FastConformerEncoder(w, cfg, "cuda", dense=True)
+    quant = E.FastConformerEncoder(w, cfg, "cuda", parts=parts)
+    for batch in (1, 8):
+        audio = torch.randn(batch, 160000, generator=torch.Generator().manual_seed(5 + batch)).cuda()
+        graph = E.EncoderGraph(quant, batch, 160000)
+        got = graph(audio).clone()
+        ref = dense(audio)
+        torch.cuda.synchronize()
+        assert got.shape == ref.shape == (batch, 125, 1024)
+        assert torch.isfinite(got).all()
+        rel = float((got.double() - ref.double()).norm() / ref.double().norm())
+        print(f"config5 parts={parts} batch={batch}: rel_err_vs_dense_fp32 = {rel:.3e}", flush=True)
+        assert rel < tol, (batch, rel)
+        del graph
+
+
 @pytest.mark.gpu
 @torch.inference_mode()
 def test_encoder_graph_replays_equal_eager():

@@ -22,6 +22,23 @@ def test_probe_arguments():
     assert L.kea_probe_mfma_i8(1, 1, None, None) == -1
 
 
+def test_floor_and_spin_probe_arguments():
+    """The launch-floor and spin probes refuse bad arguments before any launch (no GPU is touched)."""
+    L = _hip.lib()
+    vp = ctypes.c_void_p
+    assert L.kea_probe_floor(4, 128, 4096, 1024, 32, 32, None, None, None, 4096, None) == -1
+    assert b"kind" in L.kea_last_error()
+    assert L.kea_probe_floor(0, 128, 4096, 1024, 24, 32, None, None, None, 4096, None) == -1   # bm % 16
+    assert L.kea_probe_floor(0, 100, 4096, 1024, 32, 32, None, None, None, 4096, None) == -1   # m % bm
+    assert L.kea_probe_floor(0, 128, 4096, 1000, 32, 32, None, None, None, 4096, None) == -1   # k % 128
+    assert L.kea_probe_floor(1, 128, 4096, 1024, 32, 32, None, None, None, 4096, None) == -1   # loads need a, w
+    assert L.kea_probe_floor(2, 128, 4096, 1024, 32, 32, None, None, None, 4096, None) == -1   # stores need y
+    assert L.kea_probe_floor(2, 128, 4096, 1024, 32, 32, None, None, vp(16), 4000, None) == -1  # ldy < n
+    assert L.kea_probe_floor(1, 256, 256, 65536, 256, 256, vp(16), vp(16), None, 256, None) == -1  # LDS
+    assert b"LDS" in L.kea_last_error()
+    assert L.kea_probe_spin(-1, None) == -1 and L.kea_probe_spin(100000001, None) == -1
+
+
 def _operand_bytes(words):
     """[64 lanes, 4 int32] -> [64, 16] bytes, little-endian."""
     return np.asarray(words, dtype=np.int64).astype(np.uint32).view(np.uint8).reshape(64, 16)
