@@ -193,6 +193,25 @@ int kea_row_epilogue(const int32_t *slices_dev, int split, int parts, int64_t m,
 int64_t kea_lowbit_gemm_workspace(int wbits, int parts, int64_t m, int64_t n, int64_t k, int64_t ws_group,
                                   int split_k, int config);
 
+/* kea_lowbit_gemm without the workspace arguments, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). It has no counterpart in the reference. The
+ * split-K slices live in a library-owned device array of KEA_NOALLOC_SCRATCH_BYTES per GPU (a file-scope __device__
+ * array, held until the process ends); a call whose kea_lowbit_gemm_workspace() exceeds that returns KEA_ESPACE
+ * with nothing launched. The call allocates nothing (no hipMalloc, hipFree or allocating library routine). Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU (on different streams, or in graphs
+ * replayed concurrently) race on it; calls ordered on one stream do not. Results are identical to kea_lowbit_gemm's
+ * for the same arguments. */
+#define KEA_NOALLOC_SCRATCH_BYTES (8LL << 20)
+int kea_lowbit_gemm_noalloc(int wbits,
+                            const int8_t *q_dev, int64_t part_stride, int64_t ldq, int parts,
+                            const void *qs_dev, int qs_dtype, int64_t qs_stride,
+                            const uint32_t *w_dev, int64_t n, int64_t k,
+                            const void *wscale_dev, int ws_dtype, int64_t ws_group,
+                            const void *bias_dev, int bias_dtype,
+                            void *y_dev, int y_dtype, int64_t ldy,
+                            int32_t *acc_out_dev, int64_t acc_ld,
+                            int64_t m, int flags, int split_k, int config, void *stream);
+
 /* The tile configuration id config == 0 resolves to for this shape (-1 on bad arguments). */
 int kea_lowbit_gemm_tile(int wbits, int parts, int64_t m, int64_t n, int64_t k);
 

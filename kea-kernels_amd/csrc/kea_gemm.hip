@@ -21,6 +21,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -403,6 +404,67 @@ int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq
     return gemm_impl(wbits, q, part_stride, ldq, parts, qs, qs_dtype, qs_stride, w, n, k, wscale, ws_dtype, ws_group,
                      bias, bias_dtype, y, y_dtype, ldy, acc_out, acc_ld, m, flags, split_k, config, workspace,
                      workspace_bytes, nullptr, 0, 0.f, stream);
+}
+
+// ---- kea_lowbit_gemm_noalloc: split-K slices in a library-owned device array ----
+
+}  // extern "C"
+
+namespace {
+
+constexpr int64_t kScratchInts = KEA_NOALLOC_SCRATCH_BYTES / 4;
+// The split-K slices of kea_lowbit_gemm_noalloc: one copy per GPU, held until the process ends. Host code never uses
+// this name as an address (it is a host-side stand-in): the device address comes from hipGetSymbolAddress.
+static __device__ __align__(256) int32_t scratch[kScratchInts];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The calling thread's current device's copy of `scratch`, resolved once per device with that device current.
+int scratch_for_current_device(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return kea::fail((int)e, std::string("hipGetDevice failed: ") + hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return kea::fail(KEA_ENODEV, "device index out of range for the scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_lock);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return kea::fail(e != hipSuccess ? (int)e : KEA_ENODEV,
+                             std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return KEA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kea_lowbit_gemm_noalloc(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts, const void *qs,
+                            int qs_dtype, int64_t qs_stride, const uint32_t *w, int64_t n, int64_t k,
+                            const void *wscale, int ws_dtype, int64_t ws_group, const void *bias, int bias_dtype,
+                            void *y, int y_dtype, int64_t ldy, int32_t *acc_out, int64_t acc_ld, int64_t m,
+                            int flags, int split_k, int config, void *stream) {
+    const int64_t need = kea_lowbit_gemm_workspace(wbits, parts, std::max<int64_t>(m, 1), n, k, ws_group, split_k,
+                                                   config);
+    if (need < 0) return KEA_EINVAL;  // the reason is already in kea_last_error()
+    if (need > KEA_NOALLOC_SCRATCH_BYTES)
+        return kea::fail(KEA_ESPACE, "kea_lowbit_gemm_noalloc: the split-K slices need " + std::to_string(need) +
+                                         " bytes, more than the " + std::to_string(KEA_NOALLOC_SCRATCH_BYTES) +
+                                         "-byte scratch array: use kea_lowbit_gemm with a workspace, or a smaller "
+                                         "split_k / m");
+    void *ws = nullptr;
+    if (need > 0) {
+        const int rc = scratch_for_current_device(&ws);
+        if (rc != KEA_OK) return rc;
+    }
+    return gemm_impl(wbits, q, part_stride, ldq, parts, qs, qs_dtype, qs_stride, w, n, k, wscale, ws_dtype, ws_group,
+                     bias, bias_dtype, y, y_dtype, ldy, acc_out, acc_ld, m, flags, split_k, config, ws,
+                     need > 0 ? KEA_NOALLOC_SCRATCH_BYTES : 0, nullptr, 0, 0.f, stream);
 }
 
 int kea_lowbit_gemm_residual(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts, const void *qs,
