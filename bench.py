@@ -6,19 +6,30 @@ A step is one launch of the 1-bit sign-weight GEMM on BASELINE.json's configs[0]
 the metric quotes: A = int8 [128, 1024] per-token quantized from fp16 N(0,1) with fp16 scales, W = uniform random bits
 [4096, 1024] (export codes -> native layout), fp16 per-channel scales U(0.01, 0.1), fp16 output [128, 4096] (the
 int32 accumulators are written only by the parity tests, not in the timed step). Inputs are resident in HBM before
-timing. Launches go through the product C ABI (kea_lowbit_gemm) on torch's current stream; to keep the host out of the
-measurement the K launches are captured into HIP graphs of up to 100 launches each and replayed back to back.
+timing. Launches go through the product C ABI (a kea_lowbit_gemm plan, validated once) on one stream; to keep the host
+out of the measurement the K launches are queued behind a bounded spin kernel (kea_probe_spin) that outlasts their
+submission, so the GPU runs them back to back between the two HIP events (`timing.graph_us_per_step`: the same K
+launches replayed as one HIP graph).
+
+The headline is HOT: back-to-back launches on the same 640 KB of operands, which stay in the 256 MB last-level cache
+between launches. `cold` repeats the measurement with every launch reading its own copy of the operands, cycling
+through more than 768 MiB (three times that cache).
 
 Prints one JSON line: value = int8 TOPS (2*M*N*K ops per step), `roofline` for the GEMM kernel (achieved = algorithmic
-ops per launch / average launch time from HIP events on the launch stream), `encoder` = the metric's second part, ms
-per 10-s clip of the 24-layer synthetic encoder at batch 1 and 8, and `cpu_baseline` = the
-oracle's C port of the reference's b1_fallback arithmetic (unpack -> exact int32 dot -> FP32 epilogue -> fp16) timed on
-this host's cores. Other modes: --suite (configs 2-4 and the reference's tuned shapes), --case (one GEMM shape), --encoder (config 5 with
-accuracy against the FP32 dense twin), --copy-calibration (a plain copy for the PMC traffic calibration).
+ops per launch / average launch time from HIP events on the launch stream), `floors` = the launch floors of the same
+grid (an empty kernel, and kernels that only load the tiles' operand bytes and/or store the output), `encoder` = the
+metric's second part, ms per 10-s clip of the 24-layer synthetic encoder at batch 1 and 8 with
+the batch-1 error against the FP32 dense twin, and `cpu_baseline` = the oracle's C port of the reference's b1_fallback
+arithmetic (unpack -> exact int32 dot -> FP32 epilogue -> fp16) on this host's cores and on one core, beside a PyTorch
+CPU restatement of the reference's own oracle formula; that leg also checks the GPU output bitwise against the oracle
+(`parity`). Other modes: --suite (configs 2-4 and the reference's tuned shapes), --case (one GEMM shape), --encoder
+(config 5 with accuracy against the FP32 dense twin), --copy-calibration (a plain copy for the PMC traffic
+calibration), --sweep (every tile of the library at the chooser's shapes).
 """
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -56,6 +67,55 @@ def make_inputs(device):
     return host, dev
 
 
+SPIN_NS = 200_000  # the bounded spin in front of each timed region (longer than the graphs take to submit)
+
+
+def replay_timed(stream, graphs, passes: int = 1) -> float:
+    """Milliseconds of `passes` back-to-back replays of `graphs` on `stream`, between HIP events recorded on that
+    stream; a bounded spin kernel runs first so the replays are queued before the start event executes."""
+    import torch
+    from kea_kernels import _hip
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        _hip.check(_hip.lib().kea_probe_spin(SPIN_NS, stream.cuda_stream), "kea_probe_spin")
+        start.record(stream)
+        for _ in range(passes):
+            for graph in graphs:
+                graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+    return start.elapsed_time(end)
+
+
+def capture(stream, fn, count: int):
+    import torch
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(count):
+            fn(i)
+    return graph
+
+
+def queued_timed(stream, fn, steps: int, host_us: float) -> float:
+    """Milliseconds of `steps` back-to-back calls of `fn` (each enqueueing one step on `stream`), between HIP events
+    recorded on that stream. The calls are queued behind a bounded spin kernel that outlasts their submission
+    (host_us per call, doubled), so the GPU runs them back to back with no host gaps and no graph boundaries."""
+    import torch
+    from kea_kernels import _hip
+    spin = int(min(100e6, SPIN_NS + 2e3 * host_us * steps))
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        _hip.check(_hip.lib().kea_probe_spin(spin, stream.cuda_stream), "kea_probe_spin")
+        start.record(stream)
+        for i in range(steps):
+            fn(i)
+        end.record(stream)
+        torch.cuda.synchronize()
+    return start.elapsed_time(end)
+
+
 def gpu_bench(steps: int, warmup: int):
     import torch
     from kea_kernels import _hip, lowbit
@@ -63,54 +123,94 @@ def gpu_bench(steps: int, warmup: int):
     device = torch.device("cuda", 0)
     _hip.require_gfx950(device)
     host, d = make_inputs(device)
-
-    def step():
-        lowbit.gemm(1, d["q"], d["qs"], d["words"], N, K, d["alpha"], None, d["y"], None)
-
     stream = torch.cuda.Stream(device)
-    with torch.cuda.stream(stream):
-        step()  # eager warm-up outside capture
-    torch.cuda.synchronize()
+    handle = stream.cuda_stream
+    # the timed step: the product launch path with its validation done once (lowbit.GemmPlan)
+    plan = lowbit.GemmPlan(1, d["q"], d["qs"], d["words"], N, K, d["alpha"], None, d["y"], None)
 
-    def capture(count):
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
+    def step(i=0):
+        plan(handle)
+
+    for _ in range(max(1, warmup)):
+        step()
+    torch.cuda.synchronize()
+    # host cost per launch (no synchronization inside): sizes the spin that keeps submission out of the timing
+    t0 = time.perf_counter()
+    for _ in range(100):
+        step()
+    host_us = (time.perf_counter() - t0) / 100 * 1e6
+    torch.cuda.synchronize()
+    ms_per_step = queued_timed(stream, step, steps, host_us) / steps
+
+    # the same K steps replayed as one HIP graph (a graph launch adds a fixed cost per replay)
+    graph = capture(stream, step, steps)
+    replay_timed(stream, [graph])
+    graph_ms = replay_timed(stream, [graph]) / steps
+    del graph
+
+    # eager launch rate (host path included, synchronized at the end): through the plan and through lowbit.gemm
+    def eager_us(fn, count=200):
+        with torch.cuda.stream(stream):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
             for _ in range(count):
-                step()
-        return graph
+                fn()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) / count * 1e6
 
-    chunk = max(1, min(100, steps))
-    graphs = [(capture(chunk), chunk)] * (steps // chunk)
-    if steps % chunk:
-        graphs.append((capture(steps % chunk), steps % chunk))
-    wgraph = capture(max(1, min(100, warmup))) if warmup else None
-    torch.cuda.synchronize()
-
-    with torch.cuda.stream(stream):
-        done = 0
-        while wgraph is not None and done < warmup:
-            wgraph.replay()
-            done += max(1, min(100, warmup))
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for graph, _ in graphs:
-            graph.replay()
-        end.record(stream)
-        torch.cuda.synchronize()
-    ms = start.elapsed_time(end)
-    ms_per_step = ms / steps
-
-    # eager launch rate through the Python operator (host launch path included): reported beside the headline
-    with torch.cuda.stream(stream):
-        t0 = time.perf_counter()
-        for _ in range(200):
-            step()
-        torch.cuda.synchronize()
-        eager_us = (time.perf_counter() - t0) / 200 * 1e6
-
+    checked = eager_us(lambda: lowbit.gemm(1, d["q"], d["qs"], d["words"], N, K, d["alpha"], None, d["y"], None))
+    planned = eager_us(step)
     cfg = configs.choose(M, N, K, parts=1, wbits=1)
-    return ms_per_step, eager_us, cfg, host
+    return {"ms_per_step": ms_per_step, "graph_ms_per_step": graph_ms, "host_us_per_launch": host_us,
+            "eager_us": planned, "eager_checked_us": checked, "cfg": cfg, "host": host, "d": d, "stream": stream}
+
+
+def cold_bench(d, stream, launches: int = 1300) -> float:
+    """Microseconds per launch when no launch finds its operands in a cache: `launches` launches, each reading its
+    own copy of q and the weight words, cycling through >= 768 MiB of copies (three times the last-level cache),
+    queued behind a spin as the hot figure is."""
+    import torch
+    from kea_kernels import lowbit
+    per_copy = d["q"].numel() + d["words"].numel() * 4
+    copies = -(-(3 << 28) // per_copy)
+    plans = [lowbit.GemmPlan(1, d["q"].clone(), d["qs"], d["words"].clone(), N, K, d["alpha"], None, d["y"], None)
+             for _ in range(copies)]
+    handle = stream.cuda_stream
+    torch.cuda.synchronize()
+    for pl in plans:  # one untimed pass
+        pl(handle)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(100):
+        plans[i % copies](handle)
+    host_us = (time.perf_counter() - t0) / 100 * 1e6
+    us = queued_timed(stream, lambda i: plans[i % copies](handle), launches, host_us) * 1000 / launches
+    del plans
+    torch.cuda.empty_cache()
+    return us
+
+
+def launch_floors(d, stream, tile_name: str, reps: int = 10) -> dict:
+    """Per-launch microseconds of the launch-floor probes (include/kea_probe.h) on the GEMM's own grid: one
+    workgroup per BM x BN tile of the chosen configuration, doing nothing, only loading its tile's operand bytes,
+    only storing its fp16 outputs, or both; graphs of 100 launches, timed as the GEMM is."""
+    import ctypes
+    import torch
+    from kea_kernels import _hip
+    L = _hip.lib()
+    bm, bn = (int(v) for v in tile_name.split()[0].split("x"))
+    vp = ctypes.c_void_p
+    y = torch.empty_like(d["y"])  # the probes' stores must not touch the GEMM's output (checked later)
+    out = {"tile": f"{bm}x{bn}", "workgroups": (M // bm) * (N // bn)}
+    for kind, name in enumerate(("empty_us", "loads_us", "stores_us", "loads_stores_us")):
+        def probe(i, kind=kind):
+            rc = L.kea_probe_floor(kind, M, N, K, bm, bn, vp(d["q"].data_ptr()), vp(d["words"].data_ptr()),
+                                   vp(y.data_ptr()), N, vp(torch.cuda.current_stream().cuda_stream))
+            _hip.check(rc, "kea_probe_floor")
+        graph = capture(stream, probe, 100)
+        replay_timed(stream, [graph])
+        out[name] = round(replay_timed(stream, [graph], reps) * 1000 / (100 * reps), 3)
+    return out
 
 
 def measured_peaks(reps: int = 5) -> dict:
@@ -154,9 +254,24 @@ def measured_peaks(reps: int = 5) -> dict:
                       "device-to-device copy (read + write bytes), best of 5"}
 
 
-def cpu_baseline(host, seconds: float = 10.0):
-    """The oracle's C port of b1_fallback on the same workload, repeated for about `seconds` on this host's cores."""
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(host, y_gpu, seconds: float = 10.0) -> dict:
+    """The oracle's C port of b1_fallback on the same workload, repeated for about `seconds` on this host's cores,
+    then for a third of that on one core; beside it, a PyTorch CPU restatement of the reference's own oracle formula
+    (q.to(int64) @ signs.to(int64).T, tests/test_kernels_gpu.py:23-27, then the FP32 epilogue) for a third of that.
+    The oracle's fp16 output is also the checker of the GPU's: `parity` is "bitwise" or the count of differing
+    outputs."""
     import numpy as np
+    import torch
     from oracle import oracle as O
     cores = len(os.sched_getaffinity(0))
     threads = O.set_threads(min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
@@ -164,29 +279,71 @@ def cpu_baseline(host, seconds: float = 10.0):
     codes = host["codes"].numpy()
     qs = host["qs"].float().numpy().reshape(1, M)
     alpha = host["alpha"].float().numpy()
-    reps, t0 = 0, time.perf_counter()
+
+    def timed_oracle(budget):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            y = O.to_f16_bits(O.epilogue(O.b1_gemm(q, codes, K), qs, alpha))
+            reps += 1
+            if time.perf_counter() - t0 >= budget:
+                return y, reps, time.perf_counter() - t0
+
+    y, reps, elapsed = timed_oracle(seconds)
+    got = y_gpu.view(torch.int16).cpu().numpy().view(np.uint16).reshape(M, N)
+    mismatches = int((got != y.reshape(M, N)).sum())
+    O.set_threads(1)
+    _, reps1, elapsed1 = timed_oracle(seconds / 3)
+    O.set_threads(threads)
+
+    # the reference's oracle formula on PyTorch's CPU backend (int64 matmul), then the same FP32 epilogue
+    signs = torch.from_numpy(O.unpack_signs(codes, K).astype(np.int8))
+    q64, s64 = host["q"].to(torch.int64), signs.to(torch.int64)
+    qs32, al32 = host["qs"].float(), host["alpha"].float()
+    treps, t0 = 0, time.perf_counter()
     while True:
-        acc = O.b1_gemm(q, codes, K)
-        y = O.to_f16_bits(O.epilogue(acc, qs, alpha))
-        reps += 1
-        if time.perf_counter() - t0 >= seconds:
+        acc = q64 @ s64.T
+        yt = ((acc.to(torch.float32) * qs32[:, None]) * al32[None, :]).to(torch.float16)
+        treps += 1
+        if time.perf_counter() - t0 >= seconds / 3:
             break
-    elapsed = time.perf_counter() - t0
-    del y
+    telapsed = time.perf_counter() - t0
+    del yt
     return {"value": round(OPS * reps / elapsed / 1e12, 6), "unit": "TOPS", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{reps} full config-1 GEMMs (M=128, N=4096, K=1024, unpack + exact int32 dot + FP32 epilogue "
-                      f"+ fp16 rounding) in {elapsed:.1f} s, OpenMP over output columns"}
+                      f"+ fp16 rounding) in {elapsed:.1f} s, OpenMP over output columns on {threads} threads",
+            "one_core": {"value": round(OPS * reps1 / elapsed1 / 1e12, 6), "unit": "TOPS", "cores": 1,
+                         "sample": f"{reps1} GEMMs in {elapsed1:.1f} s"},
+            "torch_int64": {"value": round(OPS * treps / telapsed / 1e12, 6), "unit": "TOPS",
+                            "cores": torch.get_num_threads(),
+                            "sample": f"{treps} x (q.to(int64) @ signs.to(int64).T + FP32 epilogue + fp16) in "
+                                      f"{telapsed:.1f} s, torch CPU"},
+            "parity": "bitwise" if mismatches == 0 else f"{mismatches} of {M * N} fp16 outputs differ"}
+
+
+TRAFFIC_PROFILE = ROOT / "profiles" / "b1_gemm_config1_traffic.json"
+
+
+def kernel_sources_sha() -> str:
+    """SHA-256 (16 hex digits) of the library's kernel sources (csrc/*), the build a traffic profile belongs to."""
+    h = hashlib.sha256()
+    for path in sorted((ROOT / "kea-kernels_amd" / "csrc").iterdir()):
+        if path.suffix in (".hip", ".h", ".cpp"):
+            h.update(path.name.encode())
+            h.update(path.read_bytes())
+    return h.hexdigest()[:16]
 
 
 def traffic_from_profiles():
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if one exists (else None)."""
-    path = ROOT / "profiles" / "b1_gemm_config1_traffic.json"
-    if not path.is_file():
-        return None
+    """HBM bytes per launch from the committed rocprofv3 PMC summary and the kernel-source hash it was measured on,
+    or (None, None) if there is none."""
+    if not TRAFFIC_PROFILE.is_file():
+        return None, None
     try:
-        return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+        data = json.loads(TRAFFIC_PROFILE.read_text())
     except (OSError, ValueError):
-        return None
+        return None, None
+    return data.get("hbm_bytes_per_launch"), data.get("kernel_sources_sha")
 
 
 # --- secondary measurements (python bench.py --suite): BASELINE.json configs 2-4 and the reference's tuned shapes ---
@@ -194,7 +351,8 @@ REF_SHAPES = [(n, k, m) for n, k in [(1024, 1024), (1024, 4096), (2048, 1024), (
               for m in (38, 126, 256, 368)]  # kk/binary/configs.py:17-36 (RTX 5090 timings, three parts, FP32 out)
 
 
-def _suite_case(wbits, parts, m, n, k, *, scale_dtype, out_dtype, seed, reps=200, ws_group=0, cold=False):
+def _suite_case(wbits, parts, m, n, k, *, scale_dtype, out_dtype, seed, reps=200, ws_group=0, cold=False,
+                config=None):
     """Per-launch microseconds of the library's default configuration, inputs resident, HIP-graph replay.
 
     cold: every launch reads its own copy of the weights and activations, cycling through at least 768 MiB of
@@ -227,31 +385,15 @@ def _suite_case(wbits, parts, m, n, k, *, scale_dtype, out_dtype, seed, reps=200
 
     def step(i=0):
         qi, wi = operands[i % copies]
-        lowbit.gemm(wbits, qi, qs, wi, n, k, alpha, None, y, None, ws_group=ws_group)
+        lowbit.gemm(wbits, qi, qs, wi, n, k, alpha, None, y, None, ws_group=ws_group, config=config)
 
     with torch.cuda.stream(stream):
         step()
     torch.cuda.synchronize()
-    graphs = []
-    for g0 in range(0, max(copies, 100), 100):
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(g0, g0 + 100):
-                step(i)
-        graphs.append(graph)
+    graphs = [capture(stream, lambda i, g0=g0: step(g0 + i), 100) for g0 in range(0, max(copies, 100), 100)]
     passes = max(1, reps // (100 * len(graphs)))
-    with torch.cuda.stream(stream):
-        for graph in graphs:
-            graph.replay()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(passes):
-            for graph in graphs:
-                graph.replay()
-        b.record(stream)
-        torch.cuda.synchronize()
-    us = a.elapsed_time(b) * 1000 / (passes * 100 * len(graphs))
+    replay_timed(stream, graphs)  # one untimed pass
+    us = replay_timed(stream, graphs, passes) * 1000 / (passes * 100 * len(graphs))
     del operands
     esz = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
     ops = 2 * m * n * k * parts
@@ -282,6 +424,37 @@ def suite() -> None:
         row = _suite_case(w, p, m, n, k, scale_dtype=sd, out_dtype=od, seed=i,
                           ws_group=128 if name.endswith("group128") else 0, cold=name.endswith("_cold"))
         print(json.dumps({"case": name, **row}), flush=True)
+
+
+# the chooser's shapes: BASELINE configs 1-4, the encoder's linears at batch 1 and 8 (M = 125, 1000), the reference's
+# tuned (N, K, M) points, each at one, two and three activation parts
+SWEEP_SHAPES = sorted({(n, k) for n, k in [(4096, 1024), (1024, 4096), (3072, 1024), (1024, 1024), (2048, 1024),
+                                           (2560, 640), (1030, 640)]})
+SWEEP_M = (1, 4, 16, 38, 64, 125, 128, 192, 256, 368, 512, 750, 1000)
+
+
+def sweep(parts_list=(1, 2, 3), wbits_list=(1, 2)) -> None:
+    """One JSON line per (wbits, parts, M, N, K): the per-launch microseconds of every tile configuration of the
+    library (split 0: the library's split for that tile) and which one the chooser picks. The committed chooser
+    table is read from these lines."""
+    import torch
+    from kea_kernels.binary import configs, kernels
+    ntiles = kernels.tile_count()
+    for wbits in wbits_list:
+        for parts in parts_list:
+            for n, k in SWEEP_SHAPES:
+                for m in SWEEP_M:
+                    row = {"wbits": wbits, "parts": parts, "M": m, "N": n, "K": k,
+                           "chosen": configs.choose(m, n, k, parts, wbits).tile}
+                    for tile in range(1, ntiles + 1):
+                        try:
+                            r = _suite_case(wbits, parts, m, n, k, scale_dtype=torch.float16,
+                                            out_dtype=torch.float16, seed=m + n + k, reps=300,
+                                            config=kernels.GemmConfig(tile, 0))
+                        except ValueError:
+                            continue  # the tile does not fit this part count / K
+                        row[f"t{tile}"] = r["us"]
+                    print(json.dumps(row), flush=True)
 
 
 def encoder_bench(batch: int, parts: int, reps: int = 20, seed: int = 5, check_dense: bool = True) -> dict:
@@ -355,9 +528,17 @@ def main(argv=None) -> int:
     ap.add_argument("--case", default=None, metavar="BITS,P,M,N,K",
                     help="only time one GEMM shape (fp16 scales and output, library-chosen configuration) for "
                          "--steps launches; used for the rocprofv3 counter passes of the larger configs")
+    ap.add_argument("--sweep", default=None, metavar="PARTS",
+                    help="only time every tile configuration at the chooser's shapes for these part counts "
+                         "(e.g. 1,2,3; one JSON line per shape)")
+    ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache config-1 figure")
+    ap.add_argument("--no-floors", action="store_true", help="skip the launch-floor probes")
     args = ap.parse_args(argv)
     if args.suite:
         suite()
+        return 0
+    if args.sweep:
+        sweep(tuple(int(v) for v in args.sweep.split(",")))
         return 0
     if args.case:
         w, p, m, n, k = (int(v) for v in args.case.split(","))
@@ -387,15 +568,17 @@ def main(argv=None) -> int:
     if args.steps < 1:
         print("--steps must be >= 1", file=sys.stderr)
         return 2
-    ms_per_step, eager_us, cfg, host = gpu_bench(args.steps, args.warmup)
+    r = gpu_bench(args.steps, args.warmup)
+    ms_per_step, cfg, host, d, stream = r["ms_per_step"], r["cfg"], r["host"], r["d"], r["stream"]
     tops = OPS / (ms_per_step * 1e-3) / 1e12
     mfma_time = OPS / (PEAK_INT8_TOPS * 1e12)
     hbm_time = BYTES / (PEAK_HBM_GBS * 1e9)
     bound = "mfma" if mfma_time >= hbm_time else "hbm"
     if bound == "mfma":
-        achieved, peak, unit = tops, PEAK_INT8_TOPS, "TFLOP/s"
+        achieved, peak, unit = tops, PEAK_INT8_TOPS, "TOPS"
     else:
         achieved, peak, unit = BYTES / (ms_per_step * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
+    traffic, traffic_sha = traffic_from_profiles()
     line = {
         "metric": METRIC,
         "value": round(tops, 3),
@@ -410,14 +593,34 @@ def main(argv=None) -> int:
         "dtype": "int8",
         "data": "synthetic",
         "config": {"workload": "config1: 1-bit sign-weight x int8 GEMM, M=128 K=1024 N=4096, 1 activation part, "
-                               "fp16 per-token and per-channel scales, fp16 output, inputs resident in HBM, HIP-graph "
-                               "replay of back-to-back launches",
+                               "fp16 per-token and per-channel scales, fp16 output, inputs resident in HBM; HOT: "
+                               "back-to-back launches on the same 640 KB of operands, which stay in the 256 MB "
+                               "last-level cache (the cold figure is `cold`)",
                    "M": M, "N": N, "K": K, "parts": 1, "weight_bits": 1, "tile": cfg.label()},
         "roofline": {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-                     "frac": round(achieved / peak, 5), "traffic": traffic_from_profiles(),
+                     "frac": round(achieved / peak, 5), "traffic": traffic,
+                     "traffic_build": {"kernel_sources_sha": traffic_sha,
+                                       "this_build": kernel_sources_sha(),
+                                       "same_build": traffic_sha == kernel_sources_sha()},
                      "algorithmic_bytes": BYTES, "ops": OPS},
-        "eager_launch_us": round(eager_us, 3),
+        "timing": {"method": "the K launches (a validated lowbit.GemmPlan each) queued behind a bounded spin kernel "
+                             "that outlasts their submission, HIP events on the launch stream around them",
+                   "host_us_per_launch": round(r["host_us_per_launch"], 3),
+                   "graph_us_per_step": round(r["graph_ms_per_step"] * 1e3, 3),
+                   "graph_note": "the same K launches replayed as one HIP graph; a replay adds a fixed cost"},
+        "eager_launch_us": round(r["eager_us"], 3),
+        "eager_launch_us_checked": round(r["eager_checked_us"], 3),
     }
+    if not args.no_cold:
+        cold_us = cold_bench(d, stream)
+        line["cold"] = {"us_per_step": round(cold_us, 3), "tops": round(OPS / cold_us / 1e6, 3),
+                        "frac": round(mfma_time / (cold_us * 1e-6), 5),
+                        "method": "every launch reads its own copy of q and the weight words, cycling through "
+                                  ">= 768 MiB of copies (3x the last-level cache); HIP-graph replay"}
+    if not args.no_floors:
+        floors = launch_floors(d, stream, _hip_config_name(cfg.tile))
+        floors["gemm_us"] = round(ms_per_step * 1e3, 3)
+        line["floors"] = floors
     if not args.no_peaks:
         peaks = measured_peaks()
         measured = peaks["mfma_i8_tops"] if bound == "mfma" else peaks["copy_gbs"]
@@ -425,16 +628,29 @@ def main(argv=None) -> int:
         line["roofline"]["frac_of_measured"] = round(achieved / measured, 5)
         line["measured_peaks"] = peaks
     if not args.no_encoder:
-        # the metric's second part: ms per 10-s clip of the 24-layer encoder (config 5), one int8 part, HIP graph
-        enc = {f"batch{b}": encoder_bench(b, 1, check_dense=False) for b in (1, 8)}
+        # the metric's second part: ms per 10-s clip of the 24-layer encoder (config 5), one int8 part, HIP graph;
+        # batch 1 also carries its error against the same model with FP32 dense linears
+        enc = {f"batch{b}": encoder_bench(b, 1, check_dense=(b == 1)) for b in (1, 8)}
         line["encoder"] = {"ms_per_clip_batch1": enc["batch1"]["ms_per_clip"],
                            "ms_per_clip_batch8": enc["batch8"]["ms_per_clip"], "parts": 1,
+                           "rel_err_vs_dense_fp32_batch1": enc["batch1"]["rel_err_vs_dense_fp32"],
                            "workload": "config5: 10 s of 16 kHz noise -> log-mel -> 8x subsampling -> 24 FastConformer "
                                        "layers (d 1024, 8 heads, FFN 4096, conv k 9), 1-bit linears, random init"}
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds)
+        import torch
+        torch.cuda.synchronize()
+        line["cpu_baseline"] = cpu_baseline(host, d["y"], args.cpu_seconds)
+        line["parity"] = line["cpu_baseline"]["parity"]
     print(json.dumps(line), flush=True)
+    if line.get("parity", "bitwise") != "bitwise":
+        print(f"bench.py: the GPU output differs from the oracle: {line['parity']}", file=sys.stderr)
+        return 1
     return 0
+
+
+def _hip_config_name(tile: int) -> str:
+    from kea_kernels import _hip
+    return _hip.lib().kea_config_name(tile).decode()
 
 
 if __name__ == "__main__":

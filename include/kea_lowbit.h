@@ -193,6 +193,29 @@ int kea_row_epilogue(const int32_t *slices_dev, int split, int parts, int64_t m,
 int64_t kea_lowbit_gemm_workspace(int wbits, int parts, int64_t m, int64_t n, int64_t k, int64_t ws_group,
                                   int split_k, int config);
 
+/* Plans: kea_lowbit_gemm's checks and its tile / split / kernel resolution done once, for callers that launch the
+ * same GEMM on the same buffers many times (serving loops, benchmarks): kea_lowbit_gemm_plan takes kea_lowbit_gemm's
+ * arguments (without the stream) plus kea_lowbit_gemm_residual's residual, ldr and factor (residual NULL: none) and
+ * returns a host-side plan, or NULL with kea_last_error() set on any argument kea_lowbit_gemm would refuse. The plan
+ * records the pointers: their buffers must stay allocated, with the same contents layout, while it is launched.
+ * kea_lowbit_gemm_plan_launch enqueues the GEMM (and its split-K finish) on `stream` exactly as kea_lowbit_gemm would;
+ * kea_lowbit_gemm_plan_free releases the plan (host memory only). No counterpart in the reference, whose launches
+ * re-validate on every call (kk/binary/layer.py:182-201). */
+typedef struct kea_gemm_plan kea_gemm_plan;
+kea_gemm_plan *kea_lowbit_gemm_plan(int wbits,
+                                    const int8_t *q_dev, int64_t part_stride, int64_t ldq, int parts,
+                                    const void *qs_dev, int qs_dtype, int64_t qs_stride,
+                                    const uint32_t *w_dev, int64_t n, int64_t k,
+                                    const void *wscale_dev, int ws_dtype, int64_t ws_group,
+                                    const void *bias_dev, int bias_dtype,
+                                    void *y_dev, int y_dtype, int64_t ldy,
+                                    int32_t *acc_out_dev, int64_t acc_ld,
+                                    int64_t m, int flags, int split_k, int config,
+                                    void *workspace_dev, int64_t workspace_bytes,
+                                    const float *residual_dev, int64_t ldr, float factor);
+int kea_lowbit_gemm_plan_launch(const kea_gemm_plan *plan, void *stream);
+void kea_lowbit_gemm_plan_free(kea_gemm_plan *plan);
+
 /* kea_lowbit_gemm without the workspace arguments, for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). It has no counterpart in the reference. The
  * split-K slices live in a library-owned device array of KEA_NOALLOC_SCRATCH_BYTES per GPU (a file-scope __device__

@@ -28,6 +28,10 @@ ARCH = "gfx950"
 # (AGPR) form the register allocator shuffles them with accvgpr moves every iteration, which would be measured as
 # matrix-core time, so it selects the VGPR form of the MFMAs.
 SOURCE_FLAGS = {"kea_probe.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# The wave-split kernels take their load operands as ten leading scalar arguments (4 pointers, 6 ints: 14 SGPRs) that
+# the dispatch preloads into SGPRs, so the first loads issue without a kernel-argument round trip.
+for _p in (1, 2, 3):
+    SOURCE_FLAGS[f"kea_gemm_wsplit_p{_p}.hip"] = ["-mllvm", "-amdgpu-kernarg-preload-count=10"]
 
 
 def hipcc() -> str:

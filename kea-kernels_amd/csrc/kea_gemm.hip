@@ -22,6 +22,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <mutex>
+#include <new>
 #include <string>
 #include <type_traits>
 
@@ -255,13 +256,30 @@ int kea_lowbit_gemm_split(int wbits, int parts, int64_t m, int64_t n, int64_t k,
     return s;
 }
 
-static int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts, const void *qs,
-                     int qs_dtype, int64_t qs_stride, const uint32_t *w, int64_t n, int64_t k, const void *wscale,
-                     int ws_dtype, int64_t ws_group, const void *bias, int bias_dtype, void *y, int y_dtype,
-                     int64_t ldy, int32_t *acc_out, int64_t acc_ld, int64_t m, int flags, int split_k, int config,
-                     void *workspace, int64_t workspace_bytes, const float *residual, int64_t ldr, float factor,
-                     void *stream) {
+}  // extern "C"
+
+namespace {
+
+// A validated GEMM launch, resolved once (tile, split, kernel instance, grid, LDS) and enqueued any number of times.
+struct LaunchSpec {
+    Params p;
+    bool empty;          // m == 0: nothing to launch
+    bool wsplit;         // the wave-split kernel (else the LDS-ring kernel)
+    WsplitLaunch wl;
+    KernelFn ring_fn;
+    dim3 grid, block;
+    int lds_bytes;
+    int splits, parts;   // splits > 1: a finish launch follows
+    dim3 finish_grid;
+};
+
+int gemm_prepare(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts, const void *qs, int qs_dtype,
+                 int64_t qs_stride, const uint32_t *w, int64_t n, int64_t k, const void *wscale, int ws_dtype,
+                 int64_t ws_group, const void *bias, int bias_dtype, void *y, int y_dtype, int64_t ldy,
+                 int32_t *acc_out, int64_t acc_ld, int64_t m, int flags, int split_k, int config, void *workspace,
+                 int64_t workspace_bytes, const float *residual, int64_t ldr, float factor, LaunchSpec *ls) {
     int tile, s, qps, gq = 0;
+    *ls = LaunchSpec{};
     if (ws_group != 0) {
         if (ws_group != 64 && ws_group != 128 && ws_group != 256)
             return kea::fail(KEA_EINVAL, "ws_group must be 0 (per-channel scales), 64, 128 or 256");
@@ -289,7 +307,10 @@ static int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ld
     if (acc_out && acc_ld < n) return kea::fail(KEA_EINVAL, "acc_ld < n");
     if (residual && !y) return kea::fail(KEA_EINVAL, "a residual needs y");
     if (residual && ldr < n) return kea::fail(KEA_EINVAL, "ldr < n");
-    if (m == 0) return KEA_OK;
+    if (m == 0) {
+        ls->empty = true;
+        return KEA_OK;
+    }
     if (!q) return kea::fail(KEA_EINVAL, "q is required");
     if (ldq < k) return kea::fail(KEA_EINVAL, "ldq < k");
     if (parts > 1 && part_stride < m * ldq) return kea::fail(KEA_EINVAL, "part_stride < m * ldq (parts overlap)");
@@ -299,7 +320,7 @@ static int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ld
     if ((int64_t)(parts - 1) * part_stride + m * ldq > (int64_t)INT32_MAX)
         return kea::fail(KEA_EINVAL, "q spans more than 2 GiB: split the call along M");
 
-    Params p = {};
+    Params &p = ls->p;
     p.q = q; p.part_stride = part_stride; p.ldq = ldq;
     p.qs = qs; p.qs_stride = qs_stride; p.qs_dtype = qs_dtype;
     p.w = w; p.ws = wscale; p.ws_dtype = ws_dtype;
@@ -318,32 +339,29 @@ static int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ld
     p.acc_vec = acc_out && (acc_ld % 4 == 0) && ((uintptr_t)acc_out % 16 == 0);
     p.ws_vec = ((uintptr_t)wscale % (ws_dtype == KEA_F16 ? 8 : 16)) == 0;
     p.bias_vec = bias && ((uintptr_t)bias % (bias_dtype == KEA_F16 ? 8 : 16)) == 0;
+    ls->splits = s;
+    ls->parts = parts;
+    if (s > 1) {
+        const int64_t need = (int64_t)s * parts * m * n * 4;
+        if (!workspace || workspace_bytes < need)
+            return kea::fail(KEA_ESPACE, "split-K workspace too small: need " + std::to_string(need) + " bytes");
+        if ((uintptr_t)workspace & 15) return kea::fail(KEA_EALIGN, "workspace must be 16-byte aligned");
+        if (!kea::fits_dispatch(cdivl(m * cdivl(n, 4), 256), 256))
+            return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N or M");
+        p.slices = (int32_t *)workspace;
+        p.slice_vec = (n % 4 == 0);
+        ls->finish_grid = dim3((unsigned)cdivl(m * cdivl(n, 4), 256));
+    }
 
-    hipStream_t st = (hipStream_t)stream;
     if (tile > kNumTiles) {
         if (gq) return kea::fail(KEA_EINVAL, "per-group weight scales run the LDS-ring tiles");
         const WsplitTile &wt = kWsplitTiles[tile - kNumTiles - 1];
-        if (!kea::fits_dispatch(cdivl(n, wt.nt * 16), wt.nw * 64) ||
-            (s > 1 && !kea::fits_dispatch(cdivl(m * cdivl(n, 4), 256), 256)))
+        if (!kea::fits_dispatch(cdivl(n, wt.nt * 16), wt.nw * 64))
             return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N or M");
-        if (s > 1) {
-            const int64_t need = (int64_t)s * parts * m * n * 4;
-            if (!workspace || workspace_bytes < need)
-                return kea::fail(KEA_ESPACE, "split-K workspace too small: need " + std::to_string(need) + " bytes");
-            if ((uintptr_t)workspace & 15) return kea::fail(KEA_EALIGN, "workspace must be 16-byte aligned");
-            p.slices = (int32_t *)workspace;
-            p.slice_vec = (n % 4 == 0);
-        }
         p.steps_per_slice = qps;
-        const int steps = qps / wt.nw;
-        hipError_t e = kea::wsplit_launch(p, wbits, parts, tile - kNumTiles - 1, steps, s, s > 1, st);
-        if (e != hipSuccess) return kea::fail((int)e, std::string("gemm launch failed: ") + hipGetErrorString(e));
-        if (s > 1) {
-            const long long work = m * cdivl(n, 4);
-            hipLaunchKernelGGL(pick_finish(parts), dim3((unsigned)cdivl(work, 256)), dim3(256), 0, st, p, s);
-            e = hipGetLastError();
-            if (e != hipSuccess) return kea::fail((int)e, std::string("finish launch failed: ") + hipGetErrorString(e));
-        }
+        const hipError_t e = kea::wsplit_prepare(p, wbits, parts, tile - kNumTiles - 1, qps / wt.nw, s, s > 1, &ls->wl);
+        if (e != hipSuccess) return kea::fail((int)e, std::string("no wave-split kernel: ") + hipGetErrorString(e));
+        ls->wsplit = true;
         return KEA_OK;
     }
     const Tile &t = kTiles[tile - 1];
@@ -365,36 +383,88 @@ static int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ld
         if (lds_bytes > kLdsBudget)
             return kea::fail(KEA_EINVAL, "too many weight-scale groups for one workgroup's LDS: use a larger ws_group");
     }
-    if (!kea::fits_dispatch(cdivl(n, bn), t.wm * t.wn * 64) ||
-        (s > 1 && !kea::fits_dispatch(cdivl(m * cdivl(n, 4), 256), 256)))
+    if (!kea::fits_dispatch(cdivl(n, bn), t.wm * t.wn * 64))
         return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N or M");
-    dim3 grid((unsigned)cdivl(n, bn), (unsigned)cdivl(m, bm), (unsigned)s);
-    dim3 block(t.wm * t.wn * 64);
-    if (s > 1) {
-        const int64_t need = (int64_t)s * parts * m * n * 4;
-        if (!workspace || workspace_bytes < need)
-            return kea::fail(KEA_ESPACE, "split-K workspace too small: need " + std::to_string(need) + " bytes");
-        if ((uintptr_t)workspace & 15) return kea::fail(KEA_EALIGN, "workspace must be 16-byte aligned");
-        p.slices = (int32_t *)workspace;
-        p.slice_vec = (n % 4 == 0);
-    }
-    KernelFn fn = gq ? pick_group(wbits, parts, gq, tile, (k & 15) != 0)
+    ls->grid = dim3((unsigned)cdivl(n, bn), (unsigned)cdivl(m, bm), (unsigned)s);
+    ls->block = dim3(t.wm * t.wn * 64);
+    ls->ring_fn = gq ? pick_group(wbits, parts, gq, tile, (k & 15) != 0)
                      : pick_kernel(wbits, parts, tile, s > 1, (k & 15) != 0);
+    if (!ls->ring_fn) return kea::fail(KEA_EINVAL, "no kernel instance for this tile");
     if (lds_bytes > 65536) {
-        hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
+        hipError_t e = hipFuncSetAttribute((const void *)ls->ring_fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           lds_bytes);
         if (e != hipSuccess) return kea::fail((int)e, std::string("LDS attribute refused: ") + hipGetErrorString(e));
     }
-    hipLaunchKernelGGL(fn, grid, block, lds_bytes, st, p);
-    hipError_t e = hipGetLastError();
+    ls->lds_bytes = lds_bytes;
+    return KEA_OK;
+}
+
+int gemm_launch(const LaunchSpec &ls, hipStream_t st) {
+    if (ls.empty) return KEA_OK;
+    hipError_t e;
+    if (ls.wsplit) {
+        e = kea::wsplit_enqueue(ls.wl, ls.p, st);
+    } else {
+        hipLaunchKernelGGL(ls.ring_fn, ls.grid, ls.block, ls.lds_bytes, st, ls.p);
+        e = hipGetLastError();
+    }
     if (e != hipSuccess) return kea::fail((int)e, std::string("gemm launch failed: ") + hipGetErrorString(e));
-    if (s > 1) {
-        const long long work = m * cdivl(n, 4);
-        hipLaunchKernelGGL(pick_finish(parts), dim3((unsigned)cdivl(work, 256)), dim3(256), 0, st, p, s);
+    if (ls.splits > 1) {
+        hipLaunchKernelGGL(pick_finish(ls.parts), ls.finish_grid, dim3(256), 0, st, ls.p, ls.splits);
         e = hipGetLastError();
         if (e != hipSuccess) return kea::fail((int)e, std::string("finish launch failed: ") + hipGetErrorString(e));
     }
     return KEA_OK;
 }
+
+int gemm_impl(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts, const void *qs, int qs_dtype,
+              int64_t qs_stride, const uint32_t *w, int64_t n, int64_t k, const void *wscale, int ws_dtype,
+              int64_t ws_group, const void *bias, int bias_dtype, void *y, int y_dtype, int64_t ldy, int32_t *acc_out,
+              int64_t acc_ld, int64_t m, int flags, int split_k, int config, void *workspace, int64_t workspace_bytes,
+              const float *residual, int64_t ldr, float factor, void *stream) {
+    LaunchSpec ls;
+    const int rc = gemm_prepare(wbits, q, part_stride, ldq, parts, qs, qs_dtype, qs_stride, w, n, k, wscale, ws_dtype,
+                                ws_group, bias, bias_dtype, y, y_dtype, ldy, acc_out, acc_ld, m, flags, split_k,
+                                config, workspace, workspace_bytes, residual, ldr, factor, &ls);
+    if (rc != KEA_OK) return rc;
+    return gemm_launch(ls, (hipStream_t)stream);
+}
+
+}  // namespace
+
+struct kea_gemm_plan {
+    LaunchSpec spec;
+};
+
+extern "C" {
+
+kea_gemm_plan *kea_lowbit_gemm_plan(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts,
+                                    const void *qs, int qs_dtype, int64_t qs_stride, const uint32_t *w, int64_t n,
+                                    int64_t k, const void *wscale, int ws_dtype, int64_t ws_group, const void *bias,
+                                    int bias_dtype, void *y, int y_dtype, int64_t ldy, int32_t *acc_out,
+                                    int64_t acc_ld, int64_t m, int flags, int split_k, int config, void *workspace,
+                                    int64_t workspace_bytes, const float *residual, int64_t ldr, float factor) {
+    kea_gemm_plan *plan = new (std::nothrow) kea_gemm_plan;
+    if (!plan) {
+        kea::fail(KEA_EINVAL, "out of host memory for a plan");
+        return nullptr;
+    }
+    const int rc = gemm_prepare(wbits, q, part_stride, ldq, parts, qs, qs_dtype, qs_stride, w, n, k, wscale, ws_dtype,
+                                ws_group, bias, bias_dtype, y, y_dtype, ldy, acc_out, acc_ld, m, flags, split_k,
+                                config, workspace, workspace_bytes, residual, ldr, factor, &plan->spec);
+    if (rc != KEA_OK) {
+        delete plan;
+        return nullptr;
+    }
+    return plan;
+}
+
+int kea_lowbit_gemm_plan_launch(const kea_gemm_plan *plan, void *stream) {
+    if (!plan) return kea::fail(KEA_EINVAL, "plan is NULL");
+    return gemm_launch(plan->spec, (hipStream_t)stream);
+}
+
+void kea_lowbit_gemm_plan_free(kea_gemm_plan *plan) { delete plan; }
 
 int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts, const void *qs,
                     int qs_dtype, int64_t qs_stride, const uint32_t *w, int64_t n, int64_t k, const void *wscale,
@@ -513,8 +583,9 @@ int kea_lowbit_gemm_slices(int wbits, const int8_t *q, int64_t part_stride, int6
         if (!kea::fits_dispatch(cdivl(n, wt.nt * 16), wt.nw * 64))
             return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N");
         p.steps_per_slice = qps;
-        const hipError_t e = kea::wsplit_launch(p, wbits, parts, tile - kNumTiles - 1, qps / wt.nw, s, true,
-                                                (hipStream_t)stream);
+        WsplitLaunch wl;
+        hipError_t e = kea::wsplit_prepare(p, wbits, parts, tile - kNumTiles - 1, qps / wt.nw, s, true, &wl);
+        if (e == hipSuccess) e = kea::wsplit_enqueue(wl, p, (hipStream_t)stream);
         if (e != hipSuccess) return kea::fail((int)e, std::string("slice launch failed: ") + hipGetErrorString(e));
         return KEA_OK;
     }

@@ -53,7 +53,8 @@ inline bool wsplit_fits(int wbits, int parts, const WsplitTile &t, int s) {
     return regs <= (t.nw == 4 ? 320 : 160) && wsplit_lds_bytes(parts, t) <= 160 * 1024;
 }
 
-using WsplitFn = void (*)(Params);
+using WsplitFn = void (*)(const int8_t *, const uint32_t *, const void *, const void *, int, int, int, int, int,
+                         int, Params);
 
 // The kernel instance for a wave-split tile index, s k-steps per wave, SLICED and RAGGED flags (nullptr when that
 // register budget does not fit). Defined per activation part count.
@@ -61,10 +62,25 @@ WsplitFn wsplit_pick_p1(int wbits, int tile, int s, bool sliced, bool ragged);
 WsplitFn wsplit_pick_p2(int wbits, int tile, int s, bool sliced, bool ragged);
 WsplitFn wsplit_pick_p3(int wbits, int tile, int s, bool sliced, bool ragged);
 
-// Launches the wave-split kernel over grid (ceil(N / BN), ceil(M / BM), splits) with `s` k-steps per wave;
-// p.steps_per_slice is the K range of one workgroup in k-steps (all of K when unsplit). SLICED: write int32 slices.
-// Returns the launch's hipError_t.
-hipError_t wsplit_launch(const Params &p, int wbits, int parts, int tile, int s, int splits, bool sliced,
-                         hipStream_t stream);
+// A resolved wave-split launch: kernel instance, grid, workgroup size, dynamic LDS and the dtype bits of its scales.
+struct WsplitLaunch {
+    WsplitFn fn;
+    dim3 grid, block;
+    int lds;
+    int meta;
+};
+
+// Resolves the launch of the wave-split kernel over grid (ceil(N / BN), ceil(M / BM), splits) with `s` k-steps per
+// wave (p.steps_per_slice is the K range of one workgroup in k-steps) and raises the kernel's LDS limit where it needs
+// more than 64 KiB. SLICED: the kernel writes int32 slices. Returns a hipError_t.
+hipError_t wsplit_prepare(const Params &p, int wbits, int parts, int tile, int s, int splits, bool sliced,
+                          WsplitLaunch *out);
+
+// Enqueues a resolved wave-split launch on `stream`; returns the launch's hipError_t.
+inline hipError_t wsplit_enqueue(const WsplitLaunch &l, const Params &p, hipStream_t stream) {
+    hipLaunchKernelGGL(l.fn, l.grid, l.block, l.lds, stream, p.q, p.w, p.qs, p.ws, p.M, p.N, p.K, (int)p.ldq, l.meta,
+                       (int)p.part_stride, p);
+    return hipGetLastError();
+}
 
 }  // namespace kea

@@ -5,8 +5,8 @@
 
 namespace kea {
 
-hipError_t wsplit_launch(const Params &p, int wbits, int parts, int tile, int s, int splits, bool sliced,
-                         hipStream_t stream) {
+hipError_t wsplit_prepare(const Params &p, int wbits, int parts, int tile, int s, int splits, bool sliced,
+                          WsplitLaunch *out) {
     const WsplitTile &t = kWsplitTiles[tile];
     // unmasked vector loads need whole k-step ranges in every workgroup and complete weight quads (or one word)
     const int ksteps = (p.K + 63) / 64, words = wbits == 1 ? s / 2 : s;
@@ -20,10 +20,14 @@ hipError_t wsplit_launch(const Params &p, int wbits, int parts, int tile, int s,
         const hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) return e;
     }
-    const dim3 grid((unsigned)((p.N + t.nt * 16 - 1) / (t.nt * 16)), (unsigned)((p.M + t.rm * 16 - 1) / (t.rm * 16)),
-                    (unsigned)splits);
-    hipLaunchKernelGGL(fn, grid, dim3(t.nw * 64), lds, stream, p);
-    return hipGetLastError();
+    out->fn = fn;
+    out->grid = dim3((unsigned)((p.N + t.nt * 16 - 1) / (t.nt * 16)), (unsigned)((p.M + t.rm * 16 - 1) / (t.rm * 16)),
+                     (unsigned)splits);
+    out->block = dim3(t.nw * 64);
+    out->lds = lds;
+    out->meta = (p.qs_dtype == KEA_F16 ? 1 : 0) | (p.ws_dtype == KEA_F16 ? 2 : 0) |
+                (p.bias && p.bias_dtype == KEA_F16 ? 4 : 0);
+    return hipSuccess;
 }
 
 }  // namespace kea

@@ -36,14 +36,16 @@ namespace {
 
 using namespace kea;
 
-// The aligned 32-bit word holding element i of an f32 or f16 vector (f16: the half is selected at conversion time).
-// The word lies inside the 4-byte block of an in-bounds element, so it never reaches past a page the vector touches.
-__device__ __forceinline__ uint32_t load_raw(const void *v, bool f16, long long i) {
-    const long long off = f16 ? (i * 2) & ~3LL : i * 4;
-    return *(const uint32_t *)((const char *)v + off);
+// The aligned 32-bit word holding element i of an f32 or f16 vector (f16: the half is selected at conversion time by
+// raw_to_f32 with the same v and i). The word lies inside the 4-byte block of an in-bounds element, so it never
+// reaches past a page the vector touches.
+__device__ __forceinline__ uint32_t load_raw(const void *v, bool f16, uint32_t i) {
+    const char *a = (const char *)v + (f16 ? 2u * i : 4u * i);
+    return *(const uint32_t *)__builtin_align_down(a, 4);  // keeps the pointer's (global) address space
 }
-__device__ __forceinline__ float raw_to_f32(uint32_t raw, bool f16, long long i) {
-    const float h = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw >> ((i & 1) * 16)));
+__device__ __forceinline__ float raw_to_f32(uint32_t raw, bool f16, const void *v, uint32_t i) {
+    const uint32_t hi = (uint32_t)(((uintptr_t)v >> 1) + i) & 1u;  // f16: which half of the word
+    const float h = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw >> (hi * 16)));
     return f16 ? h : __builtin_bit_cast(float, raw);
 }
 
@@ -51,8 +53,13 @@ __device__ __forceinline__ float raw_to_f32(uint32_t raw, bool f16, long long i)
 // multiple of NW * S k-steps) and that its weight words lie in complete quads (J % 4 == 0 or one word per wave), so
 // every load is an unmasked vector load. RAGGED = true: loads from clamped addresses, masked to zero at k >= kend
 // (per byte, so K % 16 != 0 is covered).
+// The operands the loads need come first, as scalar arguments, so the dispatch can preload them into SGPRs
+// (-amdgpu-kernarg-preload-count): no kernel-argument round trip stands before the first load. meta: bit 0 qs is
+// f16, bit 1 wscale is f16, bit 2 bias is f16. The rest (epilogue, slices) is read from `p`.
 template <int WBITS, int P, int RM, int NT, int NW, int S, bool SLICED, bool RAGGED>
-__global__ void __launch_bounds__(NW * 64) wsplit_kernel(Params p) {
+__global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const uint32_t *w, const void *qs,
+                                                         const void *ws, int M, int N, int K, int ldq, int meta,
+                                                         int part_stride, Params p) {
     static_assert(WBITS == 2 || S % 2 == 0, "1-bit waves take whole words (two k-steps each)");
     constexpr int KSW = WBITS == 1 ? 2 : 1;       // k-steps per native word
     constexpr int WPW = S / KSW;                  // words per lane per n-tile for one wave
@@ -62,16 +69,11 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(Params p) {
     constexpr int PART = P * RM * NT * 256;       // int32 of one wave's partial tile in LDS
     extern __shared__ __attribute__((aligned(16))) int32_t red[];  // [NW][P][RM][NT][64 lanes][4]
 
-    // The parameters the loads need, all read before the first load is issued: one kernel-argument round trip.
-    const int8_t *const q = p.q;
-    const uint32_t *const w = p.w;
-    const void *const qs = p.qs, *const ws = p.ws, *const bias = p.bias;
-    const long long part_stride = p.part_stride, ldq = p.ldq, qs_stride = p.qs_stride;
-    const int M = p.M, N = p.N, K = p.K, J = p.J, NTILES = p.NT, sps = p.steps_per_slice;
-    const bool qs16 = p.qs_dtype == KEA_F16, ws16 = p.ws_dtype == KEA_F16, b16 = p.bias_dtype == KEA_F16;
-    asm volatile("" ::"s"(q), "s"(w), "s"(qs), "s"(ws), "s"(bias), "s"(part_stride), "s"(ldq), "s"(qs_stride),
-                 "s"(M), "s"(N), "s"(K), "s"(J), "s"(NTILES), "s"(sps), "s"(p.qs_dtype), "s"(p.ws_dtype),
-                 "s"(p.bias_dtype));
+    const void *const bias = p.bias;
+    const long long qs_stride = p.qs_stride;
+    const int J = WBITS == 1 ? (K + 127) >> 7 : (K + 63) >> 6, NTILES = (N + 15) >> 4;
+    const int sps = SLICED ? p.steps_per_slice : 0;
+    const bool qs16 = meta & 1, ws16 = (meta >> 1) & 1, b16 = (meta >> 2) & 1;
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
@@ -82,13 +84,15 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(Params p) {
     const int kend = min(K, sb * 64);
 
     // ---- loads: weights, activations, epilogue scales, all issued before the first wait ----
+    const uint32_t lane16 = (uint32_t)lane * 16u;  // < 1024
     uint32_t wv[NT][WPW];
     {
         const int j0 = s0 / KSW;
 #pragma unroll
         for (int jn = 0; jn < NT; ++jn) {
+            // wave-uniform base of the n-tile's words, plus a 32-bit per-lane byte offset (SGPR-base loads)
             const int t = min((n0 >> 4) + jn, NTILES - 1);
-            const uint32_t *tb = w + (long long)t * J * 64;
+            const char *tb = (const char *)(w + (long long)t * J * 64);
             if constexpr (WPW == 1 || RAGGED) {
                 // general addressing: a short last quad has lane stride wq < 4; words past J load any valid word
                 // (their activations are zero)
@@ -96,15 +100,15 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(Params p) {
                 for (int u = 0; u < WPW; ++u) {
                     const int j = min(j0 + u, J - 1), jq = j & ~3;
                     const int wq = min(4, J - jq);
-                    wv[jn][u] = tb[jq * 64 + lane * wq + (j & 3)];
+                    wv[jn][u] = *(const uint32_t *)(tb + jq * 256 + (j & 3) * 4 + lane16 / 4 * (uint32_t)wq);
                 }
             } else if constexpr (WPW == 2) {
-                const uint2 v = ((const uint2 *)(tb + (j0 >> 2) * 256 + lane * 4))[(j0 >> 1) & 1];
+                const uint2 v = *(const uint2 *)(tb + (j0 >> 2) * 1024 + ((j0 >> 1) & 1) * 8 + lane16);
                 wv[jn][0] = v.x; wv[jn][1] = v.y;
             } else {
 #pragma unroll
                 for (int g = 0; g < WPW / 4; ++g) {
-                    const uint4 v = *(const uint4 *)(tb + ((j0 >> 2) + g) * 256 + lane * 4);
+                    const uint4 v = *(const uint4 *)(tb + ((j0 >> 2) + g) * 1024 + lane16);
                     wv[jn][4 * g] = v.x; wv[jn][4 * g + 1] = v.y; wv[jn][4 * g + 2] = v.z; wv[jn][4 * g + 3] = v.w;
                 }
             }
@@ -117,16 +121,18 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(Params p) {
         for (int c = 0; c < P; ++c)
 #pragma unroll
             for (int i = 0; i < RM; ++i) {
+                // wave-uniform base plus a 32-bit per-lane offset (q spans less than 2 GiB)
                 const int m = min(m0 + i * 16 + (lane & 15), M - 1);
-                const int8_t *row = q + c * part_stride + (long long)m * ldq;
+                const int8_t *part = q + (long long)c * part_stride;
+                const uint32_t row = (uint32_t)m * (uint32_t)ldq;
 #pragma unroll
                 for (int t = 0; t < S; ++t) {
                     const int k = (s0 + t) * 64 + kl;
                     if constexpr (!RAGGED) {
-                        af[c][i][t] = *(const v4i *)(row + k);
+                        af[c][i][t] = *(const v4i *)(part + (long long)s0 * 64 + t * 64 + (row + (uint32_t)kl));
                     } else {
                         // k < kend <= K <= ldq with ldq % 16 == 0: the 16 bytes lie in the row; else load the row start
-                        v4i v = *(const v4i *)(row + (k < kend ? k : 0));
+                        v4i v = *(const v4i *)(part + (row + (uint32_t)(k < kend ? k : 0)));
 #pragma unroll
                         for (int d = 0; d < 4; ++d) {
                             const int valid = kend - (k + 4 * d);  // bytes at k >= kend must not contribute
@@ -139,6 +145,8 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(Params p) {
                 }
             }
     }
+    // the operand loads go out before anything that needs a kernel argument outside the preloaded ones
+    __builtin_amdgcn_sched_barrier(0);
     // epilogue scales of the blocks this wave finishes: raw words now, converted in the epilogue
     uint32_t rs[UB][3], ra[UB][4], rb[UB][4];
     if constexpr (!SLICED) {
@@ -148,7 +156,7 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(Params p) {
             const int i = b / NT, jn = b - (b / NT) * NT;
             const int m = min(m0 + i * 16 + (lane & 15), M - 1);
 #pragma unroll
-            for (int c = 0; c < 3; ++c) rs[u][c] = c < P ? load_raw(qs, qs16, c * qs_stride + m) : 0u;
+            for (int c = 0; c < 3; ++c) rs[u][c] = c < P ? load_raw(qs, qs16, (uint32_t)(c * qs_stride + m)) : 0u;
             const int nb = n0 + jn * 16 + (lane >> 4) * 4;
 #pragma unroll
             for (int r = 0; r < 4; ++r) ra[u][r] = load_raw(ws, ws16, min(nb + r, N - 1));
@@ -161,7 +169,10 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(Params p) {
             }
         }
     }
-    __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first instruction that waits
+    // Every load above is issued before the first instruction that waits. The memory clobber keeps the compiler from
+    // sinking the scale loads to their use in the epilogue, where their latency would stand alone.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- MFMAs: straight-line code over the wave's S k-steps ----
     v4i acc[P][RM][NT];
@@ -235,12 +246,13 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(Params p) {
         } else {
             EpiOperands e;
 #pragma unroll
-            for (int c = 0; c < 3; ++c) e.s[c] = c < P ? raw_to_f32(rs[u][c], qs16, c * qs_stride + m) : 0.f;
+            for (int c = 0; c < 3; ++c)
+                e.s[c] = c < P ? raw_to_f32(rs[u][c], qs16, qs, (uint32_t)(c * qs_stride + m)) : 0.f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int n = min(nb + r, N - 1);
-                e.alpha[r] = raw_to_f32(ra[u][r], ws16, n);
-                e.bias[r] = bias ? raw_to_f32(rb[u][r], b16, n) : kNoBias;
+                e.alpha[r] = raw_to_f32(ra[u][r], ws16, ws, (uint32_t)n);
+                e.bias[r] = bias ? raw_to_f32(rb[u][r], b16, bias, (uint32_t)n) : kNoBias;
             }
             load_residual(p, m, nb, e.res);
             if (plain && mt + 16 <= M && nt + 16 <= N) {

@@ -34,6 +34,11 @@ SIGNATURES = {
     "kea_t2_unlayout_host": (_i32, [_vp, _i64, _i64, _vp]),
     "kea_lowbit_gemm": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _vp, _i32, _i64,
                                _vp, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _i64, _vp]),
+    "kea_lowbit_gemm_plan": (_vp, [_i32, _vp, _i64, _i64, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _vp, _i32, _i64,
+                                    _vp, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _i64, _vp,
+                                    _i64, _f32]),
+    "kea_lowbit_gemm_plan_launch": (_i32, [_vp, _vp]),
+    "kea_lowbit_gemm_plan_free": (None, [_vp]),
     "kea_lowbit_gemm_noalloc": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _vp, _i32,
                                        _i64, _vp, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _i32, _i32, _i32, _vp]),
     "kea_lowbit_gemm_residual": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _vp, _i32,

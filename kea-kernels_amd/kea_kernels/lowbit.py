@@ -41,14 +41,16 @@ def _check_words(words: Tensor, n: int, k: int, wbits: int) -> None:
                          f"{wbits}-bit matrix")
 
 
-def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscale: Tensor, bias: Tensor | None,
-         y: Tensor | None = None, acc_out: Tensor | None = None, *, m: int | None = None, silu: bool = False,
-         order: int = 0, config=None, ws_group: int = 0, residual: Tensor | None = None,
-         residual_factor: float = 1.0, glu: bool = False) -> None:
-    """y[:m] (rows of stride y.stride(0)) and/or acc_out [P, m, N] from q int8 [P, M, ldq] (16-byte aligned rows) and
-    qs [P, M] (f32 or f16). words: native layout of `wbits`-bit weights; wscale [N] (or [N, G] with ws_group).
-    residual (FP32 [>= m, >= N] rows, may be y itself): y = residual + value * residual_factor.
-    glu: y [m, N/2] = value[2j] * sigmoid(value[2j + 1]) (weight rows interleaved value, gate)."""
+@functools.lru_cache(maxsize=1024)
+def _workspace_bytes(wbits: int, parts: int, m: int, n: int, k: int, ws_group: int, split: int, tile: int) -> int:
+    need = _hip.lib().kea_lowbit_gemm_workspace(wbits, parts, m, n, k, ws_group, split, tile)
+    if need < 0:
+        _hip.check(-1, "kea_lowbit_gemm_workspace")
+    return need
+
+
+def _gemm_args(wbits, q, qs, words, n, k, wscale, bias, y, acc_out, m, silu, order, config, ws_group, residual, glu):
+    """Checks the arguments of a GEMM call and returns (C arguments up to the workspace, device, workspace)."""
     if q.dtype != torch.int8 or q.dim() != 3:
         raise ValueError(f"q must be int8 [P, M, ldq], got {q.dtype} {tuple(q.shape)}")
     parts, rows, ldq = q.shape
@@ -82,14 +84,11 @@ def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscal
         raise RuntimeError("the low-bit GEMM is inference only: an input requires grad")
     device = q.device
     _on(device, qs, words, wscale, bias, y, acc_out, residual)
-    L = _hip.lib()
     if config is not None and not hasattr(config, "tile"):
         config = None  # a reference tile tuple (its RTX 5090 tiling): accepted, results never depend on tiles
     tile = 0 if config is None else int(config.tile)
     split = 0 if config is None else int(config.split)
-    need = L.kea_lowbit_gemm_workspace(wbits, parts, max(m, 1), n, k, ws_group, split, tile)
-    if need < 0:
-        _hip.check(-1, "kea_lowbit_gemm_workspace")
+    need = _workspace_bytes(wbits, parts, max(m, 1), n, k, ws_group, split, tile)
     workspace = torch.empty(need, dtype=torch.uint8, device=device) if need else None
     args = (wbits, q.data_ptr(), q.stride(0), ldq, parts,
             qs.data_ptr(), _hip.dtype_code(qs.dtype), qs.stride(0),
@@ -100,11 +99,59 @@ def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscal
             _hip.ptr(acc_out), acc_out.stride(1) if acc_out is not None else 0,
             m, int(silu) | (2 * int(order)) | (4 * int(glu)), split, tile,
             _hip.ptr(workspace), need)
+    return args, device, workspace
+
+
+def gemm(wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscale: Tensor, bias: Tensor | None,
+         y: Tensor | None = None, acc_out: Tensor | None = None, *, m: int | None = None, silu: bool = False,
+         order: int = 0, config=None, ws_group: int = 0, residual: Tensor | None = None,
+         residual_factor: float = 1.0, glu: bool = False) -> None:
+    """y[:m] (rows of stride y.stride(0)) and/or acc_out [P, m, N] from q int8 [P, M, ldq] (16-byte aligned rows) and
+    qs [P, M] (f32 or f16). words: native layout of `wbits`-bit weights; wscale [N] (or [N, G] with ws_group).
+    residual (FP32 [>= m, >= N] rows, may be y itself): y = residual + value * residual_factor.
+    glu: y [m, N/2] = value[2j] * sigmoid(value[2j + 1]) (weight rows interleaved value, gate)."""
+    args, device, _ = _gemm_args(wbits, q, qs, words, n, k, wscale, bias, y, acc_out, m, silu, order, config,
+                                 ws_group, residual, glu)
+    L = _hip.lib()
     if residual is None:
         _hip.check(L.kea_lowbit_gemm(*args, _hip.stream_handle(device)), "kea_lowbit_gemm")
     else:
         _hip.check(L.kea_lowbit_gemm_residual(*args, residual.data_ptr(), residual.stride(0), float(residual_factor),
                                               _hip.stream_handle(device)), "kea_lowbit_gemm_residual")
+
+
+class GemmPlan:
+    """A GEMM call validated once: the checks of gemm() and the library's tile / split / kernel resolution run here
+    (kea_lowbit_gemm_plan), and each call only enqueues the launch (kea_lowbit_gemm_plan_launch) on the given stream
+    or torch's current stream. Same arguments as gemm(). The plan keeps references to every tensor it was built on
+    (they must keep their storage: the plan launches on those buffers) and its own split-K workspace."""
+
+    def __init__(self, wbits: int, q: Tensor, qs: Tensor, words: Tensor, n: int, k: int, wscale: Tensor,
+                 bias: Tensor | None, y: Tensor | None = None, acc_out: Tensor | None = None, *, m: int | None = None,
+                 silu: bool = False, order: int = 0, config=None, ws_group: int = 0, residual: Tensor | None = None,
+                 residual_factor: float = 1.0, glu: bool = False):
+        args, self.device, workspace = _gemm_args(wbits, q, qs, words, n, k, wscale, bias, y, acc_out, m, silu,
+                                                  order, config, ws_group, residual, glu)
+        self._keep = (q, qs, words, wscale, bias, y, acc_out, residual, workspace)
+        L = _hip.lib()
+        self._free = L.kea_lowbit_gemm_plan_free
+        self._launch = L.kea_lowbit_gemm_plan_launch
+        self._handle = L.kea_lowbit_gemm_plan(*args, _hip.ptr(residual), residual.stride(0) if residual is not None
+                                              else 0, float(residual_factor))
+        if not self._handle:
+            _hip.check(-1, "kea_lowbit_gemm_plan")
+
+    def __call__(self, stream: int | None = None) -> None:
+        """Enqueue the GEMM on `stream` (a hipStream_t handle, e.g. torch.cuda.Stream.cuda_stream) or on torch's
+        current stream."""
+        rc = self._launch(self._handle, _hip.stream_handle(self.device) if stream is None else stream)
+        if rc:
+            _hip.check(rc, "kea_lowbit_gemm_plan_launch")
+
+    def __del__(self):
+        handle, self._handle = getattr(self, "_handle", None), None
+        if handle:
+            self._free(handle)
 
 
 def gemm_slices(wbits: int, q: Tensor, words: Tensor, n: int, k: int, slices: Tensor, *, m: int | None = None,

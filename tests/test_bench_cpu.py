@@ -45,6 +45,13 @@ def test_config1_accounting():
 
 def test_traffic_comes_from_the_committed_profile():
     data = json.loads((ROOT / "profiles" / "b1_gemm_config1_traffic.json").read_text())
-    assert bench.traffic_from_profiles() == data["hbm_bytes_per_launch"]
+    assert bench.traffic_from_profiles() == (data["hbm_bytes_per_launch"], data.get("kernel_sources_sha"))
     assert data["hbm_bytes_per_launch"] == data["fetch_bytes_per_launch"] + data["write_bytes_per_launch"]
     assert data["algorithmic_bytes_per_launch"] == bench.BYTES
+
+
+def test_kernel_source_hash_names_the_build():
+    """The hash a traffic profile is labeled with covers every kernel source and nothing else."""
+    h = bench.kernel_sources_sha()
+    assert len(h) == 16 and h == bench.kernel_sources_sha()
+    int(h, 16)

@@ -168,3 +168,18 @@ def test_tile_and_split_tables_are_pure_functions():
         assert s >= 1
         ws = L.kea_lowbit_gemm_workspace(1, 1, m, n, k, 0, 0, 0)
         assert ws == (s * m * n * 4 if s > 1 else 0)
+
+
+def test_plan_refuses_what_the_direct_call_refuses():
+    """kea_lowbit_gemm_plan returns NULL (with the same message) on arguments kea_lowbit_gemm refuses; nothing is
+    launched and no device is touched."""
+    L = _hip.lib()
+    h = L.kea_lowbit_gemm_plan(3, None, 0, 16, 1, None, 0, 1, None, 64, 64, None, 0, 0, None, 0, None, 0, 64, None,
+                               0, 1, 0, 0, 0, None, 0, None, 0, 1.0)
+    assert not h and b"wbits" in L.kea_last_error()
+    h = L.kea_lowbit_gemm_plan(1, ctypes.c_void_p(8), 0, 64, 1, ctypes.c_void_p(16), 0, 1, ctypes.c_void_p(16), 64,
+                               64, ctypes.c_void_p(16), 0, 0, None, 0, ctypes.c_void_p(16), 0, 64, None, 0, 1, 0, 0,
+                               0, None, 0, None, 0, 1.0)
+    assert not h and b"aligned" in L.kea_last_error()
+    assert L.kea_lowbit_gemm_plan_launch(None, None) == -1
+    L.kea_lowbit_gemm_plan_free(None)

@@ -229,6 +229,36 @@ def test_leading_rows_of_a_taller_q(wbits, k, split):
     assert torch.isnan(y[m:]).all()
 
 
+@pytest.mark.parametrize("wbits,m,n,k,config", [(1, 128, 4096, 1024, None), (2, 40, 300, 4096, (4, 4)),
+                                                 (1, 70, 200, 1152, (kernels.tile_count(), 0))])
+@torch.inference_mode()
+def test_plan_launches_equal_direct_calls(wbits, m, n, k, config):
+    """lowbit.GemmPlan (kea_lowbit_gemm_plan + _launch): validated once, launched twice, the same bits as gemm()
+    and the oracle, including a split-K plan (its own workspace) and a residual epilogue."""
+    case = Case(wbits, 1, m, n, k, seed=46 + m, bias=True)
+    cfg = None if config is None else kernels.GemmConfig(*config)
+    y_ref, acc_ref = case.run(config=cfg)
+    assert_parity(case, y_ref, acc_ref)
+    y = torch.full((m, n), float("nan"), device=DEV, dtype=torch.float16)
+    acc = torch.full((1, m, n), -7, device=DEV, dtype=torch.int32)
+    plan = lowbit.GemmPlan(wbits, case.dq, case.dqs, case.words, n, k, case.dalpha, case.dbias, y, acc, config=cfg)
+    for _ in range(2):
+        y.fill_(float("nan"))
+        plan()
+        torch.cuda.synchronize()
+        assert torch.equal(y.cpu().view(torch.int16), y_ref.view(torch.int16))
+        assert np.array_equal(acc.cpu().numpy(), acc_ref)
+    # residual epilogue through a plan: y = r + value * 0.5, against gemm(residual=...)
+    r = torch.randn(m, n, generator=torch.Generator().manual_seed(3)).to(DEV)
+    y1, y2 = torch.empty(m, n, device=DEV), torch.empty(m, n, device=DEV)
+    lowbit.gemm(wbits, case.dq, case.dqs, case.words, n, k, case.dalpha, case.dbias, y1, None, config=cfg,
+                residual=r, residual_factor=0.5)
+    lowbit.GemmPlan(wbits, case.dq, case.dqs, case.words, n, k, case.dalpha, case.dbias, y2, None, config=cfg,
+                    residual=r, residual_factor=0.5)()
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
+
+
 @torch.inference_mode()
 def test_zero_rows_is_a_no_op():
     case = Case(1, 1, 4, 64, 128, seed=1)
