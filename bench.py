@@ -426,34 +426,49 @@ def suite() -> None:
         print(json.dumps({"case": name, **row}), flush=True)
 
 
-# the chooser's shapes: BASELINE configs 1-4, the encoder's linears at batch 1 and 8 (M = 125, 1000), the reference's
-# tuned (N, K, M) points, each at one, two and three activation parts
-SWEEP_SHAPES = sorted({(n, k) for n, k in [(4096, 1024), (1024, 4096), (3072, 1024), (1024, 1024), (2048, 1024),
-                                           (2560, 640), (1030, 640)]})
-SWEEP_M = (1, 4, 16, 38, 64, 125, 128, 192, 256, 368, 512, 750, 1000)
+# the chooser's shapes: BASELINE configs 1-4 and the encoder's linears (N, K) at M from single tokens to batch 8 of
+# 125 frames, the reference's tuned M points among them (kk/binary/configs.py:17-36)
+SWEEP_SHAPES = [(4096, 1024), (1024, 4096), (3072, 1024), (1024, 1024), (2048, 1024), (2560, 640), (1030, 640)]
+SWEEP_M = (1, 16, 38, 64, 126, 256, 368, 512, 1000)
 
 
 def sweep(parts_list=(1, 2, 3), wbits_list=(1, 2)) -> None:
-    """One JSON line per (wbits, parts, M, N, K): the per-launch microseconds of every tile configuration of the
-    library (split 0: the library's split for that tile) and which one the chooser picks. The committed chooser
-    table is read from these lines."""
+    """One JSON line per (wbits, parts, M, N, K): per-launch microseconds of every tile configuration of the library
+    (split 0: the library's split for that tile; fp16 scales and output, HIP-graph replay of 100 launches behind a
+    spin) and the tile the chooser picks. The chooser table (csrc/kea_gemm_table.h) is read from these lines."""
     import torch
-    from kea_kernels.binary import configs, kernels
+    from kea_kernels import formats, lowbit
+    from kea_kernels.binary import bits, configs, kernels
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.Stream(dev)
     ntiles = kernels.tile_count()
     for wbits in wbits_list:
-        for parts in parts_list:
-            for n, k in SWEEP_SHAPES:
+        for n, k in SWEEP_SHAPES:
+            g = torch.Generator().manual_seed(n + k + wbits)
+            if wbits == 1:
+                codes = bits.pack_signs(torch.where(torch.rand(n, k, generator=g) < 0.5, -1, 1).to(torch.int8))
+            else:
+                codes = formats.pack_ternary(torch.randint(-1, 2, (n, k), generator=g, dtype=torch.int8))
+            words = kernels.relayout_codes(codes, k, wbits).to(dev)
+            alpha = (torch.rand(n, generator=g) * 0.09 + 0.01).half().to(dev)
+            for parts in parts_list:
                 for m in SWEEP_M:
+                    ldq = -(-k // 16) * 16
+                    q = torch.randint(-127, 128, (parts, m, ldq), generator=g, dtype=torch.int8).to(dev)
+                    qs = (torch.rand(parts, m, generator=g) * 0.01 + 1e-3).half().to(dev)
+                    y = torch.empty(m, n, dtype=torch.float16, device=dev)
                     row = {"wbits": wbits, "parts": parts, "M": m, "N": n, "K": k,
                            "chosen": configs.choose(m, n, k, parts, wbits).tile}
                     for tile in range(1, ntiles + 1):
                         try:
-                            r = _suite_case(wbits, parts, m, n, k, scale_dtype=torch.float16,
-                                            out_dtype=torch.float16, seed=m + n + k, reps=300,
-                                            config=kernels.GemmConfig(tile, 0))
+                            plan = lowbit.GemmPlan(wbits, q, qs, words, n, k, alpha, None, y, None,
+                                                   config=kernels.GemmConfig(tile, 0))
                         except ValueError:
                             continue  # the tile does not fit this part count / K
-                        row[f"t{tile}"] = r["us"]
+                        graph = capture(stream, lambda i: plan(), 100)
+                        replay_timed(stream, [graph])
+                        row[f"t{tile}"] = round(replay_timed(stream, [graph], 3) * 1000 / 300, 3)
+                        del graph, plan
                     print(json.dumps(row), flush=True)
 
 

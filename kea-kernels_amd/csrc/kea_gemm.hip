@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <mutex>
@@ -29,6 +30,7 @@
 #include "kea_epilogue.h"
 #include "kea_gemm_common.h"
 #include "kea_gemm_ring.h"
+#include "kea_gemm_table.h"
 #include "kea_gemm_wsplit.h"
 #include "kea_internal.h"
 
@@ -117,19 +119,10 @@ FinishFn pick_finish(int parts) {
     return finish_kernel<3>;
 }
 
-// Tile and split choice: a pure function of (wbits, parts, m, n, k), fitted to MI355X sweeps of every tile x split
-// over BASELINE.json's shapes, the reference's tuned (N, K, M) points and the encoder's shapes at P = 1, 2 and 3 (HIP
-// graph replay, M from 1 to 1000). Small M wants many workgroups: the 16x64 (P >= 2) and 32x32 (P = 1) tiles, whose
-// register budgets leave room for co-resident workgroups. As M grows the activation tile, re-read once per column
-// tile, becomes the traffic that bounds a CU, so the winners widen in N: 32x64 / 64x64 at P = 1, and at P >= 2 (where
-// the activations are P times larger) the eight-wavefront 32x128 and 64x256 tiles, 10-17% faster than the
-// four-wavefront ones at M = 1000.
-int choose_tile(int wbits, int parts, long long m, long long n, long long k) {
-    (void)wbits;
-    // Small M, one part: the wave-split kernel, whose launches are set by memory latency rather than by the matrix
-    // cores (MI355X, HIP-graph replay: config 1 4.35 -> 3.86 us, config 2 7.88 -> 4.36 us, M = 16 at K = 4096
-    // 5.69 -> 3.86 us). 16x32 tiles while that grid stays within 320 workgroups, 16x64 above.
-    if (parts == 1 && m <= 256 && k <= 4096) return cdivl(m, 16) * cdivl(n, 32) <= 320 ? kNumTiles + 6 : kNumTiles + 3;
+// The LDS-ring tile for shapes the measured table cannot serve (see choose_tile): small M wants many workgroups (the
+// 16x64 tile at P >= 2, 32x32 at P = 1); as M grows the activation tile, re-read once per column tile, bounds a CU,
+// so the winners widen in N.
+int ring_tile(int parts, long long m, long long n) {
     if (parts >= 3) {
         if (m >= 850) return n >= 4096 ? 10 : 12;
         if (n <= 1024) return 1;
@@ -147,6 +140,38 @@ int choose_tile(int wbits, int parts, long long m, long long n, long long k) {
     if (m < 512) return ((n >= 4096 && m >= 192) || (n >= 3072 && m >= 320)) ? 2 : 4;
     if (m < 850) return n <= 1024 ? 4 : n >= 4096 ? 5 : m < 600 ? 2 : 5;
     return n <= 1024 ? 2 : n >= 4096 ? 11 : 5;
+}
+
+// Tile choice: a pure function of (wbits, parts, m, n, k) read from the table measured on MI355X (kea_gemm_table.h:
+// the fastest tile of every swept shape). Rows of the same weight width, part count, N and K give the tile of the
+// nearest swept M in log scale; other shapes take the nearest entry of the same width and part count in
+// (log M, log N, log K), K and N weighted above M.
+int choose_tile(int wbits, int parts, long long m, long long n, long long k) {
+    struct Logs {
+        float m[kTileTableSize], n[kTileTableSize], k[kTileTableSize];
+        Logs() {
+            for (int i = 0; i < kTileTableSize; ++i) {
+                m[i] = std::log2((float)kTileTable[i].m);
+                n[i] = std::log2((float)kTileTable[i].n);
+                k[i] = std::log2((float)kTileTable[i].k);
+            }
+        }
+    };
+    static const Logs logs;  // built once (thread-safe static initialisation)
+    const float lm = std::log2((float)std::max(1LL, m)), ln = std::log2((float)n), lk = std::log2((float)k);
+    int best = 0;
+    float best_d = 1e30f;
+    for (int i = 0; i < kTileTableSize; ++i) {
+        const TileChoice &e = kTileTable[i];
+        if (e.wbits != wbits || e.parts != parts) continue;
+        const float dm = lm - logs.m[i], dn = ln - logs.n[i], dk = lk - logs.k[i];
+        const float d = (e.n == n && e.k == k) ? std::fabs(dm) : 1e6f + dm * dm + 4.f * dn * dn + 4.f * dk * dk;
+        if (d < best_d) {
+            best_d = d;
+            best = e.tile;
+        }
+    }
+    return best ? best : ring_tile(parts, m, n);
 }
 
 // Split factor for split_k == 0: split K only for long K ranges (>= 2048) whose tiling leaves at most 64 workgroups,
@@ -193,6 +218,16 @@ static int resolve(int wbits, int parts, int64_t m, int64_t n, int64_t k, int sp
     if (config < 0 || config > kNumTiles + kNumWsplitTiles) return kea::fail(KEA_EINVAL, "unknown config id");
     if (split_k < 0) return kea::fail(KEA_EINVAL, "split_k must be >= 0");
     int id = config ? config : choose_tile(wbits, parts, m, n, k);
+    if (!config && id > kNumTiles) {
+        // an automatic wave-split pick must fit its registers and LDS, run unsplit when K % 16 != 0, and honour a
+        // requested split exactly (the K range of one of its workgroups is at least nw * 2 k-steps)
+        const WsplitTile &wt = kWsplitTiles[id - kNumTiles - 1];
+        const long long ksteps = cdivl(k, 64), want = split_k > 1 ? split_k : 1;
+        const int s = kea::wsplit_steps(wbits, cdivl(ksteps, want), wt.nw);
+        const bool ok = s && kea::wsplit_fits(wbits, parts, wt, s) && (!(k & 15) || s * wt.nw * 64 >= k) &&
+                        (split_k <= 1 || cdivl(ksteps, (long long)wt.nw * s) == split_k);
+        if (!ok) id = ring_tile(parts, m, n);
+    }
     if (id > kNumTiles) {
         // wave-split tile: a workgroup covers nw waves x s k-steps; the split is raised to what the K range needs
         const WsplitTile &wt = kWsplitTiles[id - kNumTiles - 1];
