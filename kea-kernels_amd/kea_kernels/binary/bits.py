@@ -76,11 +76,8 @@ def dense_weight(codes: Tensor, scale: Tensor, in_features: int, dtype: torch.dt
 
 def resident_bytes(*tensors: Tensor | None) -> int:
     """Bytes of the distinct GPU storages behind `tensors` (a view counts its whole storage once)."""
-    sizes: dict[int, int] = {}
-    for t in tensors:
-        if t is None or not t.is_cuda:
-            continue
-        storage = t.untyped_storage()
-        key = storage.data_ptr()
-        sizes[key] = max(sizes.get(key, 0), storage.nbytes())
-    return sum(sizes.values())
+    storages = {(s.data_ptr(), s.nbytes()) for s in (t.untyped_storage() for t in tensors if t is not None and t.is_cuda)}
+    largest: dict[int, int] = {}
+    for ptr, nbytes in storages:
+        largest[ptr] = max(nbytes, largest.get(ptr, 0))
+    return sum(largest.values())

@@ -1,6 +1,6 @@
 """The 1-bit layers at the projection-provider seam (drop-in for kk/binary/provider.py).
 
-Every quantized-layer call of the encoder goes through one `provider` object (kk/binary/provider.py:3-15):
+The contract kept from the reference (kk/binary/provider.py:3-23):
 
     provider(x, mod, conv=False, components=3, activation="", norm=None, config=None, input_activation="")
 
@@ -11,251 +11,286 @@ Every quantized-layer call of the encoder goes through one `provider` object (kk
     y  = y * sigmoid(y) if activation == "silu" else y
     return y.transpose(1, 2) if conv else y          # conv returns a [B, N, T] view
 
-`components` is the number of residual int8 activation parts. Modules carry no GPU weights: a module's `packed_t` is
-a CPU int64 row HANDLE [1, N] (global row ids), and torch.cat of the Q/K/V handles yields the handle of the fused
-[3072, 1024] QKV layer, which the provider resolves to that layer (kk/binary/provider.py:17-23, :78-79). The 1-bit
-layer objects (Int8MmaLayer / Int8MmaPartsLayer) hold the only GPU copy of the weights.
+`components` is the number of residual int8 activation parts. A module's `packed_t` is a CPU int64 row HANDLE [1, N]
+of global row ids, and torch.cat of the Q/K/V handles of one block is the handle of their fused [3072, 1024] layer.
+
+How this module keeps it: every prepared layer owns a contiguous range of a global row space (RowSpace, searched by
+bisection); modules are views of row ranges (BinaryLinear / BinaryPointwiseConv1d, subclasses of the ternary packed
+modules because encoder transforms dispatch on those types); BinaryProjection resolves a handle once per handle
+tensor and runs the layer's fused op, slicing the rows a member handle names. The layer objects (Int8MmaLayer /
+Int8MmaPartsLayer) hold the only GPU copy of the weights.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass, field
+import bisect
+from dataclasses import dataclass
 from pathlib import Path
 
 import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
+from kea_kernels.ternary.runtime import PackedLinear, PackedPointwiseConv1d
+
 QKV = ("linear_q", "linear_k", "linear_v")
 
 
-@dataclass
-class Entry:
-    """One prepared 1-bit layer and the global row-handle range of its outputs."""
+@dataclass(frozen=True)
+class Segment:
+    """A prepared layer's rows [first, first + out_features) of the global row space."""
     name: str
     layer: object
     kind: str            # "linear" or "conv"
+    first: int
     out_features: int
     in_features: int
-    start: int           # first global row id
-    members: tuple = ()  # a fused QKV entry: the three module names
+    members: tuple = ()  # a fused QKV layer: the names of the modules that are its row slices
+
+    @property
+    def stop(self) -> int:
+        return self.first + self.out_features
 
 
-@dataclass
-class Table:
-    entries: list = field(default_factory=list)
-    next_row: int = 0
+class RowSpace:
+    """Global row ids of the prepared layers: each layer is allocated the next contiguous range."""
 
-    def add(self, name, layer, kind, n, k, members=()) -> Entry:
-        entry = Entry(name, layer, kind, n, k, self.next_row, tuple(members))
-        self.entries.append(entry)
-        self.next_row += n
-        return entry
+    def __init__(self):
+        self.segments: list[Segment] = []
+        self._firsts: list[int] = []
 
-    def resolve(self, start: int, count: int) -> tuple[Entry, int]:
-        """(entry, offset) of the layer whose rows [start, start + count) are; ValueError across layers."""
-        for entry in self.entries:
-            if entry.start <= start < entry.start + entry.out_features:
-                if start + count > entry.start + entry.out_features:
-                    raise ValueError("handle range crosses layers")
-                return entry, start - entry.start
-        raise KeyError(f"no layer owns row handle {start}")
+    @property
+    def rows(self) -> int:
+        return self.segments[-1].stop if self.segments else 0
+
+    def allocate(self, name: str, layer, kind: str, out_features: int, in_features: int, members=()) -> Segment:
+        segment = Segment(name, layer, kind, self.rows, out_features, in_features, tuple(members))
+        self.segments.append(segment)
+        self._firsts.append(segment.first)
+        return segment
+
+    def locate(self, first: int, count: int) -> tuple[Segment, int]:
+        """(segment, offset) of the layer owning rows [first, first + count): KeyError when no layer owns `first`,
+        ValueError when the range runs past the end of that layer."""
+        i = bisect.bisect_right(self._firsts, first) - 1
+        if i < 0 or first >= self.segments[i].stop:
+            raise KeyError(f"no layer owns row handle {first}")
+        segment = self.segments[i]
+        if first + count > segment.stop:
+            raise ValueError(f"row handle [{first}, {first + count}) crosses layers")
+        return segment, first - segment.first
 
     def weight_bytes(self) -> int:
-        return sum(entry.layer.weight_bytes() for entry in self.entries)
+        return sum(segment.layer.weight_bytes() for segment in self.segments)
 
 
-def _handle(start: int, n: int) -> Tensor:
-    return torch.arange(start, start + n, dtype=torch.int64).view(1, n)
+def row_handle(first: int, count: int) -> Tensor:
+    """The CPU int64 [1, count] handle of rows first .. first + count - 1."""
+    return torch.arange(first, first + count, dtype=torch.int64).unsqueeze(0)
 
 
-class _BinaryMixin:
-    """The attributes encoder transforms read: in_features, out_features, mode, packed_t (a row handle), scale, bias."""
+def _bind_rows(module: nn.Module, segment: Segment, offset: int, out_features: int, scale: Tensor,
+               bias: Tensor | None) -> None:
+    """Makes `module` the view of rows [offset, offset + out_features) of `segment`'s layer. The attributes the encoder
+    transforms read (packed_t = the row handle, scale, bias) are plain host attributes: never moved to the GPU and
+    absent from state_dict."""
+    nn.Module.__init__(module)
+    module.in_features, module.out_features, module.mode = segment.in_features, out_features, "binary"
+    module._segment, module._offset = segment, offset
+    for name, value in (("packed_t", row_handle(segment.first + offset, out_features)),
+                        ("scale", scale.detach().clone().contiguous()),
+                        ("bias", None if bias is None else bias.detach().clone().contiguous())):
+        object.__setattr__(module, name, value)
+    module.eval()
 
-    def _setup(self, entry: Entry, offset: int, n: int, k: int, scale_cpu: Tensor, bias_cpu: Tensor | None):
-        nn.Module.__init__(self)
-        self.in_features, self.out_features, self.mode = k, n, "binary"
-        self._entry, self._offset = entry, offset
-        # plain attributes, not buffers: never moved to the GPU, absent from state_dict
-        object.__setattr__(self, "packed_t", _handle(entry.start + offset, n))
-        object.__setattr__(self, "scale", scale_cpu.detach().clone().contiguous())
-        object.__setattr__(self, "bias", None if bias_cpu is None else bias_cpu.detach().clone().contiguous())
-        self.eval()
 
-    def _run(self, x: Tensor, conv: bool) -> Tensor:
-        entry = self._entry
-        y = entry.layer.conv(x) if conv else entry.layer.linear(x)
-        if self.out_features == entry.out_features:
-            return y
-        lo, hi = self._offset, self._offset + self.out_features  # a member of a fused layer called alone
-        return y[:, lo:hi] if conv else y[..., lo:hi]
+def _rows_forward(module, x: Tensor, conv: bool) -> Tensor:
+    segment = module._segment
+    y = segment.layer.conv(x) if conv else segment.layer.linear(x)
+    if module.out_features == segment.out_features:
+        return y
+    rows = slice(module._offset, module._offset + module.out_features)  # a member of a fused layer, called alone
+    return y[:, rows] if conv else y[..., rows]
+
+
+class BinaryLinear(PackedLinear):
+    """A linear module standing for rows of a prepared 1-bit layer."""
+
+    def __init__(self, segment: Segment, offset: int, out_features: int, scale: Tensor, bias: Tensor | None = None):
+        _bind_rows(self, segment, offset, out_features, scale, bias)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return _rows_forward(self, x, conv=False)
 
     def extra_repr(self):
-        return f"in_features={self.in_features}, out_features={self.out_features}, layer={self._entry.name!r}"
+        return f"in_features={self.in_features}, out_features={self.out_features}, layer={self._segment.name!r}"
 
 
-def _packed_classes():
-    """BinaryLinear / BinaryPointwiseConv1d: subclasses of the ternary packed modules, as encoder transforms that
-    dispatch on module type expect (kk/binary/provider.py:107-124)."""
-    from kea_kernels.ternary.runtime import PackedLinear, PackedPointwiseConv1d
+class BinaryPointwiseConv1d(PackedPointwiseConv1d):
+    """A pointwise Conv1d ([B, K, T] -> [B, N, T]) standing for rows of a prepared 1-bit layer."""
 
-    class BinaryLinear(_BinaryMixin, PackedLinear):
-        def __init__(self, *a):
-            self._setup(*a)
+    def __init__(self, segment: Segment, offset: int, out_features: int, scale: Tensor, bias: Tensor | None = None):
+        _bind_rows(self, segment, offset, out_features, scale, bias)
 
-        def forward(self, x):
-            return self._run(x, False)
+    def forward(self, x: Tensor) -> Tensor:
+        return _rows_forward(self, x, conv=True)
 
-    class BinaryPointwiseConv1d(_BinaryMixin, PackedPointwiseConv1d):
-        def __init__(self, *a):
-            self._setup(*a)
+    def extra_repr(self):
+        return f"in_features={self.in_features}, out_features={self.out_features}, layer={self._segment.name!r}"
 
-        def forward(self, x):
-            return self._run(x, True)
 
-    return BinaryLinear, BinaryPointwiseConv1d
+_ACTIVATIONS = ("", "silu")
 
 
 class BinaryProjection:
-    """The provider object: resolves a module's row handle to its layer and runs the fused op."""
+    """The provider object: resolves a module's row handle to its prepared layer and runs the fused op."""
 
-    def __init__(self, table: Table, names: dict | None = None):
+    def __init__(self, table: RowSpace, names: dict | None = None):
         self.table = table
-        self._resolved: dict = {}
         self.names = names or {}
+        self._handles: dict = {}  # id(handle tensor) -> (handle, segment, offset, count)
 
     @property
     def bytes(self) -> int:
         return self.table.weight_bytes()
 
-    def _lookup(self, mod) -> tuple[Entry, int, int]:
+    def resolve(self, mod) -> tuple[Segment, int, int]:
+        """(segment, offset, count) of the rows `mod.packed_t` names (cached per handle tensor)."""
         handle = mod.packed_t
-        key = (handle.data_ptr(), tuple(handle.shape))
-        hit = self._resolved.get(key)
-        if hit is None:
-            if handle.is_cuda or handle.dtype != torch.int64 or handle.dim() != 2 or handle.shape[0] != 1:
-                raise TypeError("BinaryProjection serves BinaryLinear / BinaryPointwiseConv1d handles only")
-            start, count = int(handle[0, 0]), handle.shape[1]
-            if not torch.equal(handle[0], torch.arange(start, start + count)):
-                raise ValueError("non-contiguous row handle")
-            entry, offset = self.table.resolve(start, count)
-            hit = (entry, offset, count)
-            self._resolved[key] = hit
-        return hit
+        hit = self._handles.get(id(handle))
+        if hit is not None and hit[0] is handle:
+            return hit[1:]
+        if not isinstance(handle, Tensor) or handle.device.type != "cpu" or handle.dtype != torch.int64 \
+                or handle.dim() != 2 or handle.shape[0] != 1:
+            raise TypeError("BinaryProjection serves the CPU int64 [1, N] row handles of BinaryLinear / "
+                            "BinaryPointwiseConv1d")
+        first, count = int(handle[0, 0]), handle.shape[1]
+        if not torch.equal(handle, row_handle(first, count)):
+            raise ValueError("non-contiguous row handle")
+        segment, offset = self.table.locate(first, count)
+        self._handles[id(handle)] = (handle, segment, offset, count)
+        return segment, offset, count
 
     def __call__(self, x, mod, conv=False, components=3, activation="", norm=None, config=None, input_activation=""):
         if config is not None:
             raise ValueError("BinaryProjection takes no tile config")
-        if activation not in ("", "silu") or input_activation not in ("", "silu"):
+        if activation not in _ACTIVATIONS or input_activation not in _ACTIVATIONS:
             raise ValueError(f"unsupported activation {activation!r} / {input_activation!r}")
-        entry, offset, count = self._lookup(mod)
-        layer = entry.layer
+        segment, offset, count = self.resolve(mod)
+        layer = segment.layer
         if hasattr(layer, "project"):
             y = layer.project(x, conv=conv, components=components, activation=activation, norm=norm,
                               input_activation=input_activation)
-        else:  # a layer object with linear / conv only: unfused LayerNorm / SiLU around it
-            z = x.transpose(1, 2) if conv else x
-            if norm is not None:
-                z = F.layer_norm(z, norm.normalized_shape, norm.weight, norm.bias, norm.eps)
-            if input_activation == "silu":
-                z = F.silu(z)
-            y = layer.linear(z)
-            if activation == "silu":
-                y = F.silu(y)
-            if conv:
-                y = y.transpose(1, 2)
-        if count != entry.out_features:
-            y = y[:, offset:offset + count] if conv else y[..., offset:offset + count]
-        return y
+        else:
+            y = _unfused(layer, x, conv, activation, norm, input_activation)
+        if count == segment.out_features:
+            return y
+        rows = slice(offset, offset + count)
+        return y[:, rows] if conv else y[..., rows]
+
+
+def _unfused(layer, x: Tensor, conv: bool, activation: str, norm, input_activation: str) -> Tensor:
+    """The provider semantics around a layer object that has linear() only."""
+    z = x.transpose(1, 2) if conv else x
+    if norm is not None:
+        z = F.layer_norm(z, norm.normalized_shape, norm.weight, norm.bias, norm.eps)
+    if input_activation == "silu":
+        z = F.silu(z)
+    y = layer.linear(z)
+    if activation == "silu":
+        y = F.silu(y)
+    return y.transpose(1, 2) if conv else y
 
 
 class PartCount:
-    """Wraps a provider and sets `components` (the int8 activation part count) to n on every call, including callers
-    that hard-code components=3. Attribute writes other than (provider, n) reach the wrapped provider
+    """A provider wrapper that runs every call at `n` activation parts (whatever `components` the caller passes).
+    Reads of other attributes and writes other than `provider` / `n` go to the wrapped provider
     (kk/binary/provider.py:185-209)."""
 
-    OWN = ("provider", "n")
+    _OWN = frozenset(("provider", "n"))
 
     def __init__(self, provider, n: int):
         if n not in (1, 2, 3):
             raise ValueError("n must be 1, 2 or 3")
-        object.__setattr__(self, "provider", provider)
-        object.__setattr__(self, "n", n)
-
-    def __setattr__(self, name, value):
-        if name in PartCount.OWN:
-            object.__setattr__(self, name, value)
-        else:
-            setattr(self.provider, name, value)
+        self.__dict__.update(provider=provider, n=n)
 
     def __call__(self, x, mod, conv=False, components=3, activation="", norm=None, config=None, input_activation=""):
         return self.provider(x, mod, conv, self.n, activation, norm, config, input_activation)
 
     def __getattr__(self, name):
-        return getattr(self.provider, name)
+        return getattr(self.__dict__["provider"], name)
+
+    def __setattr__(self, name, value):
+        if name in PartCount._OWN:
+            self.__dict__[name] = value
+        else:
+            setattr(self.provider, name, value)
+
+
+def _unpack_item(item) -> tuple:
+    """(codes, scale, bias, kind, in_features) from a layer item (codes, scale, bias, kind[, in_features])."""
+    codes, scale, bias, kind = item[:4]
+    return codes, scale, bias, kind, (item[4] if len(item) > 4 else 8 * codes.shape[1])
 
 
 def prepare_table(layers: dict, layer_cls, device="cuda", *, fuse_qkv: bool = True):
-    """Table and modules from {name: (codes, scale, bias, kind)} without NeMo: Q/K/V of one attention block are
-    prepared as one fused layer (the handles of the three modules are row slices of it). Returns (table, modules)."""
-    BinaryLinear, BinaryPointwiseConv1d = _packed_classes()
-    table = Table()
-    modules = {}
-    pending = dict(layers)
+    """(RowSpace, {name: module}) from {name: (codes, scale, bias, kind[, in_features])} without NeMo. With fuse_qkv,
+    the Q, K and V linears of one attention block (equal shapes, no bias) are prepared as one layer and their three
+    modules are row slices of it."""
+    space, modules = RowSpace(), {}
+    fused = set()
     if fuse_qkv:
-        blocks = sorted({name.rsplit(".", 1)[0] for name in layers if name.endswith("." + QKV[0])})
+        blocks = sorted({name[: -len(QKV[0]) - 1] for name in layers if name.endswith("." + QKV[0])})
         for block in blocks:
-            names = [f"{block}.{q}" for q in QKV]
+            names = [f"{block}.{member}" for member in QKV]
             if not all(name in layers for name in names):
                 continue
-            shapes = {tuple(layers[name][0].shape) for name in names}
-            if len(shapes) != 1 or any(layers[name][2] is not None or layers[name][3] != "linear" for name in names):
+            items = [_unpack_item(layers[name]) for name in names]
+            if len({tuple(codes.shape) for codes, *_ in items}) != 1 or \
+                    any(bias is not None or kind != "linear" for _, _, bias, kind, _ in items):
                 raise ValueError(f"{block}: Q/K/V must be equal-shape bias-free linear layers")
-            k = layers[names[0]][4] if len(layers[names[0]]) > 4 else 8 * layers[names[0]][0].shape[1]
-            n = layers[names[0]][0].shape[0]
-            codes = torch.cat([layers[name][0] for name in names])
-            scales = torch.cat([layers[name][1] for name in names])
-            layer = layer_cls.prepare(codes, scales, None, k, device)
-            entry = table.add(f"{block}.qkv", layer, "linear", 3 * n, k, names)
+            n, k = items[0][0].shape[0], items[0][4]
+            codes = torch.cat([item[0] for item in items])
+            scales = torch.cat([item[1] for item in items])
+            segment = space.allocate(f"{block}.qkv", layer_cls.prepare(codes, scales, None, k, device), "linear",
+                                     3 * n, k, names)
             for i, name in enumerate(names):
-                modules[name] = BinaryLinear(entry, i * n, n, k, scales[i * n:(i + 1) * n], None)
-                del pending[name]
-    for name, item in pending.items():
-        codes, scale, bias, kind = item[:4]
-        k = item[4] if len(item) > 4 else 8 * codes.shape[1]
-        layer = layer_cls.prepare(codes, scale, bias, k, device)
-        entry = table.add(name, layer, kind, codes.shape[0], k)
+                modules[name] = BinaryLinear(segment, i * n, n, scales[i * n:(i + 1) * n])
+            fused.update(names)
+    for name, item in layers.items():
+        if name in fused:
+            continue
+        codes, scale, bias, kind, k = _unpack_item(item)
+        segment = space.allocate(name, layer_cls.prepare(codes, scale, bias, k, device), kind, codes.shape[0], k)
         cls = BinaryPointwiseConv1d if kind == "conv" else BinaryLinear
-        modules[name] = cls(entry, 0, codes.shape[0], k, scale, bias)
-    return table, modules
+        modules[name] = cls(segment, 0, codes.shape[0], scale, bias)
+    return space, modules
 
 
 def load_binary_model(directory, manifest: dict, layer_cls, device="cuda", *, fuse_qkv: bool = True):
-    """(NeMo model on `device`, Table) from a validated parakeet-binary-v1 export (kk/binary/provider.py:212-262).
-
-    Needs nemo_toolkit (not installed in this build's image): RuntimeError from formats.build_nemo otherwise."""
+    """(NeMo model on `device`, RowSpace) from a validated parakeet-binary-v1 export: the 264 quantized modules
+    replaced by row views of prepared 1-bit layers, every other tensor loaded as FP32. Needs nemo_toolkit
+    (RuntimeError from formats.build_nemo without it)."""
     from safetensors.torch import load_file
 
     from kea_kernels import formats
     directory = Path(directory)
-    device = torch.device(device)
     model = formats.build_nemo(manifest, directory)
     tensors = load_file(directory / manifest["file"])
     layers = {}
     for name, info in manifest["quantized_layers"].items():
-        n, k = info["shape"]
-        bias = tensors.pop(f"{name}.bias") if info["bias"] else None
         kind = "conv" if info["kind"] == "pointwise_conv1d" else "linear"
-        layers[name] = (tensors.pop(f"{name}.codes"), tensors.pop(f"{name}.scale"), bias, kind, k)
-    table, modules = prepare_table(layers, layer_cls, device, fuse_qkv=fuse_qkv)
+        bias = tensors.pop(f"{name}.bias") if info["bias"] else None
+        layers[name] = (tensors.pop(f"{name}.codes"), tensors.pop(f"{name}.scale"), bias, kind, info["shape"][1])
+    space, modules = prepare_table(layers, layer_cls, torch.device(device), fuse_qkv=fuse_qkv)
     for name, module in modules.items():
-        original = model.get_submodule(name)
-        if tuple(original.weight.shape[:2]) != (module.out_features, module.in_features):
+        if tuple(model.get_submodule(name).weight.shape[:2]) != (module.out_features, module.in_features):
             raise ValueError(f"invalid shape for {name}")
         model.set_submodule(name, module)
-    state = {key: value.float() if value.is_floating_point() else value for key, value in tensors.items()}
-    model.load_state_dict(state, strict=True)
-    return model.to(device=device).eval(), table
+    model.load_state_dict({key: value.float() if value.is_floating_point() else value
+                           for key, value in tensors.items()}, strict=True)
+    return model.to(device=torch.device(device)).eval(), space
 
 
 def module_names(model) -> dict:
-    return {id(m): n for n, m in model.named_modules()}
+    """{id(module): qualified name} of every module of `model`."""
+    return {id(module): name for name, module in model.named_modules()}

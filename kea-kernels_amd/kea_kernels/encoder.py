@@ -482,7 +482,7 @@ class FastConformerEncoder:
         (kea_lowbit_gemm_residual; r is not used afterwards). Dense: PyTorch."""
         if self.dense:
             return torch.add(r, self._linear(name, z, input_activation=input_activation), alpha=factor)
-        layer = self.modules[name]._entry.layer
+        layer = self.modules[name]._segment.layer
         b, t, k = z.shape
         m, n = b * t, layer.out_features
         q, qs, _ = lowbit.quantize(z, (z.stride(0), z.stride(1), z.stride(2), t), m, k, self.parts,
@@ -496,11 +496,11 @@ class FastConformerEncoder:
         """The prepared layer behind `name` (the fused QKV handle resolves through the provider's table)."""
         mod = self._fused.get(name)
         if mod is None:
-            return self.modules[name]._entry.layer
-        entry, offset, count = self.project._lookup(mod)
-        if offset or count != entry.out_features:
+            return self.modules[name]._segment.layer
+        segment, offset, count = self.project.resolve(mod)
+        if offset or count != segment.out_features:
             raise ValueError(f"{name} does not cover a whole prepared layer")
-        return entry.layer
+        return segment.layer
 
     def _gemm(self, name: str, q: Tensor, qs: Tensor, m: int, *, silu: bool = False, glu: bool = False) -> Tensor:
         """The quantized linear `name` on pre-quantized activations (q, qs): FP32 [m, N] (glu: [m, N/2])."""

@@ -10,10 +10,12 @@ The Kea-B 0.1 download is an 8-bit bundle ("keab-8bit-v1") whose `compat/` direc
 """
 from __future__ import annotations
 
+import copy
 import hashlib
 import json
 import math
 import re
+import struct
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -83,6 +85,10 @@ def unpack_ternary(packed: Tensor, in_features: int) -> Tensor:
 
 
 # --- exports ------------------------------------------------------------------------------------------------------
+# What the checks keep from the reference (kk/formats.py:84-189): the format strings, the order in which an export
+# is rejected (format, listed file, hashes, model target, layer names, per-layer tensors) and the message fragments
+# callers match on. How they run is this module's own: a table of format handlers for describe(), a list of checks
+# for check_export(), and the safetensors header parsed directly (no tensor is read).
 
 @dataclass(frozen=True)
 class ModelDir:
@@ -93,6 +99,17 @@ class ModelDir:
     default_mode: str
 
 
+@dataclass(frozen=True)
+class _Layout:
+    """One export format: its manifest / metadata string and how many weight codes a byte holds."""
+    format: str
+    codes_per_byte: int
+
+
+_LAYOUTS = {"binary": _Layout(BINARY_FORMAT, 8), "ternary": _Layout(TERNARY_FORMAT, 4)}
+_LAYER_KINDS = ("linear", "pointwise_conv1d")
+
+
 def read_manifest(directory: Path) -> dict:
     path = Path(directory) / MANIFEST
     if not path.is_file():
@@ -100,95 +117,146 @@ def read_manifest(directory: Path) -> dict:
     return json.loads(path.read_text())
 
 
+def safetensors_header(path: Path) -> dict:
+    """The header of a safetensors file without reading any tensor: its first 8 bytes are the little-endian length of
+    a UTF-8 JSON object mapping each tensor name to {"dtype", "shape", "data_offsets"}, plus "__metadata__"."""
+    with open(path, "rb") as handle:
+        raw = handle.read(8)
+        if len(raw) != 8:
+            raise ValueError(f"{path}: not a safetensors file")
+        (length,) = struct.unpack("<Q", raw)
+        if length > (64 << 20):
+            raise ValueError(f"{path}: implausible safetensors header length {length}")
+        header = handle.read(length)
+    try:
+        return json.loads(header)
+    except ValueError as exc:
+        raise ValueError(f"{path}: unreadable safetensors header") from exc
+
+
+# describe(): one handler per manifest format
+
+def _describe_bundle(directory: Path, manifest: dict) -> ModelDir:
+    """Kea-B 0.1: an 8-bit bundle whose compat/ directory is a binary export recording the bundle's hash."""
+    compat = directory / COMPAT_DIR
+    if not (compat / MANIFEST).is_file():
+        raise ValueError(f"{directory}: a {BUNDLE_FORMAT} bundle without its {COMPAT_DIR}/ export; download the "
+                         "whole repository")
+    inner = describe(compat)
+    if inner.kind != "binary":
+        raise ValueError(f"{compat}: expected a {BINARY_FORMAT} export")
+    keab = (read_manifest(compat).get("extra") or {}).get("keab") or {}
+    if keab.get("bundle_sha256") != manifest.get("sha256"):
+        raise ValueError(f"{compat}: its manifest does not record this directory's bundle")
+    return inner
+
+
+def _describe_binary(directory: Path, manifest: dict) -> ModelDir:
+    # the compat export of a Kea-B 0.1 bundle carries extra.keab; its default mode is one part
+    if (manifest.get("extra") or {}).get("keab"):
+        return ModelDir("kea-b-0.1", "binary", directory, "x1")
+    return ModelDir("kea-b", "binary", directory, "x2")
+
+
+def _describe_ternary(directory: Path, manifest: dict) -> ModelDir:
+    return ModelDir("kea-t", "ternary", directory, "x2")
+
+
+_DESCRIBE = {BUNDLE_FORMAT: _describe_bundle, BINARY_FORMAT: _describe_binary, TERNARY_FORMAT: _describe_ternary}
+
+
 def describe(directory) -> ModelDir:
     """Which model `directory` holds: a Kea-B 0.1 bundle, a Kea-B or Kea-T export, or an export inside a bundle."""
     directory = Path(directory).expanduser().resolve()
     manifest = read_manifest(directory)
-    fmt = manifest.get("format")
-    if fmt == BUNDLE_FORMAT:
-        compat = directory / COMPAT_DIR
-        if not (compat / MANIFEST).is_file():
-            raise ValueError(f"{directory}: a {BUNDLE_FORMAT} bundle without its {COMPAT_DIR}/ export; download the "
-                             "whole repository")
-        inner = describe(compat)
-        if inner.kind != "binary":
-            raise ValueError(f"{compat}: expected a {BINARY_FORMAT} export")
-        recorded = ((read_manifest(compat).get("extra") or {}).get("keab") or {}).get("bundle_sha256")
-        if recorded != manifest.get("sha256"):
-            raise ValueError(f"{compat}: its manifest does not record this directory's bundle")
-        return inner
-    if fmt == BINARY_FORMAT:
-        if (manifest.get("extra") or {}).get("keab"):
-            return ModelDir("kea-b-0.1", "binary", directory, "x1")
-        return ModelDir("kea-b", "binary", directory, "x2")
-    if fmt == TERNARY_FORMAT:
-        return ModelDir("kea-t", "ternary", directory, "x2")
-    raise ValueError(f"{directory}: unsupported format {fmt!r} (expected {BINARY_FORMAT}, {TERNARY_FORMAT} or "
-                     f"{BUNDLE_FORMAT})")
+    handler = _DESCRIBE.get(manifest.get("format"))
+    if handler is None:
+        raise ValueError(f"{directory}: unsupported format {manifest.get('format')!r} (expected {BINARY_FORMAT}, "
+                         f"{TERNARY_FORMAT} or {BUNDLE_FORMAT})")
+    return handler(directory, manifest)
+
+
+# check_export(): the checks, in the order a broken export is reported
+
+def _check_format(directory, manifest, layout, verify):
+    if manifest.get("format") != layout.format:
+        raise ValueError(f"{directory}: export format {manifest.get('format')!r}, expected {layout.format!r}")
+
+
+def _check_files(directory, manifest, layout, verify):
+    files = manifest.get("files") or {}
+    if manifest.get("file") != FILE or FILE not in files:
+        raise ValueError(f"{directory}: manifest does not list {FILE}")
+    if not verify:
+        return
+    for rel, digest in files.items():
+        path = directory / rel
+        if not path.is_file() or sha256_file(path) != digest:
+            raise ValueError(f"{path} does not match the manifest SHA-256")
+
+
+def _check_target(directory, manifest, layout, verify):
+    target = (manifest.get("config") or {}).get("target")
+    if target != MODEL_TARGET:
+        raise ValueError(f"{directory}: unexpected model target {target!r}")
+
+
+def _check_layer_names(directory, manifest, layout, verify):
+    names = list((manifest.get("quantized_layers") or {}).keys())
+    if len(names) != EXPECTED_MODULES or any(QUANTIZED_PATTERN.fullmatch(name) is None for name in names):
+        raise ValueError(f"{directory}: expected the {EXPECTED_MODULES} Parakeet quantized layers, got {len(names)}")
+
+
+def _check_tensors(directory, manifest, layout, verify):
+    header = safetensors_header(directory / FILE)
+    if (header.get("__metadata__") or {}).get("format") != layout.format:
+        raise ValueError(f"{directory}: safetensors metadata format is not {layout.format!r}")
+    for name, info in manifest["quantized_layers"].items():
+        if info.get("kind") not in _LAYER_KINDS:
+            raise ValueError(f"{name}: unknown kind {info.get('kind')!r}")
+        n, k = info["shape"]
+        if f"{name}.weight" in header:
+            raise ValueError(f"{name}: dense weight present in a quantized export")
+        width = -(-k // layout.codes_per_byte)
+        codes, scale = header.get(f"{name}.codes") or {}, header.get(f"{name}.scale") or {}
+        if codes.get("dtype") != "U8" or codes.get("shape") != [n, width]:
+            raise ValueError(f"{name}: codes must be uint8 [{n}, {width}]")
+        if scale.get("dtype") != "F32" or scale.get("shape") != [n]:
+            raise ValueError(f"{name}: scale must be FP32 [{n}]")
+        if bool(info.get("bias")) != (f"{name}.bias" in header):
+            raise ValueError(f"{name}: bias presence differs from the manifest")
+
+
+_EXPORT_CHECKS = (_check_format, _check_files, _check_target, _check_layer_names, _check_tensors)
 
 
 def check_export(directory, kind: str, *, verify_hashes: bool = True) -> dict:
     """The manifest of an intact parakeet-binary-v1 / parakeet-ternary-v1 export of the 264 Parakeet layers.
 
-    Checks the format (manifest and safetensors metadata), every listed file's SHA-256 (unless verify_hashes is
-    False), the 264 layer names and kinds, and each layer's codes / scale / bias dtype and shape without loading the
-    tensors. ValueError otherwise (kk/formats.py:130-173)."""
-    from safetensors import safe_open
+    Runs, in order: the manifest's format, the listed export file and (unless verify_hashes is False) every listed
+    file's SHA-256, the model target, the 264 layer names, and each layer's kind and codes / scale / bias dtypes and
+    shapes as the safetensors header records them. ValueError at the first failure."""
+    if kind not in _LAYOUTS:
+        raise ValueError(f"unknown export kind {kind!r} (binary or ternary)")
     directory = Path(directory)
     manifest = read_manifest(directory)
-    fmt = {"binary": BINARY_FORMAT, "ternary": TERNARY_FORMAT}[kind]
-    if manifest.get("format") != fmt:
-        raise ValueError(f"{directory}: export format {manifest.get('format')!r}, expected {fmt!r}")
-    files = manifest.get("files", {})
-    if manifest.get("file") != FILE or FILE not in files:
-        raise ValueError(f"{directory}: manifest does not list {FILE}")
-    if verify_hashes:
-        for rel, digest in files.items():
-            path = directory / rel
-            if not path.is_file() or sha256_file(path) != digest:
-                raise ValueError(f"{path} does not match the manifest SHA-256")
-    if (manifest.get("config") or {}).get("target") != MODEL_TARGET:
-        raise ValueError(f"{directory}: unexpected model target {(manifest.get('config') or {}).get('target')!r}")
-    layers = manifest.get("quantized_layers") or {}
-    if len(layers) != EXPECTED_MODULES or not all(QUANTIZED_PATTERN.fullmatch(name) for name in layers):
-        raise ValueError(f"{directory}: expected the {EXPECTED_MODULES} Parakeet quantized layers, got {len(layers)}")
-    per_byte = 8 if kind == "binary" else 4
-    with safe_open(directory / FILE, framework="pt") as f:
-        if (f.metadata() or {}).get("format") != fmt:
-            raise ValueError(f"{directory}: safetensors metadata format is not {fmt!r}")
-        keys = set(f.keys())
-        for name, info in layers.items():
-            if info.get("kind") not in ("linear", "pointwise_conv1d"):
-                raise ValueError(f"{name}: unknown kind {info.get('kind')!r}")
-            n, k = info["shape"]
-            if f"{name}.weight" in keys:
-                raise ValueError(f"{name}: dense weight present in a quantized export")
-            codes, scale = f.get_slice(f"{name}.codes"), f.get_slice(f"{name}.scale")
-            width = math.ceil(k / per_byte)
-            if codes.get_dtype() != "U8" or codes.get_shape() != [n, width]:
-                raise ValueError(f"{name}: codes must be uint8 [{n}, {width}]")
-            if scale.get_dtype() != "F32" or scale.get_shape() != [n]:
-                raise ValueError(f"{name}: scale must be FP32 [{n}]")
-            if bool(info.get("bias")) != (f"{name}.bias" in keys):
-                raise ValueError(f"{name}: bias presence differs from the manifest")
+    for check in _EXPORT_CHECKS:
+        check(directory, manifest, _LAYOUTS[kind], verify_hashes)
     return manifest
 
 
 def build_nemo(manifest: dict, directory: Path):
-    """An FP32 NeMo EncDecRNNTBPEModel from the manifest's config (needs nemo_toolkit, which this image lacks)."""
+    """An FP32 NeMo EncDecRNNTBPEModel from the manifest's config, pointed at the export's own tokenizer files and
+    with no datasets (needs nemo_toolkit[asr] and omegaconf; RuntimeError without them)."""
     try:
         from nemo.collections.asr.models import EncDecRNNTBPEModel
-        from omegaconf import OmegaConf, open_dict
+        from omegaconf import OmegaConf
     except ImportError as exc:
         raise RuntimeError("building the NeMo model needs nemo_toolkit[asr] and omegaconf, which are not "
                            "installed") from exc
-    directory = Path(directory)
-    cfg = OmegaConf.create(manifest["config"])
-    with open_dict(cfg):
-        cfg.tokenizer.dir = str(directory / TOKENIZER_DIR)
-        for key, filename in TOKENIZER_FILES.items():
-            cfg.tokenizer[key] = str(directory / TOKENIZER_DIR / filename)
-        for ds in ("train_ds", "validation_ds", "test_ds"):
-            if ds in cfg:
-                cfg[ds] = None
-    return EncDecRNNTBPEModel(cfg=cfg)
+    cfg = copy.deepcopy(manifest["config"])
+    tokenizer_dir = Path(directory) / TOKENIZER_DIR
+    cfg["tokenizer"] = {**(cfg.get("tokenizer") or {}), "dir": str(tokenizer_dir),
+                        **{key: str(tokenizer_dir / name) for key, name in TOKENIZER_FILES.items()}}
+    cfg.update({section: None for section in ("train_ds", "validation_ds", "test_ds") if section in cfg})
+    return EncDecRNNTBPEModel(cfg=OmegaConf.create(cfg))

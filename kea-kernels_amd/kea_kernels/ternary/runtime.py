@@ -48,28 +48,42 @@ def native_words(mod) -> torch.Tensor:
     return native
 
 
+def _finite_f32_vector(t, n: int) -> bool:
+    return t.shape == (n,) and t.dtype == torch.float32 and bool(torch.isfinite(t).all())
+
+
+def _validate(packed: torch.Tensor, scale: torch.Tensor, in_features: int, bias: torch.Tensor | None,
+              mode: str) -> None:
+    """The module's argument checks, in the reference's order and with its messages (kk/ternary/runtime.py:12-31):
+    dimensions, one device, valid 2-bit codes (the 11 pattern and tail codes raise), finite FP32 scale and bias of
+    length N, a known mode."""
+    from kea_kernels.formats import unpack_ternary
+    if in_features < 1 or packed.ndim != 2 or packed.shape[0] < 1:
+        raise ValueError("weight dimensions must be positive")
+    if any(t is not None and t.device != packed.device for t in (scale, bias)):
+        raise ValueError("codes, scales, and bias must be on the same device")
+    unpack_ternary(packed, in_features)
+    n = packed.shape[0]
+    if not _finite_f32_vector(scale, n):
+        raise ValueError("scale must be finite FP32 [N]")
+    if bias is not None and not _finite_f32_vector(bias, n):
+        raise ValueError("bias must be finite FP32 [N]")
+    if mode not in MODES:
+        raise ValueError(f"unknown mode {mode!r}")
+
+
 class PackedLinear(nn.Module):
+    """A ternary linear layer kept 2 bits per weight on the GPU: `packed_t` (the reference's resident words) and
+    `native` (the gfx950 layout the int8 GEMM reads); forward quantizes x to `parts` int8 parts and runs the GEMM."""
+
     def __init__(self, packed: torch.Tensor, scale: torch.Tensor, in_features: int, bias: torch.Tensor | None = None,
                  *, mode: str = "bf16x3"):
         super().__init__()
-        from kea_kernels.formats import unpack_ternary
-        if in_features < 1 or packed.ndim != 2 or packed.shape[0] < 1:
-            raise ValueError("weight dimensions must be positive")
-        if packed.device != scale.device or (bias is not None and bias.device != packed.device):
-            raise ValueError("codes, scales, and bias must be on the same device")
-        unpack_ternary(packed, in_features)  # validates: the 11 pattern and tail codes raise
-        n = packed.shape[0]
-        if scale.shape != (n,) or scale.dtype != torch.float32 or not bool(torch.isfinite(scale).all()):
-            raise ValueError("scale must be finite FP32 [N]")
-        if bias is not None and (bias.shape != (n,) or bias.dtype != torch.float32
-                                 or not bool(torch.isfinite(bias).all())):
-            raise ValueError("bias must be finite FP32 [N]")
-        if mode not in MODES:
-            raise ValueError(f"unknown mode {mode!r}")
-        self.in_features, self.out_features, self.mode = in_features, n, mode
+        _validate(packed, scale, in_features, bias, mode)
+        self.in_features, self.out_features, self.mode = in_features, packed.shape[0], mode
         self.register_buffer("packed_t", packed_t_from_codes(packed))
         self.register_buffer("scale", scale.contiguous())
-        self.register_buffer("bias", bias.contiguous() if bias is not None else None)
+        self.register_buffer("bias", None if bias is None else bias.contiguous())
         self.register_buffer("native", layout.relayout_codes(packed.cpu(), in_features, 2).to(packed.device),
                              persistent=False)
         self.eval()
@@ -92,32 +106,32 @@ class PackedPointwiseConv1d(PackedLinear):
         return int8_matmul(x, self, conv=True, components=self.parts)
 
 
-def load_packed(directory: str | Path, manifest: dict, device: str | torch.device = "cuda", *, mode: str = "bf16x3"):
-    """A NeMo model from a validated export with the 264 ternary layers packed (kk/ternary/runtime.py:52-82).
+_PACKED_KINDS = {"linear": PackedLinear, "pointwise_conv1d": PackedPointwiseConv1d}
+LOADER_MODES = ("tf32x3", "bf16x3")
 
-    Needs nemo_toolkit (not installed in this build's image): RuntimeError from formats.build_nemo otherwise."""
+
+def load_packed(directory: str | Path, manifest: dict, device: str | torch.device = "cuda", *, mode: str = "bf16x3"):
+    """A NeMo model from a validated parakeet-ternary-v1 export with its 264 quantized modules replaced by packed
+    modules built from the export's codes (no dense ternary weight is formed) and every other tensor loaded as FP32.
+    Needs nemo_toolkit (RuntimeError from formats.build_nemo without it)."""
     from safetensors.torch import load_file
 
     from kea_kernels import formats
-    if mode not in ("tf32x3", "bf16x3"):
+    if mode not in LOADER_MODES:
         raise ValueError("the model loader requires a high-accuracy mode (tf32x3 or bf16x3)")
-    device = torch.device(device)
     directory = Path(directory)
-    layers = manifest["quantized_layers"]
     model = formats.build_nemo(manifest, directory)
     tensors = load_file(directory / manifest["file"])
-    packed_state = {}
-    for name, layer in layers.items():
-        original = model.get_submodule(name)
-        n, k = layer["shape"]
-        if tuple(original.weight.shape[:2]) != (n, k):
+    state = {}
+    for name, info in manifest["quantized_layers"].items():
+        n, k = info["shape"]
+        if tuple(model.get_submodule(name).weight.shape[:2]) != (n, k):
             raise ValueError(f"invalid shape for {name}")
-        cls = {"linear": PackedLinear, "pointwise_conv1d": PackedPointwiseConv1d}[layer["kind"]]
-        module = cls(tensors.pop(f"{name}.codes"), tensors.pop(f"{name}.scale"), k,
-                     tensors.pop(f"{name}.bias") if layer["bias"] else None, mode=mode)
+        bias = tensors.pop(f"{name}.bias") if info["bias"] else None
+        module = _PACKED_KINDS[info["kind"]](tensors.pop(f"{name}.codes"), tensors.pop(f"{name}.scale"), k, bias,
+                                             mode=mode)
         model.set_submodule(name, module)
-        packed_state.update((f"{name}.{key}", value) for key, value in module.state_dict().items())
-    state = {key: value.float() if value.is_floating_point() else value for key, value in tensors.items()}
-    state.update(packed_state)
+        state.update({f"{name}.{key}": value for key, value in module.state_dict().items()})
+    state.update({key: value.float() if value.is_floating_point() else value for key, value in tensors.items()})
     model.load_state_dict(state, strict=True)
-    return model.to(device=device).eval()
+    return model.to(device=torch.device(device)).eval()

@@ -239,16 +239,17 @@ def _layers(n=16, k=32, seed=0):
 def test_table_fuses_qkv_and_hands_out_row_handles():
     layers = _layers()
     table, modules = provider.prepare_table(layers, DenseLayer, "cpu")
-    names = [e.name for e in table.entries]
-    assert names[0] == "enc.0.self_attn.qkv" and table.entries[0].out_features == 48
+    names = [s.name for s in table.segments]
+    assert names[0] == "enc.0.self_attn.qkv" and table.segments[0].out_features == 48
     q, k, v = (modules[f"enc.0.self_attn.{x}"] for x in provider.QKV)
     assert torch.equal(torch.cat([q.packed_t, k.packed_t, v.packed_t], 1), torch.arange(48).view(1, 48))
-    assert table.resolve(16, 16) == (table.entries[0], 16)
-    assert table.resolve(0, 48) == (table.entries[0], 0)
+    assert table.locate(16, 16) == (table.segments[0], 16)
+    assert table.locate(0, 48) == (table.segments[0], 0)
+    assert table.locate(48, 16) == (table.segments[1], 0)
     with pytest.raises(ValueError, match="crosses"):
-        table.resolve(40, 16)
+        table.locate(40, 16)
     with pytest.raises(KeyError):
-        table.resolve(10_000, 1)
+        table.locate(10_000, 1)
     assert all(not isinstance(getattr(m, "packed_t"), torch.nn.Parameter) for m in modules.values())
     assert "packed_t" not in q.state_dict()
 

@@ -193,7 +193,7 @@ def test_binary_provider_table_and_part_count_on_gpu():
     y = proj(x, handle)
     assert y.shape == (2, 19, 3 * n)
     assert torch.equal(proj(x, kk), y[..., n:2 * n])
-    qkv_layer = table.entries[0].layer
+    qkv_layer = table.segments[0].layer
     assert torch.equal(y, qkv_layer.project(x))
     ff = modules["b.0.feed_forward1.linear1"]
     ff_codes, ff_scale, ff_bias = layers["b.0.feed_forward1.linear1"][:3]
@@ -201,7 +201,7 @@ def test_binary_provider_table_and_part_count_on_gpu():
     for parts, tol in [(1, 2e-2), (2, 1e-4), (3, 1e-6)]:
         yp = provider.PartCount(proj, parts)(x, ff, components=3)
         assert (yp.cpu().double() - ref).norm() / ref.norm() < tol
-    assert table.weight_bytes() == sum(e.layer.weight_bytes() for e in table.entries)
+    assert table.weight_bytes() == sum(s.layer.weight_bytes() for s in table.segments)
 
 
 def test_layer_errors_match_the_reference_contract():
