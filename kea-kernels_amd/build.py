@@ -21,7 +21,8 @@ CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "kea_kernels" / "lib" / "libkea_hip.so"
 SOURCES = ["kea_gemm_ring_w1.hip", "kea_gemm_ring_w2.hip", "kea_gemm_wsplit_p1.hip", "kea_gemm_wsplit_p2.hip",
-           "kea_gemm_wsplit_p3.hip", "kea_gemm.hip", "kea_gemm_wsplit.hip", "kea_quantize.hip", "kea_encoder.hip",
+           "kea_gemm_wsplit_p3.hip", "kea_gemm_rows_p1.hip", "kea_gemm_rows_p2.hip", "kea_gemm_rows_p3.hip",
+           "kea_gemm.hip", "kea_gemm_wsplit.hip", "kea_quantize.hip", "kea_encoder.hip",
            "kea_probe.hip", "kea_layout.cpp"]
 ARCH = "gfx950"
 # Per-source flags. The probe's loop keeps eight MFMA accumulators live across iterations; in the accumulator
@@ -30,8 +31,10 @@ ARCH = "gfx950"
 SOURCE_FLAGS = {"kea_probe.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 # The wave-split kernels take their load operands as ten leading scalar arguments (4 pointers, 6 ints: 14 SGPRs) that
 # the dispatch preloads into SGPRs, so the first loads issue without a kernel-argument round trip.
+# The row-quantizing kernels likewise take eight (3 pointers, 5 ints: 11 SGPRs).
 for _p in (1, 2, 3):
     SOURCE_FLAGS[f"kea_gemm_wsplit_p{_p}.hip"] = ["-mllvm", "-amdgpu-kernarg-preload-count=10"]
+    SOURCE_FLAGS[f"kea_gemm_rows_p{_p}.hip"] = ["-mllvm", "-amdgpu-kernarg-preload-count=8"]
 
 
 def hipcc() -> str:

@@ -1,0 +1,143 @@
+// The parts of the wave-split GEMM that do not depend on where the activation fragments come from, shared by the
+// int8-input kernel (kea_gemm_wsplit_inst.h) and the kernel that quantizes FP32 rows itself (kea_gemm_rows_inst.h):
+// the weight loads, the MFMA sequence, the exact LDS reduction over the waves and the epilogue dispatch of one
+// 16x16 block. Every function is force-inlined over compile-time shapes, so the arrays stay in registers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kea_gemm_common.h"
+
+namespace kea {
+
+// The aligned 32-bit word holding element i of an f32 or f16 vector (f16: the half is selected at conversion time by
+// raw_to_f32 with the same v and i). The word lies inside the 4-byte block of an in-bounds element, so it never
+// reaches past a page the vector touches.
+__device__ __forceinline__ uint32_t load_raw(const void *v, bool f16, uint32_t i) {
+    const char *a = (const char *)v + (f16 ? 2u * i : 4u * i);
+    return *(const uint32_t *)__builtin_align_down(a, 4);  // keeps the pointer's (global) address space
+}
+__device__ __forceinline__ float raw_to_f32(uint32_t raw, bool f16, const void *v, uint32_t i) {
+    const uint32_t hi = (uint32_t)(((uintptr_t)v >> 1) + i) & 1u;  // f16: which half of the word
+    const float h = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw >> (hi * 16)));
+    return f16 ? h : __builtin_bit_cast(float, raw);
+}
+
+// The wave's weight words: WPW native words per lane for each of the NT n-tiles from the tile at column n0, starting
+// at word j0 (J words per lane per n-tile). RAGGED = false: complete quads of words (or one word per wave), loaded
+// with 64- or 128-bit vector loads; otherwise general per-word addressing (a short last quad has lane stride < 4,
+// words past J load any valid word, whose activations are zero).
+template <int NT, int WPW, bool RAGGED>
+__device__ __forceinline__ void wsplit_load_w(const uint32_t *w, int n0, int NTILES, int J, int j0, uint32_t lane16,
+                                              uint32_t (&wv)[NT][WPW]) {
+#pragma unroll
+    for (int jn = 0; jn < NT; ++jn) {
+        // wave-uniform base of the n-tile's words, plus a 32-bit per-lane byte offset (SGPR-base loads)
+        const int t = min((n0 >> 4) + jn, NTILES - 1);
+        const char *tb = (const char *)(w + (long long)t * J * 64);
+        if constexpr (WPW == 1 || RAGGED) {
+#pragma unroll
+            for (int u = 0; u < WPW; ++u) {
+                const int j = min(j0 + u, J - 1), jq = j & ~3;
+                const int wq = min(4, J - jq);
+                wv[jn][u] = *(const uint32_t *)(tb + jq * 256 + (j & 3) * 4 + lane16 / 4 * (uint32_t)wq);
+            }
+        } else if constexpr (WPW == 2) {
+            const uint2 v = *(const uint2 *)(tb + (j0 >> 2) * 1024 + ((j0 >> 1) & 1) * 8 + lane16);
+            wv[jn][0] = v.x; wv[jn][1] = v.y;
+        } else {
+#pragma unroll
+            for (int g = 0; g < WPW / 4; ++g) {
+                const uint4 v = *(const uint4 *)(tb + ((j0 >> 2) + g) * 1024 + lane16);
+                wv[jn][4 * g] = v.x; wv[jn][4 * g + 1] = v.y; wv[jn][4 * g + 2] = v.z; wv[jn][4 * g + 3] = v.w;
+            }
+        }
+    }
+}
+
+// Straight-line MFMAs over the wave's S k-steps: each weight word is expanded once (1 bit: v_and + v_perm per 4
+// weights, two k-steps per word; 2 bits: one k-step per word) and feeds the RM row blocks x P parts of
+// v_mfma_i32_16x16x64_i8 with the weights as the A operand.
+template <int WBITS, int P, int RM, int NT, int S, int WPW>
+__device__ __forceinline__ void wsplit_mfma(const uint32_t (&wv)[NT][WPW], const v4i (&af)[P][RM][S],
+                                            v4i (&acc)[P][RM][NT]) {
+    constexpr int KSW = WBITS == 1 ? 2 : 1;
+#pragma unroll
+    for (int c = 0; c < P; ++c)
+#pragma unroll
+        for (int i = 0; i < RM; ++i)
+#pragma unroll
+            for (int jn = 0; jn < NT; ++jn) acc[c][i][jn] = (v4i){0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+        const int u = t / KSW, h = t % KSW;
+#pragma unroll
+        for (int jn = 0; jn < NT; ++jn) {
+            const uint32_t w32 = wv[jn][u];
+            v4i bf;
+            if constexpr (WBITS == 1) {
+                if (h == 0) {
+                    bf[0] = b1_expand<0>(w32); bf[1] = b1_expand<1>(w32); bf[2] = b1_expand<2>(w32); bf[3] = b1_expand<3>(w32);
+                } else {
+                    bf[0] = b1_expand<4>(w32); bf[1] = b1_expand<5>(w32); bf[2] = b1_expand<6>(w32); bf[3] = b1_expand<7>(w32);
+                }
+            } else {
+                const uint32_t w4 = w32 >> 4;
+                bf[0] = t2_lo(w32); bf[1] = t2_hi(w32); bf[2] = t2_lo(w4); bf[3] = t2_hi(w4);
+            }
+#pragma unroll
+            for (int c = 0; c < P; ++c)
+#pragma unroll
+                for (int i = 0; i < RM; ++i)
+                    acc[c][i][jn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af[c][i][t], acc[c][i][jn], 0, 0, 0);
+        }
+    }
+}
+
+// Writes the wave's partial tile to its LDS slice ([P][RM][NT][64 lanes][4] int32); a barrier must follow.
+template <int P, int RM, int NT>
+__device__ __forceinline__ void wsplit_share(int32_t *mine, int lane, const v4i (&acc)[P][RM][NT]) {
+#pragma unroll
+    for (int c = 0; c < P; ++c)
+#pragma unroll
+        for (int i = 0; i < RM; ++i)
+#pragma unroll
+            for (int jn = 0; jn < NT; ++jn) *(v4i *)(mine + ((c * RM + i) * NT + jn) * 256 + lane * 4) = acc[c][i][jn];
+}
+
+// The exact sum over the NW wave partials of block (i, jn) for this lane's 4 outputs, in wave order.
+template <int P, int RM, int NT, int NW>
+__device__ __forceinline__ void wsplit_block_sum(const int32_t *red, int i, int jn, int lane, int (&a)[P][4]) {
+    constexpr int PART = P * RM * NT * 256;
+#pragma unroll
+    for (int c = 0; c < P; ++c) {
+        const int32_t *src = red + ((c * RM + i) * NT + jn) * 256 + lane * 4;
+        v4i sum = *(const v4i *)src;
+#pragma unroll
+        for (int v = 1; v < NW; ++v) sum += *(const v4i *)(src + v * PART);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a[c][r] = sum[r];
+    }
+}
+
+// The epilogue of row m, columns nb .. nb + 3 of the block at (mt, nt) of an M x N output: one vector store of
+// compile-time dtype when the block is whole and the output plain (`plain`), else the general epilogue.
+template <int P>
+__device__ __forceinline__ void wsplit_epilogue(const Params &p, bool plain, int M, int N, int m, int mt, int nt,
+                                                int nb, const int (&a)[P][4], const EpiOperands &e) {
+    if (plain && mt + 16 <= M && nt + 16 <= N) {
+        if (p.y_dtype == KEA_F16) {
+            epilogue4_full<P, KEA_F16, false, true>(p, (uint16_t *)p.y + (long long)m * p.ldy, nb, a, e);
+        } else if (p.y_dtype == KEA_BF16) {
+            epilogue4_full<P, KEA_BF16, false, true>(p, (uint16_t *)p.y + (long long)m * p.ldy, nb, a, e);
+        } else {
+            epilogue4_full<P, KEA_F32, false, true>(p, (float *)p.y + (long long)m * p.ldy, nb, a, e);
+        }
+    } else {
+        epilogue4<P>(p, m, nb, a, e);
+    }
+}
+
+}  // namespace kea

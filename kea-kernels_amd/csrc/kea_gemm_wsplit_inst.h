@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "kea_gemm_wsplit.h"
+#include "kea_gemm_wsplit_body.h"
 
 #ifndef KEA_WSPLIT_P
 #error "define KEA_WSPLIT_P (1, 2 or 3) before including kea_gemm_wsplit_inst.h"
@@ -35,19 +36,6 @@
 namespace {
 
 using namespace kea;
-
-// The aligned 32-bit word holding element i of an f32 or f16 vector (f16: the half is selected at conversion time by
-// raw_to_f32 with the same v and i). The word lies inside the 4-byte block of an in-bounds element, so it never
-// reaches past a page the vector touches.
-__device__ __forceinline__ uint32_t load_raw(const void *v, bool f16, uint32_t i) {
-    const char *a = (const char *)v + (f16 ? 2u * i : 4u * i);
-    return *(const uint32_t *)__builtin_align_down(a, 4);  // keeps the pointer's (global) address space
-}
-__device__ __forceinline__ float raw_to_f32(uint32_t raw, bool f16, const void *v, uint32_t i) {
-    const uint32_t hi = (uint32_t)(((uintptr_t)v >> 1) + i) & 1u;  // f16: which half of the word
-    const float h = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw >> (hi * 16)));
-    return f16 ? h : __builtin_bit_cast(float, raw);
-}
 
 // RAGGED = false: the host guarantees that every wave's K range is whole (K % 64 == 0, the workgroup's range a
 // multiple of NW * S k-steps) and that its weight words lie in complete quads (J % 4 == 0 or one word per wave), so
@@ -86,34 +74,7 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
     // ---- loads: weights, activations, epilogue scales, all issued before the first wait ----
     const uint32_t lane16 = (uint32_t)lane * 16u;  // < 1024
     uint32_t wv[NT][WPW];
-    {
-        const int j0 = s0 / KSW;
-#pragma unroll
-        for (int jn = 0; jn < NT; ++jn) {
-            // wave-uniform base of the n-tile's words, plus a 32-bit per-lane byte offset (SGPR-base loads)
-            const int t = min((n0 >> 4) + jn, NTILES - 1);
-            const char *tb = (const char *)(w + (long long)t * J * 64);
-            if constexpr (WPW == 1 || RAGGED) {
-                // general addressing: a short last quad has lane stride wq < 4; words past J load any valid word
-                // (their activations are zero)
-#pragma unroll
-                for (int u = 0; u < WPW; ++u) {
-                    const int j = min(j0 + u, J - 1), jq = j & ~3;
-                    const int wq = min(4, J - jq);
-                    wv[jn][u] = *(const uint32_t *)(tb + jq * 256 + (j & 3) * 4 + lane16 / 4 * (uint32_t)wq);
-                }
-            } else if constexpr (WPW == 2) {
-                const uint2 v = *(const uint2 *)(tb + (j0 >> 2) * 1024 + ((j0 >> 1) & 1) * 8 + lane16);
-                wv[jn][0] = v.x; wv[jn][1] = v.y;
-            } else {
-#pragma unroll
-                for (int g = 0; g < WPW / 4; ++g) {
-                    const uint4 v = *(const uint4 *)(tb + ((j0 >> 2) + g) * 1024 + lane16);
-                    wv[jn][4 * g] = v.x; wv[jn][4 * g + 1] = v.y; wv[jn][4 * g + 2] = v.z; wv[jn][4 * g + 3] = v.w;
-                }
-            }
-        }
-    }
+    wsplit_load_w<NT, WPW, RAGGED>(w, n0, NTILES, J, s0 / KSW, lane16, wv);
     v4i af[P][RM][S];
     {
         const int kl = (lane >> 4) * 16;          // this lane's 16 bytes of each k-step
@@ -176,47 +137,10 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
 
     // ---- MFMAs: straight-line code over the wave's S k-steps ----
     v4i acc[P][RM][NT];
-#pragma unroll
-    for (int c = 0; c < P; ++c)
-#pragma unroll
-        for (int i = 0; i < RM; ++i)
-#pragma unroll
-            for (int jn = 0; jn < NT; ++jn) acc[c][i][jn] = (v4i){0, 0, 0, 0};
-#pragma unroll
-    for (int t = 0; t < S; ++t) {
-        const int u = t / KSW, h = t % KSW;
-#pragma unroll
-        for (int jn = 0; jn < NT; ++jn) {
-            const uint32_t w32 = wv[jn][u];
-            v4i bf;
-            if constexpr (WBITS == 1) {
-                if (h == 0) {
-                    bf[0] = b1_expand<0>(w32); bf[1] = b1_expand<1>(w32); bf[2] = b1_expand<2>(w32); bf[3] = b1_expand<3>(w32);
-                } else {
-                    bf[0] = b1_expand<4>(w32); bf[1] = b1_expand<5>(w32); bf[2] = b1_expand<6>(w32); bf[3] = b1_expand<7>(w32);
-                }
-            } else {
-                const uint32_t w4 = w32 >> 4;
-                bf[0] = t2_lo(w32); bf[1] = t2_hi(w32); bf[2] = t2_lo(w4); bf[3] = t2_hi(w4);
-            }
-#pragma unroll
-            for (int c = 0; c < P; ++c)
-#pragma unroll
-                for (int i = 0; i < RM; ++i)
-                    acc[c][i][jn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af[c][i][t], acc[c][i][jn], 0, 0, 0);
-        }
-    }
+    wsplit_mfma<WBITS, P, RM, NT, S, WPW>(wv, af, acc);
 
     // ---- exact reduction over the waves through LDS ----
-    {
-        int32_t *mine = red + wave * PART;
-#pragma unroll
-        for (int c = 0; c < P; ++c)
-#pragma unroll
-            for (int i = 0; i < RM; ++i)
-#pragma unroll
-                for (int jn = 0; jn < NT; ++jn) *(v4i *)(mine + ((c * RM + i) * NT + jn) * 256 + lane * 4) = acc[c][i][jn];
-    }
+    wsplit_share<P, RM, NT>(red + wave * PART, lane, acc);
     __syncthreads();
 
     // ---- epilogue: block b = wave + NW * u of the tile ----
@@ -227,15 +151,7 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
         if (b >= NB) break;  // wave-uniform
         const int i = b / NT, jn = b - (b / NT) * NT;
         int a[P][4];
-#pragma unroll
-        for (int c = 0; c < P; ++c) {
-            const int32_t *src = red + ((c * RM + i) * NT + jn) * 256 + lane * 4;
-            v4i sum = *(const v4i *)src;
-#pragma unroll
-            for (int v = 1; v < NW; ++v) sum += *(const v4i *)(src + v * PART);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) a[c][r] = sum[r];
-        }
+        wsplit_block_sum<P, RM, NT, NW>(red, i, jn, lane, a);
         const int mt = m0 + i * 16, m = mt + (lane & 15);
         const int nt = n0 + jn * 16, nb = nt + (lane >> 4) * 4;
         if (m >= M || nb >= N) continue;
@@ -255,17 +171,7 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
                 e.bias[r] = bias ? raw_to_f32(rb[u][r], b16, bias, (uint32_t)n) : kNoBias;
             }
             load_residual(p, m, nb, e.res);
-            if (plain && mt + 16 <= M && nt + 16 <= N) {
-                if (p.y_dtype == KEA_F16) {
-                    epilogue4_full<P, KEA_F16, false, true>(p, (uint16_t *)p.y + (long long)m * p.ldy, nb, a, e);
-                } else if (p.y_dtype == KEA_BF16) {
-                    epilogue4_full<P, KEA_BF16, false, true>(p, (uint16_t *)p.y + (long long)m * p.ldy, nb, a, e);
-                } else {
-                    epilogue4_full<P, KEA_F32, false, true>(p, (float *)p.y + (long long)m * p.ldy, nb, a, e);
-                }
-            } else {
-                epilogue4<P>(p, m, nb, a, e);
-            }
+            wsplit_epilogue<P>(p, plain, M, N, m, mt, nt, nb, a, e);
         }
     }
 }

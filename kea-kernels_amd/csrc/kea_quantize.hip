@@ -22,22 +22,15 @@
 #include "kea_epilogue.h"
 #include "kea_internal.h"
 #include "kea_merge.h"
+#include "kea_rowq.h"
 #include "kea_wave.h"
 #include "../../include/kea_encoder.h"
 
 namespace {
 
+using kea::quantize_code;
 using kea::wave_max;
 using kea::wave_sum;
-
-// rint(z / s) with z / s the IEEE quotient, without a division per element: q = z * inv (inv = 1 / s, correctly
-// rounded) is corrected once with the residual, r = fma(-q, s, z), q' = fma(r, inv, q), which is the correctly rounded
-// quotient (Markstein's correction step for division with a fused multiply-add). Where the residual would underflow,
-// |z / s| < 1 / 4 and both round to 0.
-__device__ __forceinline__ float round_quotient(float z, float s, float inv) {
-    const float q = z * inv;
-    return rintf(fmaf(fmaf(-q, s, z), inv, q));
-}
 
 __device__ __forceinline__ float load_x(const void *x, int dtype, long long i) {
     if (dtype == KEA_F16) return (float)(((const _Float16 *)x)[i]);
@@ -177,12 +170,7 @@ quantize_kernel(const void *x, int x_dtype, long long xb, long long xt, long lon
             const int k0 = 4 * (th + TPR * i);
             uint32_t packed = 0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float v = round_quotient(z[i][j], s, inv);
-                v = fminf(fmaxf(v, -127.0f), 127.0f);
-                packed |= (uint32_t)(uint8_t)(int8_t)(int)v << (8 * j);
-                z[i][j] = z[i][j] - v * s;
-            }
+            for (int j = 0; j < 4; ++j) packed |= quantize_code(z[i][j], s, inv) << (8 * j);
             if constexpr (VEC) {
                 if (k0 < K) *(uint32_t *)(row + k0) = packed;  // k0 + 3 < ldq: ldq >= K and ldq % 4 == 0
             } else {
@@ -218,12 +206,7 @@ __device__ __forceinline__ void quantize_parts(float (*z)[4], int K, int parts, 
             const int k0 = 4 * (th + TPR * i);
             uint32_t packed = 0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float v = round_quotient(z[i][j], s, inv);
-                v = fminf(fmaxf(v, -127.0f), 127.0f);
-                packed |= (uint32_t)(uint8_t)(int8_t)(int)v << (8 * j);
-                z[i][j] = z[i][j] - v * s;
-            }
+            for (int j = 0; j < 4; ++j) packed |= quantize_code(z[i][j], s, inv) << (8 * j);
             if (k0 < K) *(uint32_t *)(row + k0) = packed;
         }
         for (long long k = ((K + 3) & ~3) + th; k < ldq; k += TPR) row[k] = 0;

@@ -183,3 +183,40 @@ def test_plan_refuses_what_the_direct_call_refuses():
     assert not h and b"aligned" in L.kea_last_error()
     assert L.kea_lowbit_gemm_plan_launch(None, None) == -1
     L.kea_lowbit_gemm_plan_free(None)
+
+
+def test_rows_gemm_refuses_bad_arguments_before_any_launch():
+    """kea_lowbit_gemm_rows checks its mode, sizes, alignment and buffer overlaps on the host; m = 0 with valid
+    arguments returns 0. No device is touched (fake addresses)."""
+    L = _hip.lib()
+    P = ctypes.c_void_p
+
+    def call(rows, *, parts=1, n=1024, k=1024, y=0x200000, m=32, flags=0, config=0, wbits=1):
+        return L.kea_lowbit_gemm_rows(wbits, None if rows is None else ctypes.byref(rows), parts, P(0x1000), n, k,
+                                      P(0x2000), 0, None, 0, P(y), 0, n, None, 0, 1.0, m, flags, config, None)
+
+    def rows(mode=_hip.ROWS_PLAIN, x=0x100000, ldx=1024, **kw):
+        r = _hip.Rows(mode=mode, x=x, ldx=ldx)
+        for key, value in kw.items():
+            setattr(r, key, value)
+        return r
+
+    assert call(None) == -1 and b"rows is required" in L.kea_last_error()
+    assert call(rows(mode=7)) == -1 and b"unknown rows mode" in L.kea_last_error()
+    assert call(rows(), k=512) == -1 and b"k must be 1024" in L.kea_last_error()
+    assert call(rows(_hip.ROWS_NORM), k=4096) == -1 and b"k must be 1024" in L.kea_last_error()
+    assert call(rows(), config=3) == -1 and b"wave-split tile id" in L.kea_last_error()
+    assert call(rows(), config=14) == -1 and b"no row-quantizing kernel" in L.kea_last_error()  # 32-row tile
+    assert call(rows(), k=4096, parts=3) == -1 and b"no row-quantizing kernel" in L.kea_last_error()
+    assert call(rows(), y=0x100000 + 4096) == -1 and b"must not overlap the source rows" in L.kea_last_error()
+    assert call(rows(x=0x100008)) == -2 and b"aligned" in L.kea_last_error()
+    assert call(rows(ldx=1000)) == -1 and b"ldx" in L.kea_last_error()
+    assert call(rows(_hip.ROWS_NORM)) == -1 and b"norm0_w" in L.kea_last_error()
+    norm2 = dict(norm0_w=0x300000, norm0_b=0x301000, norm1_w=0x302000, norm1_b=0x303000, ld_out=1024)
+    assert call(rows(_hip.ROWS_NORM2, x_out=0x100000 + 64, **norm2)) == -1
+    assert b"x_out must not overlap" in L.kea_last_error()
+    assert call(rows(_hip.ROWS_MERGE, heads=4)) == -1 and b"heads * 128" in L.kea_last_error()
+    assert call(rows(_hip.ROWS_MERGE, heads=8, ws_bytes=1024)) == -4 and b"workspace too small" in L.kea_last_error()
+    assert call(rows(), flags=4, n=1023) == -1 and b"GLU" in L.kea_last_error()
+    assert call(rows(), m=0) == 0
+    assert call(rows(_hip.ROWS_NORM2, x_out=0x800000, **norm2), m=0, parts=3) == 0
