@@ -702,7 +702,7 @@ int kea_lowbit_gemm_rows(int wbits, const kea_rows *rows, int parts, const uint3
     p.x_out = rows->x_out; p.ld_out = rows->ld_out;
     p.heads = rows->heads;
 
-    const int lds = wt.nw * parts * wt.nt * 1024;
+    const int lds = kea::rows_lds_bytes(parts, wt, s);
     if (lds > 65536) {
         const hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) return kea::fail((int)e, std::string("LDS attribute refused: ") + hipGetErrorString(e));

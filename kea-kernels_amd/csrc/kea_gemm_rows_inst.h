@@ -3,23 +3,20 @@
 //
 // The wave-split GEMM (kea_gemm_wsplit_inst.h) with the activation quantizer in front of it in the same launch: a
 // workgroup reads the FP32 rows of its 16-row tile over the whole of K, optionally puts them through one or two
-// LayerNorms, quantizes them into P residual int8 parts in registers and runs the MFMAs, reduction and epilogue of
-// the wave-split kernel on them. The codes and scales are bitwise those of kea_quantize / kea_norm_quantize /
+// LayerNorms, quantizes them into P residual int8 parts and runs the MFMAs, reduction and epilogue of the wave-split
+// kernel on them. The codes and scales are bitwise those of kea_quantize / kea_norm_quantize /
 // kea_attention_merge_quantize on the same rows (f32 scales), so the output is bitwise that of the two-launch path.
 //
 // Every workgroup of a row tile quantizes the same rows again (the N / BN column tiles each read the FP32 rows):
 // this trades L2 reads for a launch, which pays where launches dominate (small M).
 //
-// Layout: wave w of NW holds the S k-steps [w S, (w + 1) S) of every row of the tile; lane l holds row l % 16 and
-// the 16 consecutive k at 64 t + 16 (l / 16) of step t, which is exactly the int8 operand layout of
-// v_mfma_i32_16x16x64_i8 that the codes are packed into. Row statistics are reduced over the 4 lanes of a row with
-// two lane exchanges and over the waves through LDS.
-//
-// LayerNorm sums (the only reductions that are not exact) follow the quantizer's fixed order, which for K = 1024
-// (4 waves x 4 k-steps here) maps onto this layout: the quantizer's thread th of wave w holds k = 256 w + 4 (th % 64)
-// + j, i.e. step t = (th % 64) / 16, lane group (th % 16) / 4 and 4-element chunk th % 4 of wave w here. Its xor
-// butterfly over th (offsets 1 and 2: chunks inside a lane; 4 and 8: lane groups, lanes l ^ 16 and l ^ 32; 16 and 32:
-// steps) and the wave totals in wave order are reproduced term by term.
+// Layout: wave w of NW holds the k range [w S 64, (w + 1) S 64) of the tile's 16 rows. Rows are read coalesced, as
+// the quantizer reads them: lane l holds the 4 consecutive floats at k = w S 64 + 256 c + 4 l (c < S / 4) of every
+// row, so one load instruction covers 1 KiB of one row. For K = 1024 (4 waves of 4 k-steps) lane l of wave w holds
+// exactly the elements of the quantizer's thread 64 w + l, so the LayerNorm sums are the quantizer's own: each lane's
+// (((0 + a) + b) + c) + d, kea::wave_sum over the wave, then the wave totals in wave order. Row maxima are exact in
+// any order. The int8 codes go to the MFMA operand layout (lane l: row l % 16, the 16 k at 64 t + 16 (l / 16) of step
+// t) through a per-wave LDS staging area.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -30,6 +27,7 @@
 #include "kea_gemm_wsplit_body.h"
 #include "kea_merge.h"
 #include "kea_rowq.h"
+#include "kea_wave.h"
 
 #ifndef KEA_ROWS_P
 #error "define KEA_ROWS_P (1, 2 or 3) before including kea_gemm_rows_inst.h"
@@ -39,82 +37,78 @@ namespace {
 
 using namespace kea;
 
-// The total over this wave's quarter of the row (K = 1024, S = 4) in the quantizer's butterfly order: per lane
-// chunk sums (((0 + a) + b) + c) + d, the chunk pairs, the lane groups (l ^ 16, then l ^ 32), then the step pairs.
-// SQUARE: the terms are the squares of the values.
-template <bool SQUARE>
-__device__ __forceinline__ float quarter_sum(const float (&z)[4][16]) {
-    float u[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        float c4[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            float s = 0.f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) s = s + (SQUARE ? z[t][4 * c + j] * z[t][4 * c + j] : z[t][4 * c + j]);
-            c4[c] = s;
-        }
-        u[t] = (c4[0] + c4[1]) + (c4[2] + c4[3]);
-        u[t] = u[t] + __shfl_xor(u[t], 16);
-        u[t] = u[t] + __shfl_xor(u[t], 32);
-    }
-    return (u[0] + u[1]) + (u[2] + u[3]);
-}
-
-// The row total of per-wave values: slot[wave][row] written by lane group 0, one barrier, then the NW values of the
-// lane's row summed (or maxed) in wave order. Each reduction of a launch uses its own slot (no barrier before reuse).
+// The row totals (sums, or maxima with MAX) of the 16 rows from this lane's values v[r]: kea::wave_sum / wave_max
+// over the wave, then the NW wave totals of each row in wave order through LDS (slot[wave][row]; each reduction of a
+// launch uses its own slot, so no barrier precedes a slot's first write). out[r] is the same in every lane.
 template <int NW, bool MAX>
-__device__ __forceinline__ float across_waves(float v, float (*slot)[16], int lane, int wave) {
-    if ((lane >> 4) == 0) slot[wave][lane & 15] = v;
-    __syncthreads();
-    float r = slot[0][lane & 15];
+__device__ __forceinline__ void row_totals(const float (&v)[16], float (*slot)[16], int lane, int wave,
+                                           float (&out)[16]) {
+    float mine = 0.f;
 #pragma unroll
-    for (int w = 1; w < NW; ++w) r = MAX ? fmaxf(r, slot[w][lane & 15]) : r + slot[w][lane & 15];
-    return r;
+    for (int r = 0; r < 16; ++r) {
+        const float t = MAX ? wave_max(v[r]) : wave_sum(v[r]);
+        mine = lane == r ? t : mine;
+    }
+    if (lane < 16) slot[wave][lane] = mine;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        float a = slot[0][r];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) a = MAX ? fmaxf(a, slot[w][r]) : a + slot[w][r];
+        out[r] = a;
+    }
 }
 
-// LayerNorm of the lane's values (K = 1024: S = 4, NW = 4) with the quantizer's arithmetic: mean, then the sum of
-// squared deviations, inv = 1 / sqrt(var + eps), z = z * inv * w + b. lw / lb: the weights and biases at the lane's k.
+// LayerNorm of the 16 rows (K = 1024: one 4-float chunk per lane and row) with the quantizer's arithmetic: mean,
+// then the sum of squared deviations, inv = 1 / sqrt(var + eps), z = z * inv * w + b. lw / lb: the weights and
+// biases at the lane's 4 k.
 template <int NW>
-__device__ __forceinline__ void layer_norm_rows(float (&z)[4][16], const float (&lw)[4][16], const float (&lb)[4][16],
+__device__ __forceinline__ void layer_norm_rows(float (&z)[16][1][4], const float (&lw)[1][4], const float (&lb)[1][4],
                                                 float eps, int K, float (*slot0)[16], float (*slot1)[16], int lane,
                                                 int wave) {
-    const float mean = across_waves<NW, false>(quarter_sum<false>(z), slot0, lane, wave) / (float)K;
+    float part[16], tot[16];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int r = 0; r < 16; ++r) part[r] = (((0.f + z[r][0][0]) + z[r][0][1]) + z[r][0][2]) + z[r][0][3];
+    row_totals<NW, false>(part, slot0, lane, wave, tot);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) z[t][e] = z[t][e] - mean;
-    const float var = across_waves<NW, false>(quarter_sum<true>(z), slot1, lane, wave) / (float)K;
-    const float inv = 1.0f / sqrtf(var + eps);
+    for (int r = 0; r < 16; ++r) {
+        const float mean = tot[r] / (float)K;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+        for (int j = 0; j < 4; ++j) z[r][0][j] = z[r][0][j] - mean;
+        part[r] = (((0.f + z[r][0][0] * z[r][0][0]) + z[r][0][1] * z[r][0][1]) + z[r][0][2] * z[r][0][2]) +
+                  z[r][0][3] * z[r][0][3];
+    }
+    row_totals<NW, false>(part, slot1, lane, wave, tot);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) z[t][e] = z[t][e] * inv * lw[t][e] + lb[t][e];
+    for (int r = 0; r < 16; ++r) {
+        const float inv = 1.0f / sqrtf(tot[r] / (float)K + eps);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) z[r][0][j] = z[r][0][j] * inv * lw[0][j] + lb[0][j];
+    }
 }
 
-// 16 consecutive floats at src (16-byte aligned) into v.
-__device__ __forceinline__ void load16(const float *src, float (&v)[16]) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const float4 f = *(const float4 *)(src + 4 * q);
-        v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
-    }
+__device__ __forceinline__ void set4(float (&d)[4], const float4 v) {
+    d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
 }
 
 // The kernel: grid (ceil(N / BN), ceil(M / 16)), NW wave64s, K = NW * S * 64 exactly (the host checks). x: the FP32
 // rows [M][ldx], or for KEA_ROWS_MERGE the key-split attention workspace of M rows and p.heads heads (K = heads *
 // 128). meta: bit 1 wscale is f16, bit 2 bias is f16. The operands of the first loads are preloaded scalar arguments.
+// Dynamic LDS: the partial tiles [NW][P][NT][64][4] int32, then the code staging [NW][16][RS] bytes.
 template <int MODE, int WBITS, int P, int NT, int NW, int S>
 __global__ void __launch_bounds__(NW * 64) rows_kernel(const float *x, const uint32_t *w, const void *ws, int M,
                                                        int N, int K, int ldx, int meta, Params p) {
     static_assert(WBITS == 2 || S % 2 == 0, "1-bit waves take whole words (two k-steps each)");
+    static_assert(S % 4 == 0, "a wave's k range is whole 256-float chunks per row");
     constexpr bool NORM = MODE == KEA_ROWS_NORM || MODE == KEA_ROWS_NORM2;
     static_assert(!NORM || (NW == 4 && S == 4), "LayerNorm rows follow the quantizer's order for K = 1024");
     constexpr int KSW = WBITS == 1 ? 2 : 1, WPW = S / KSW;
+    constexpr int C = S / 4;                       // 4-float chunks per lane and row
+    constexpr int RS = S * 64 + 16;                // staging bytes per row (16-byte pad: conflict-free reads)
     constexpr int BN = NT * 16, UB = (NT + NW - 1) / NW, PART = P * NT * 256;
-    extern __shared__ __attribute__((aligned(16))) int32_t red[];  // [NW][P][NT][64 lanes][4]
-    __shared__ float stat[4 + P][NW][16];                           // per-wave row statistics, one slot each
+    extern __shared__ __attribute__((aligned(16))) int32_t red[];
+    __shared__ float stat[4 + P][NW][16];          // per-wave row statistics, one slot per reduction
 
     const void *const bias = p.bias;
     const int J = WBITS == 1 ? (K + 127) >> 7 : (K + 63) >> 6, NTILES = (N + 15) >> 4;
@@ -122,41 +116,41 @@ __global__ void __launch_bounds__(NW * 64) rows_kernel(const float *x, const uin
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n0 = blockIdx.x * BN, m0 = blockIdx.y * 16;
     const int s0 = wave * S;
-    const int row = min(m0 + (lane & 15), M - 1);  // rows past M repeat row M - 1 and are never stored
-    const int kl = s0 * 64 + (lane >> 4) * 16;     // the lane's first k; step t adds 64 t
+    const int kq = s0 * 64 + 4 * lane;             // the lane's first k; chunk c adds 256 c
 
     // ---- loads: weights, FP32 rows (and LayerNorm parameters), epilogue scales ----
     uint32_t wv[NT][WPW];
     wsplit_load_w<NT, WPW, false>(w, n0, NTILES, J, s0 / KSW, (uint32_t)lane * 16u, wv);
-    float z[S][16];
+    float z[16][C][4];
     if constexpr (MODE == KEA_ROWS_MERGE) {
         const int heads = p.heads;
         const SplitWs sw = split_ws((void *)x, M, heads);
         const long long hd = (long long)heads * 128;
 #pragma unroll
-        for (int t = 0; t < S; ++t) {
-            const int k = kl + 64 * t, h = k >> 7;  // 16 consecutive k lie in one head
-            const float2 ml0 = *(const float2 *)(sw.ml + ((long long)row * heads + h) * 2);
-            const float2 ml1 = *(const float2 *)(sw.ml + ((long long)(M + row) * heads + h) * 2);
+        for (int r = 0; r < 16; ++r) {
+            const long long row = min(m0 + r, M - 1);  // rows past M repeat row M - 1 and are never stored
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float4 o0 = *(const float4 *)(sw.o + (long long)row * hd + k + 4 * q);
-                const float4 o1 = *(const float4 *)(sw.o + (long long)(M + row) * hd + k + 4 * q);
-                merge_halves(o0, o1, ml0, ml1, &z[t][4 * q]);
+            for (int c = 0; c < C; ++c) {
+                const int k = kq + 256 * c, h = k >> 7;
+                const float4 o0 = *(const float4 *)(sw.o + row * hd + k);
+                const float4 o1 = *(const float4 *)(sw.o + (M + row) * hd + k);
+                const float2 ml0 = *(const float2 *)(sw.ml + (row * heads + h) * 2);
+                const float2 ml1 = *(const float2 *)(sw.ml + ((M + row) * heads + h) * 2);
+                merge_halves(o0, o1, ml0, ml1, z[r][c]);
             }
         }
     } else {
-        const float *src = x + (long long)row * ldx + kl;
 #pragma unroll
-        for (int t = 0; t < S; ++t) load16(src + 64 * t, z[t]);
-    }
-    float lw[NORM ? S : 1][16], lb[NORM ? S : 1][16];
-    if constexpr (NORM) {
+        for (int r = 0; r < 16; ++r) {
+            const float *src = x + (long long)min(m0 + r, M - 1) * ldx + kq;
 #pragma unroll
-        for (int t = 0; t < S; ++t) {
-            load16(p.nw0 + kl + 64 * t, lw[t]);
-            load16(p.nb0 + kl + 64 * t, lb[t]);
+            for (int c = 0; c < C; ++c) set4(z[r][c], *(const float4 *)(src + 256 * c));
         }
+    }
+    float lw[NORM ? C : 1][4], lb[NORM ? C : 1][4];
+    if constexpr (NORM) {
+        set4(lw[0], *(const float4 *)(p.nw0 + kq));
+        set4(lb[0], *(const float4 *)(p.nb0 + kq));
     }
     uint32_t ra[UB][4], rb[UB][4];
 #pragma unroll
@@ -177,46 +171,53 @@ __global__ void __launch_bounds__(NW * 64) rows_kernel(const float *x, const uin
         layer_norm_rows<NW>(z, lw, lb, p.eps0, K, stat[0], stat[1], lane, wave);
         if constexpr (MODE == KEA_ROWS_NORM2) {
             // LayerNorm0(x) is stored once per row, by the workgroups of the first column tile
-            if (blockIdx.x == 0 && m0 + (lane & 15) < M) {
-                float *dst = p.x_out + (long long)row * p.ld_out + kl;
+            if (blockIdx.x == 0) {
 #pragma unroll
-                for (int t = 0; t < S; ++t)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        *(float4 *)(dst + 64 * t + 4 * q) =
-                            make_float4(z[t][4 * q], z[t][4 * q + 1], z[t][4 * q + 2], z[t][4 * q + 3]);
+                for (int r = 0; r < 16; ++r)
+                    if (m0 + r < M)
+                        *(float4 *)(p.x_out + (long long)(m0 + r) * p.ld_out + kq) =
+                            make_float4(z[r][0][0], z[r][0][1], z[r][0][2], z[r][0][3]);
             }
-#pragma unroll
-            for (int t = 0; t < S; ++t) {
-                load16(p.nw1 + kl + 64 * t, lw[t]);
-                load16(p.nb1 + kl + 64 * t, lb[t]);
-            }
+            set4(lw[0], *(const float4 *)(p.nw1 + kq));
+            set4(lb[0], *(const float4 *)(p.nb1 + kq));
             layer_norm_rows<NW>(z, lw, lb, p.eps1, K, stat[2], stat[3], lane, wave);
         }
     }
+    // codes: packed in the load layout, staged through this wave's LDS rows, read back in the MFMA operand layout
+    char *stage = (char *)(red + NW * PART) + wave * 16 * RS;
     v4i af[P][1][S];
     float sc[P];
 #pragma unroll
     for (int c = 0; c < P; ++c) {
-        float amax = 0.f;
+        float amax[16];
 #pragma unroll
-        for (int t = 0; t < S; ++t)
+        for (int r = 0; r < 16; ++r) {
+            float a = 0.f;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(z[t][e]));
-        amax = fmaxf(amax, __shfl_xor(amax, 16));
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
-        amax = across_waves<NW, true>(amax, stat[4 + c], lane, wave);
-        const float s = fmaxf(amax / 127.0f, 1.0e-30f), inv = 1.0f / s;
-        sc[c] = s;
+            for (int cc = 0; cc < C; ++cc)
 #pragma unroll
-        for (int t = 0; t < S; ++t)
+                for (int j = 0; j < 4; ++j) a = fmaxf(a, fabsf(z[r][cc][j]));
+            amax[r] = a;
+        }
+        row_totals<NW, true>(amax, stat[4 + c], lane, wave, amax);
+        float mine = 0.f;
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
+        for (int r = 0; r < 16; ++r) {
+            const float s = fmaxf(amax[r] / 127.0f, 1.0e-30f), inv = 1.0f / s;
+            mine = (lane & 15) == r ? s : mine;
+#pragma unroll
+            for (int cc = 0; cc < C; ++cc) {
                 uint32_t packed = 0;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) packed |= quantize_code(z[t][4 * d + j], s, inv) << (8 * j);
-                af[c][0][t][d] = (int)packed;
+                for (int j = 0; j < 4; ++j) packed |= quantize_code(z[r][cc][j], s, inv) << (8 * j);
+                *(uint32_t *)(stage + r * RS + 256 * cc + 4 * lane) = packed;
             }
+        }
+        sc[c] = mine;
+        __builtin_amdgcn_wave_barrier();  // the wave's staging writes precede its reads (LDS runs a wave in order)
+#pragma unroll
+        for (int t = 0; t < S; ++t) af[c][0][t] = *(const v4i *)(stage + (lane & 15) * RS + 64 * t + 16 * (lane >> 4));
+        __builtin_amdgcn_wave_barrier();  // ... and the next part's writes follow these reads
     }
 
     // ---- MFMAs, exact reduction over the waves, epilogue ----
@@ -248,17 +249,18 @@ __global__ void __launch_bounds__(NW * 64) rows_kernel(const float *x, const uin
 }
 
 // Instances exist only where the registers fit: the FP32 rows (16 per k-step; twice that while the two attention
-// halves are merged), the LayerNorm parameters while they are live, the codes, weight words and accumulators, within
-// 256 per wave (NW = 4) or 224 (NW = 8, two waves per SIMD).
+// halves are merged), the codes, weight words and accumulators, within 256 per wave (NW = 4) or 224 (NW = 8, two
+// waves per SIMD).
 template <int MODE, int WBITS, int NT, int NW, int S>
 RowsFn pick_fit() {
     constexpr bool NORM = MODE == KEA_ROWS_NORM || MODE == KEA_ROWS_NORM2;
     constexpr int P = KEA_ROWS_P;
     constexpr int words = WBITS == 1 ? S / 2 : S;
-    constexpr int load_phase = S * 16 * (NORM ? 3 : MODE == KEA_ROWS_MERGE ? 2 : 1) + NT * words;
+    constexpr int load_phase = S * 16 * (MODE == KEA_ROWS_MERGE ? 2 : 1) + NT * words;
     constexpr int code_phase = S * 16 + P * S * 4 + NT * words + P * NT * 4;
     constexpr int regs = load_phase > code_phase ? load_phase : code_phase;
-    if constexpr ((!NORM || (NW == 4 && S == 4)) && regs <= (NW == 4 ? 256 : 224))
+    constexpr int lds = NW * P * NT * 1024 + NW * 16 * (S * 64 + 16);
+    if constexpr ((!NORM || (NW == 4 && S == 4)) && regs <= (NW == 4 ? 256 : 224) && lds <= 160 * 1024)
         return rows_kernel<MODE, WBITS, P, NT, NW, S>;
     else
         return nullptr;

@@ -22,9 +22,13 @@ the SiLU in front of W_pw2 fused into the quantizer (the reference's norm_quant 
 (relative-position scores, softmax, P.V) and GLU + depthwise convolution (BatchNorm folded into its weights) are the
 fused HIP kernels of include/kea_encoder.h (the reference's Triton relative_attention and glu_pad); the GLU kernel
 also applies the SiLU and quantizes for W_pw2 (kea_glu_dwconv_quantize). The four residual projections (W2 of both
-FFs, W_out, W_pw2) write exact int32 K-slices, and one row epilogue per block (kea_row_epilogue, the reference's
-row_fusions with _row_epilogue_exact) adds the residual, applies the output LayerNorm at the end of a layer and
-quantizes the next block's input through its LayerNorm. The subsampling convolutions are PyTorch on the GPU.
+FFs, W_out, W_pw2) add the residual in their GEMM epilogue, in place (the reference's row_fusions,
+kk/ternary/row_fusion.py:121-152); the quantizers run as row kernels between the GEMMs (kea_quantize,
+kea_norm_quantize, kea_attention_merge_quantize), 17 launches a layer. With rows=True every projection but W_pw2
+quantizes its own FP32 input rows inside the GEMM launch instead (kea_lowbit_gemm_rows): W1 through its LayerNorm (at
+a layer boundary also the previous layer's output LayerNorm, which it stores as the new residual stream), W2 from W1's
+output, W_qkv and W_pw1 through theirs, W_out from the key-split attention halves: 10 launches a layer, the same bits,
+but slower (see FastConformerEncoder). The subsampling convolutions are PyTorch on the GPU.
 With fused=False the same model runs with separate quantizers, the residual in the GEMM epilogue
 (kea_lowbit_gemm_residual) and PyTorch attention, GLU and convolution. The quantized linears have no bias
 (Q/K/V must be bias-free to fuse, kk/binary/provider.py:230-244).
@@ -35,6 +39,7 @@ FP32 matmuls on the dense weights (signs * alpha): the parity reference for the 
 """
 from __future__ import annotations
 
+import contextlib
 import math
 from dataclasses import dataclass
 
@@ -410,12 +415,21 @@ class FastConformerEncoder:
     """audio [B, S] -> encoder output [B, T', d]. parts = int8 activation parts of every quantized linear (1 = the
     Kea-B x1 mode); dense=True swaps the quantized linears for FP32 dense matmuls (the parity reference);
     fused=False runs attention and the GLU + depthwise convolution as PyTorch ops instead of the fused HIP kernels
-    (the dense twin always does)."""
+    (the dense twin always does). rows=True (fused only): the projections quantize their FP32 input rows inside the
+    GEMM launch (lowbit.gemm_rows) where M <= ROWS_MAX_M, 10 launches a layer instead of 17, the same bits. It is off
+    by default because it is slower on MI355X: every workgroup quantizes its whole 16-row tile on the vector ALU
+    (16 x K elements at about a dozen instructions each, 64 lanes a clock per CU: 1.3-5 us), which costs more than
+    the separate quantizer launch it replaces (about 2.5 us in a graph); measured 3.1 ms against 1.8 ms per clip at
+    batch 1."""
+
+    # Largest M (batch x frames) at which rows=True applies.
+    ROWS_MAX_M = 256
 
     def __init__(self, weights: dict, cfg: EncoderConfig = EncoderConfig(), device="cuda", *, parts: int = 1,
-                 dense: bool = False, fused: bool = True):
+                 dense: bool = False, fused: bool = True, rows: bool = False):
         self.cfg, self.parts, self.dense = cfg, parts, dense
         self.fused = fused and not dense
+        self.rows = rows and self.fused
         self._sub_out = None
         self.device = device = torch.device(device)
         if device.type == "cuda" and device.index is None:
@@ -576,6 +590,19 @@ class FastConformerEncoder:
             self._pos_cache[t] = hit
         return hit
 
+    @contextlib.contextmanager
+    def attention_workspaces(self, table: dict):
+        """Forward calls inside the block take their key-split attention workspaces from `table` ((batch, t) ->
+        workspace, filled on first use) instead of the encoder's shared table. EncoderGraph gives each graph its own,
+        so graphs replayed on different streams, and eager calls, never share one. Eager calls of one encoder that
+        overlap on different streams must each run inside their own table."""
+        saved = self._att_ws
+        self._att_ws = table
+        try:
+            yield
+        finally:
+            self._att_ws = saved
+
     def _attention_ws(self, b: int, t: int) -> Tensor | None:
         """The key-split attention workspace of this shape (None where the split does not apply), allocated on the
         first forward of the shape (the eager warm-up, before any graph capture)."""
@@ -618,37 +645,20 @@ class FastConformerEncoder:
         q, qs, _ = lowbit.quantize(z3, (z3.stride(0), z3.stride(1), z3.stride(2), t), b * t, k, self.parts, norm=norm)
         return q, qs
 
-    @staticmethod
-    def _split(m: int, k: int) -> int:
-        """K slices of a residual projection. Small batches cut the FFN down projections (K = 4096) in 4 so that
-        the GEMM fills the chip (measured on MI355X: batch 1, 125 frames, 0.2 ms per clip); at batch 8 the int32
-        slices cost more traffic than the split saves. Exact integer slices make every choice give the same bits."""
-        return 4 if k >= 4096 and m <= 256 else 1
-
     def _block(self, name: str, q: Tensor, qs: Tensor, r: Tensor, factor: float, *, norm=None, out_norm=None):
         """r <- out_norm(r + factor * linear(q)) in place; with `norm`, returns the next projection's (q, qs) = the
-        P-part quantization of norm(r). Split K: the GEMM writes exact int32 K-slices and one row epilogue launch
-        (kea_row_epilogue) finishes them, adds the residual, normalises and quantizes. Unsplit: the residual add
-        runs in the GEMM epilogue and the LayerNorm(s) + quantization in one row kernel (kea_norm_quantize /
-        kea_quantize). Both give the same bits."""
+        P-part quantization of norm(r). The residual add runs in the GEMM epilogue, the LayerNorm(s) + quantization
+        in one row kernel (kea_norm_quantize / kea_quantize)."""
         layer = self._layer(name)
         b, t, n = r.shape
-        m, k = b * t, layer.in_features
-        split = self._split(m, k)
-        r2 = r.view(m, n)
-        if split > 1:
-            slices = torch.empty(split, self.parts, m, n, device=self.device, dtype=torch.int32)
-            lowbit.gemm_slices(layer.WBITS, q, layer.words, n, k, slices, m=m)
-            return lowbit.row_epilogue(slices, qs, layer.scale, layer.bias, r2, residual=r2, factor=factor,
-                                       out_norm=out_norm, norm=norm,
-                                       quantize_parts=self.parts if norm is not None else 0)
-        lowbit.gemm(layer.WBITS, q, qs, layer.words, n, k, layer.scale, layer.bias, r2, None, residual=r2,
-                    residual_factor=factor)
-        if out_norm is not None and norm is not None:
-            return norm_quantize(r, out_norm, norm, self.parts, out=r)[1:]
+        r2 = r.view(b * t, n)
+        lowbit.gemm(layer.WBITS, q, qs, layer.words, n, layer.in_features, layer.scale, layer.bias, r2, None,
+                    residual=r2, residual_factor=factor)
         if out_norm is not None:
-            r.copy_(F.layer_norm(r, out_norm.normalized_shape, out_norm.weight, out_norm.bias, out_norm.eps))
-            return None
+            # the output LayerNorm in the library's summation order; after the last layer (no next LayerNorm) the
+            # quantization that comes with it is not used
+            _, q2, qs2 = norm_quantize(r, out_norm, norm or out_norm, self.parts, out=r)
+            return (q2, qs2) if norm is not None else None
         return self._quantize(r, norm=norm) if norm is not None else None
 
     def _layer_rows(self, i: int, x: Tensor, pos: Tensor, xq=None):
@@ -673,6 +683,70 @@ class FastConformerEncoder:
         xq = self._block(pre + "feed_forward2.linear2", *self._quantize(y), x, 0.5, norm=following,
                          out_norm=fp["norm_out"])
         return x, xq
+
+    def _rows_gemm(self, name: str, x: Tensor, m: int, *, y: Tensor | None = None, norm=None, next_norm=None,
+                   x_out: Tensor | None = None, merge: tuple | None = None, silu: bool = False, glu: bool = False,
+                   residual_factor: float | None = None) -> Tensor:
+        """The quantized linear `name` on FP32 rows x ([m, K] or [B, T, K]; with merge = (B, T), the key-split
+        attention workspace of relpos_attention(..., merged=False)), quantized inside the GEMM launch
+        (lowbit.gemm_rows) through norm (and next_norm, storing x_out = norm(x)) where the library has that kernel,
+        else by the separate quantizer first (the same bits). residual_factor: y += factor * linear(x) in place (y
+        is the residual stream [m, N]); else y is allocated."""
+        layer = self._layer(name)
+        n, k = layer.out_features, layer.in_features
+        if y is None:
+            y = torch.empty(m, n // 2 if glu else n, device=self.device, dtype=torch.float32)
+        residual = None if residual_factor is None else y
+        mode = (_hip.ROWS_MERGE if merge is not None else _hip.ROWS_NORM2 if next_norm is not None
+                else _hip.ROWS_NORM if norm is not None else _hip.ROWS_PLAIN)
+        rows = x if merge is not None else x.reshape(m, k)
+        if lowbit.rows_supported(layer.WBITS, mode, self.parts, n, k):
+            lowbit.gemm_rows(layer.WBITS, rows, layer.words, n, k, layer.scale, layer.bias, y, m=m, parts=self.parts,
+                             norm=norm, next_norm=next_norm, x_out=None if x_out is None else x_out.view(m, k),
+                             merge_heads=self.cfg.heads if merge is not None else 0, residual=residual,
+                             residual_factor=1.0 if residual_factor is None else residual_factor, silu=silu, glu=glu)
+            return y
+        if merge is not None:
+            q, qs = attention_merge_quantize(x, merge[0], merge[1], self.cfg.heads, self.parts)
+        elif next_norm is not None:
+            _, q, qs = norm_quantize(rows.view(1, m, k), norm, next_norm, self.parts, out=x_out.view(1, m, k))
+        else:
+            q, qs = self._quantize(rows, norm=norm)
+        lowbit.gemm(layer.WBITS, q, qs, layer.words, n, k, layer.scale, layer.bias, y, None, m=m, silu=silu, glu=glu,
+                    residual=residual, residual_factor=1.0 if residual_factor is None else residual_factor)
+        return y
+
+    def _layer_quantizing_rows(self, i: int, r: Tensor, pos: Tensor) -> Tensor:
+        """Layer i with every projection but W_pw2 quantizing its own input rows in the GEMM launch: 10 launches
+        (W1, W2, W_qkv, attention, W_out, W_pw1, GLU-convolution quantizer, W_pw2, W1, W2). r: the layer's input
+        before the previous layer's output LayerNorm (the subsampled features for layer 0). Returns this layer's
+        residual stream before its own output LayerNorm, which the next layer's W1 applies and stores."""
+        fp = self.layers[i]
+        pre = f"encoder.layers.{i}."
+        b, t, d = r.shape
+        m = b * t
+        if i == 0:
+            x = r
+            y = self._rows_gemm(pre + "feed_forward1.linear1", x, m, norm=fp["norm_feed_forward1"], silu=True)
+        else:
+            x = torch.empty_like(r)
+            y = self._rows_gemm(pre + "feed_forward1.linear1", r, m, norm=self.layers[i - 1]["norm_out"],
+                                next_norm=fp["norm_feed_forward1"], x_out=x, silu=True)
+        x2 = x.view(m, d)
+        self._rows_gemm(pre + "feed_forward1.linear2", y, m, y=x2, residual_factor=0.5)
+        qkv = self._rows_gemm(pre + "self_attn.qkv", x, m, norm=fp["norm_self_att"]).view(b, t, -1)
+        ws = self._attention_ws(b, t) if d // self.cfg.heads == 128 else None
+        if ws is not None:
+            relpos_attention(qkv, pos, fp["u"], fp["v"], self.cfg.heads, workspace=ws, merged=False)
+            self._rows_gemm(pre + "self_attn.linear_out", ws, m, y=x2, merge=(b, t), residual_factor=1.0)
+        else:
+            self._rows_gemm(pre + "self_attn.linear_out", self.attention(qkv, pos, fp["u"], fp["v"]), m, y=x2,
+                            residual_factor=1.0)
+        u = self._rows_gemm(pre + "conv.pointwise_conv1", x, m, norm=fp["norm_conv"], glu=True).view(b, t, -1)
+        self._block(pre + "conv.pointwise_conv2", *dwconv_quantize(u, fp["dw_w"], fp["dw_b"], self.parts), x, 1.0)
+        y = self._rows_gemm(pre + "feed_forward2.linear1", x, m, norm=fp["norm_feed_forward2"], silu=True)
+        self._rows_gemm(pre + "feed_forward2.linear2", y, m, y=x2, residual_factor=0.5)
+        return x
 
     def layer(self, i: int, x: Tensor, pos: Tensor, xq=None) -> Tensor | tuple:
         """One layer. Fused (quantized, fused=True): returns (x, xq) with x updated in place and xq = (q, qs) the
@@ -700,6 +774,11 @@ class FastConformerEncoder:
         if self.cfg.xscaling and not self.fused:  # the fused subsampling applies it in its output linear
             x = x * math.sqrt(self.cfg.d_model)
         pos = self.positions(x.shape[1])
+        if self.rows and x.shape[0] * x.shape[1] <= self.ROWS_MAX_M:
+            for i in range(self.cfg.layers):
+                x = self._layer_quantizing_rows(i, x, pos[i])
+            out_norm = self.layers[-1]["norm_out"]  # its quantization is not used
+            return norm_quantize(x, out_norm, out_norm, 1, out=x)[0]
         xq = None
         for i in range(self.cfg.layers):
             out = self.layer(i, x, pos[i], xq)
@@ -713,15 +792,18 @@ class FastConformerEncoder:
 
 class EncoderGraph:
     """One HIP graph of preprocessing + encoder for a fixed (batch, samples); __call__ copies the audio into the
-    graph's input buffer, replays and returns the graph's output buffer (overwritten by the next call)."""
+    graph's input buffer, replays and returns the graph's output buffer (overwritten by the next call). The graph owns
+    its input, its key-split attention workspace (FastConformerEncoder.attention_workspaces) and its output."""
 
     def __init__(self, encoder: FastConformerEncoder, batch: int, samples: int, *, warmup: int = 2):
         self.encoder = encoder
         dev = encoder.device
         self.audio = torch.zeros(batch, samples, device=dev)
         self.stream = torch.cuda.Stream(dev)
-        with torch.inference_mode():
+        self.workspaces: dict = {}
+        with torch.inference_mode(), encoder.attention_workspaces(self.workspaces):
             encoder.positions(encoded_length(frames_for(encoder.cfg, samples)))
+            self.stream.wait_stream(torch.cuda.current_stream(dev))
             with torch.cuda.stream(self.stream):
                 for _ in range(warmup):
                     encoder(self.audio)
@@ -748,3 +830,36 @@ class EncoderGraph:
             self.graph.replay()
         caller.wait_stream(self.stream)
         return self.out
+
+
+class EncoderGraphCache:
+    """Up to max_graphs HIP graphs of one encoder, one per (audio shape, dtype, device, caller stream): the
+    reference's bounded encoder graph cache (kk/ternary/graphs.py:11-65). The first call of a key warms up and captures
+    an EncoderGraph (its own input, attention workspace and output); later calls copy the audio in and replay it.
+    Keys past the limit, CPU audio, calls with grad enabled and calls made while the current stream is capturing run
+    the encoder eagerly. Every call returns a tensor the caller owns (a copy of the graph's output)."""
+
+    def __init__(self, encoder: FastConformerEncoder, max_graphs: int = 4, *, warmup: int = 2):
+        if max_graphs < 1:
+            raise ValueError("max_graphs must be positive")
+        self.encoder, self.max_graphs, self.warmup = encoder, max_graphs, warmup
+        self.entries: dict = {}
+
+    def __call__(self, audio: Tensor) -> Tensor:
+        if (not audio.is_cuda or audio.dim() != 2 or torch.is_grad_enabled()
+                or torch.cuda.is_current_stream_capturing()):
+            return self.encoder(audio)
+        stream = torch.cuda.current_stream(audio.device)
+        key = (tuple(audio.shape), audio.dtype, audio.device, stream.cuda_stream)
+        graph = self.entries.get(key)
+        if graph is None:
+            if len(self.entries) >= self.max_graphs:
+                return self.encoder(audio)
+            graph = self.entries[key] = EncoderGraph(self.encoder, audio.shape[0], audio.shape[1], warmup=self.warmup)
+        return graph(audio).clone()
+
+    def clear(self) -> None:
+        """Releases the graphs after the work queued on their devices has finished."""
+        for device in {graph.audio.device for graph in self.entries.values()}:
+            torch.cuda.synchronize(device)
+        self.entries.clear()

@@ -376,3 +376,13 @@ def gemm_rows(wbits: int, x: Tensor, words: Tensor, n: int, k: int, wscale: Tens
         float(residual_factor), m, int(silu) | (2 * int(order)) | (4 * int(glu)), int(config),
         _hip.stream_handle(device))
     _hip.check(rc, "kea_lowbit_gemm_rows")
+
+
+@functools.lru_cache(maxsize=256)
+def rows_supported(wbits: int, mode: int, parts: int, n: int, k: int) -> bool:
+    """Whether kea_lowbit_gemm_rows has a kernel for this weight width, KEA_ROWS_* mode, part count and shape (asked
+    of the library with m = 0, which checks everything but the buffers and launches nothing)."""
+    r = _hip.Rows(mode=mode, heads=k // 128)
+    rc = _hip.lib().kea_lowbit_gemm_rows(wbits, ctypes.byref(r), parts, 16, n, k, 16, _hip.F32, None, 0, 16,
+                                         _hip.F32, n, None, 0, 1.0, 0, 0, 0, None)
+    return rc == 0

@@ -268,6 +268,52 @@ def test_fused_encoder_matches_unfused():
     assert rel < 5e-6, rel
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("parts", [1, 3])
+@pytest.mark.parametrize("batch,samples", [(1, 160000), (2, 160000), (3, 48000)])
+@torch.inference_mode()
+def test_row_quantizing_layers_equal_separate_quantizers(parts, batch, samples):
+    """The encoder whose projections quantize their own rows (10 launches a layer; W_out merges the key-split
+    attention halves itself at batch 1-2, batch 3 runs unsplit attention) is bitwise the encoder with the quantizers
+    as separate row kernels; at three parts W2 (K = 4096) falls back to the separate quantizer."""
+    cfg = E.EncoderConfig(layers=3)
+    w = E.synthetic_weights(cfg, seed=31)
+    audio = torch.randn(batch, samples, generator=torch.Generator().manual_seed(32 + batch)).cuda()
+    rows = E.FastConformerEncoder(w, cfg, "cuda", parts=parts, rows=True)
+    assert batch * E.encoded_length(E.frames_for(cfg, samples)) <= rows.ROWS_MAX_M
+    got = rows(audio)
+    want = E.FastConformerEncoder(w, cfg, "cuda", parts=parts, rows=False)(audio)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+
+
+@pytest.mark.gpu
+@torch.inference_mode()
+def test_graph_cache_bounds_shapes_and_returns_owned_outputs():
+    """At most max_graphs graphs (one per shape and stream), bitwise the eager forward on every replay; a shape past
+    the limit runs eagerly; a returned tensor is the caller's (changing it changes no later result); every graph
+    has its own key-split attention workspace, not the encoder's shared one."""
+    cfg = E.EncoderConfig(layers=2)
+    enc = E.FastConformerEncoder(E.synthetic_weights(cfg, seed=41), cfg, "cuda", parts=1)
+    g = torch.Generator().manual_seed(42)
+    clips = {n: torch.randn(1, n, generator=g).cuda() for n in (32000, 48000, 64000)}
+    eager = {n: enc(a).clone() for n, a in clips.items()}
+    cache = E.EncoderGraphCache(enc, max_graphs=2)
+    for _ in range(2):
+        for n, a in clips.items():
+            got = cache(a)
+            torch.cuda.synchronize()
+            assert torch.equal(got, eager[n]), n
+    assert len(cache.entries) == 2
+    cache(clips[32000]).zero_()
+    assert torch.equal(cache(clips[32000]), eager[32000])
+    shared = {w.data_ptr() for w in enc._att_ws.values() if w is not None}
+    own = [w for graph in cache.entries.values() for w in graph.workspaces.values() if w is not None]
+    assert own and all(w.data_ptr() not in shared for w in own)
+    cache.clear()
+    assert not cache.entries
+
+
 def _layer_norm(k: int, g: torch.Generator) -> torch.nn.LayerNorm:
     n = torch.nn.LayerNorm(k)
     with torch.no_grad():
@@ -457,3 +503,14 @@ def test_fused_launchers_check_parameters_before_any_call():
     ln_k, ln_short = torch.nn.LayerNorm(d), torch.nn.LayerNorm(d - 1)
     with pytest.raises(ValueError, match="norm1.weight"):
         E.norm_quantize(torch.zeros(1, t, d), ln_k, ln_short, 1)
+
+
+def test_graph_cache_limits_and_eager_paths_on_cpu():
+    with pytest.raises(ValueError, match="max_graphs"):
+        E.EncoderGraphCache(None, max_graphs=0)
+    cfg = E.EncoderConfig(layers=1)
+    enc = E.FastConformerEncoder(E.synthetic_weights(cfg, seed=43), cfg, "cpu", dense=True)
+    audio = torch.randn(1, 16000, generator=torch.Generator().manual_seed(44))
+    cache = E.EncoderGraphCache(enc)
+    assert torch.equal(cache(audio), enc(audio))  # CPU audio: eager, nothing captured
+    assert not cache.entries
