@@ -465,21 +465,29 @@ KernelFn pick_fit(bool sliced) {
     else return nullptr;
 }
 
+// The instance of kTiles[I] (its geometry read from the table itself, so ids and shapes cannot drift apart).
+template <int WBITS, int P, int I>
+KernelFn pick_index(bool sliced) {
+    constexpr Tile t = kTiles[I];
+    return pick_fit<WBITS, P, t.rm, t.rn, t.wm, t.wn>(sliced);
+}
+
 template <int WBITS, int P>
 KernelFn pick_tile(int id, bool sliced) {
+    static_assert(kNumTiles == 12, "one case per tile id");
     switch (id) {
-        case 1: return pick_fit<WBITS, P, 1, 1, 1, 4>(sliced);
-        case 2: return pick_fit<WBITS, P, 2, 1, 1, 4>(sliced);
-        case 3: return pick_fit<WBITS, P, 1, 2, 2, 2>(sliced);
-        case 4: return pick_fit<WBITS, P, 1, 1, 2, 2>(sliced);
-        case 5: return pick_fit<WBITS, P, 4, 1, 1, 4>(sliced);
-        case 6: return pick_fit<WBITS, P, 8, 1, 1, 4>(sliced);
-        case 7: return pick_fit<WBITS, P, 2, 4, 2, 2>(sliced);
-        case 8: return pick_fit<WBITS, P, 4, 2, 1, 4>(sliced);
-        case 9: return pick_fit<WBITS, P, 2, 2, 1, 4>(sliced);
-        case 10: return pick_fit<WBITS, P, 2, 4, 2, 4>(sliced);
-        case 11: return pick_fit<WBITS, P, 4, 2, 2, 4>(sliced);
-        case 12: return pick_fit<WBITS, P, 1, 2, 2, 4>(sliced);
+        case 1: return pick_index<WBITS, P, 0>(sliced);
+        case 2: return pick_index<WBITS, P, 1>(sliced);
+        case 3: return pick_index<WBITS, P, 2>(sliced);
+        case 4: return pick_index<WBITS, P, 3>(sliced);
+        case 5: return pick_index<WBITS, P, 4>(sliced);
+        case 6: return pick_index<WBITS, P, 5>(sliced);
+        case 7: return pick_index<WBITS, P, 6>(sliced);
+        case 8: return pick_index<WBITS, P, 7>(sliced);
+        case 9: return pick_index<WBITS, P, 8>(sliced);
+        case 10: return pick_index<WBITS, P, 9>(sliced);
+        case 11: return pick_index<WBITS, P, 10>(sliced);
+        case 12: return pick_index<WBITS, P, 11>(sliced);
         default: return nullptr;
     }
 }
