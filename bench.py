@@ -540,9 +540,10 @@ def main(argv=None) -> int:
                     help="--encoder: skip the FP32 dense comparison (profiles then hold only the quantized encoder)")
     ap.add_argument("--suite", action="store_true",
                     help="only time BASELINE.json configs 2-4 and the reference's tuned shapes (one JSON line each)")
-    ap.add_argument("--case", default=None, metavar="BITS,P,M,N,K",
-                    help="only time one GEMM shape (fp16 scales and output, library-chosen configuration) for "
-                         "--steps launches; used for the rocprofv3 counter passes of the larger configs")
+    ap.add_argument("--case", default=None, metavar="BITS,P,M,N,K[,TILE]",
+                    help="only time one GEMM shape (fp16 scales and output; the library-chosen configuration, or "
+                         "tile id TILE unsplit) for --steps launches; used for the rocprofv3 counter passes of the "
+                         "larger configs")
     ap.add_argument("--sweep", default=None, metavar="PARTS",
                     help="only time every tile configuration at the chooser's shapes for these part counts "
                          "(e.g. 1,2,3; one JSON line per shape)")
@@ -556,11 +557,14 @@ def main(argv=None) -> int:
         sweep(tuple(int(v) for v in args.sweep.split(",")))
         return 0
     if args.case:
-        w, p, m, n, k = (int(v) for v in args.case.split(","))
+        fields = [int(v) for v in args.case.split(",")]
+        w, p, m, n, k = fields[:5]
         import torch
+        from kea_kernels.binary.kernels import GemmConfig
+        config = GemmConfig(fields[5], 1) if len(fields) > 5 else None
         row = _suite_case(w, p, m, n, k, scale_dtype=torch.float16, out_dtype=torch.float16, seed=0,
-                          reps=max(100, args.steps // 100 * 100))
-        print(json.dumps({"case": "gemm", **row}), flush=True)
+                          reps=max(100, args.steps // 100 * 100), config=config)
+        print(json.dumps({"case": "gemm", "tile": fields[5] if config else 0, **row}), flush=True)
         return 0
     if args.encoder:
         for case in args.encoder_cases.split(","):

@@ -1,8 +1,10 @@
 """Build libkea_hip.so (the gfx950 kernels and the C ABI of include/kea_lowbit.h) in-tree with hipcc.
 
-    python kea-kernels_amd/build.py [-j JOBS]
+    python kea-kernels_amd/build.py [-j JOBS] [--max-stages N]
 
 Objects go to kea-kernels_amd/_build/, the library to kea-kernels_amd/kea_kernels/lib/libkea_hip.so.
+--max-stages N rebuilds every translation unit with another LDS-ring depth cap for the ring kernel (default 2; a
+measurement knob: the host's LDS sizing and the kernels must agree, so it is never set per file).
 Every source is compiled for gfx950 only; device FP contraction is off (the epilogue's FP32 op order is part
 of the contract) and packed-FP32 instruction selection is disabled.
 """
@@ -44,8 +46,11 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libkea_hip.so)")
 
 
+EXTRA_DEFINES: list[str] = []
+
+
 def flags() -> list[str]:
-    return ["-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off",
+    return [*EXTRA_DEFINES, "-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off",
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function",
             f"-I{HERE.parent / 'include'}"]
 
@@ -85,4 +90,10 @@ def build(jobs: int | None = None) -> Path:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("-j", "--jobs", type=int, default=None)
-    print(build(ap.parse_args().jobs))
+    ap.add_argument("--max-stages", type=int, default=None, help="ring depth cap (2..8)")
+    args = ap.parse_args()
+    if args.max_stages is not None:
+        if not 2 <= args.max_stages <= 8:
+            ap.error("--max-stages must be 2..8")
+        EXTRA_DEFINES.append(f"-DKEA_MAX_STAGES={args.max_stages}")
+    print(build(args.jobs))
