@@ -69,6 +69,10 @@ __device__ __forceinline__ int t2_hi(uint32_t w) {
 }
 
 __device__ __forceinline__ uint16_t to_f16_bits(float v) {
+    // The FP32 value is rounded to FP32 first and then to FP16 (the contract's two roundings). Without the empty asm
+    // the instruction selector may fuse an fma that produced v into a mixed-precision fma with one FP16 rounding
+    // (v_fma_mixlo_f16), which differs in the last FP16 bit for some inputs.
+    asm("" : "+v"(v));
     _Float16 h = (_Float16)v;  // IEEE round to nearest even
     return __builtin_bit_cast(uint16_t, h);
 }
@@ -227,19 +231,22 @@ __device__ __forceinline__ void epilogue4(const Params &p, int m, int nb, const 
 
 // epilogue4 for a plain output (no GLU pairs, no raw accumulators) of compile-time dtype DT whose 4 columns are all
 // inside N with a vector-aligned y: the same values, one vector store at yrow + nb (yrow: the row's first element),
-// no per-lane selection. RES: the residual is applied (Params::res is set).
-template <int P, int DT, bool RES, bool SMALL>
+// no per-lane selection. RES: the residual is applied (Params::res is set). SILU: 1 / 0 the SiLU is / is not applied
+// (known at compile time: a run-time flag makes the compiler evaluate the SiLU for every output and select), -1: as
+// Params::flags says.
+template <int P, int DT, bool RES, bool SMALL, int SILU = -1>
 __device__ __forceinline__ void epilogue4_full(const Params &p, void *yrow, int nb, const int (*a)[4],
                                                const EpiOperands &e) {
+    const int flags = SILU < 0 ? p.flags : SILU ? (p.flags | KEA_FLAG_SILU) : (p.flags & ~KEA_FLAG_SILU);
     float v[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         int ar[3] = {a[0][r], P > 1 ? a[1][r] : 0, P > 2 ? a[2][r] : 0};
         if constexpr (SMALL) {
-            v[r] = finish(combine<P>(ar, e.s, p.flags), e.alpha[r], p.bias != nullptr, e.bias[r], p.flags);
+            v[r] = finish(combine<P>(ar, e.s, flags), e.alpha[r], p.bias != nullptr, e.bias[r], flags);
             if (p.res) v[r] = e.res[r] + v[r] * p.res_factor;
         } else {
-            v[r] = finish(combine<P>(ar, e.s, p.flags), e.alpha[r], e.bias[r], p.flags);
+            v[r] = finish(combine<P>(ar, e.s, flags), e.alpha[r], e.bias[r], flags);
             if constexpr (RES) v[r] = e.res[r] + v[r] * p.res_factor;
         }
     }

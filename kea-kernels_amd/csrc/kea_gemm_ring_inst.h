@@ -379,9 +379,10 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     // DT >= 0: the output dtype as a compile-time constant; then 16x16 tiles wholly inside [M, N) take a path without
     // per-lane bounds or dtype selection (the tile test is wave-uniform). DT < 0: the general epilogue.
     constexpr bool SMALL = RM * RN <= 2;
-    auto epilogue = [&](auto dt_tag, auto res_tag) {
+    auto epilogue = [&](auto dt_tag, auto res_tag, auto silu_tag) {
         constexpr int DT = decltype(dt_tag)::value;
         constexpr bool RES = decltype(res_tag)::value;
+        constexpr int SILU = decltype(silu_tag)::value;
 #pragma unroll
         for (int i = 0; i < RM; ++i) {
             const int mt = m0 + (wm * RM + i) * 16, m = mt + (lane & 15);
@@ -415,7 +416,7 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
                         epilogue4_groups<P>(p, m, nb, a, racc[i][jn], e);
                     } else if constexpr (DT >= 0) {
                         if (mt + 16 <= p.M && nt + 16 <= p.N) {
-                            epilogue4_full<P, DT, RES, SMALL>(p, yrow, nb, a, e);
+                            epilogue4_full<P, DT, RES, SMALL, SILU>(p, yrow, nb, a, e);
                             continue;
                         }
                         epilogue4<P>(p, m, nb, a, e);
@@ -430,26 +431,36 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     const bool plain = !SLICED && GQ == 0 && p.y && !p.acc && !(p.flags & KEA_FLAG_GLU) && p.y_vec;
     using kRes = std::true_type;
     using kNoRes = std::false_type;
+    using kSiluAtRunTime = std::integral_constant<int, -1>;
     // Tiles of one or two 16x16 blocks per wave (the small-M shapes) keep one epilogue copy per dtype with the
-    // residual and bias tested at run time: separate copies measured slower there (config 1: 4.13 vs 4.27 us).
+    // residual, bias and SiLU tested at run time: separate copies measured slower there (config 1: 4.13 vs 4.27 us).
     if constexpr (SMALL) {
-        if (plain && p.y_dtype == KEA_F16) epilogue(std::integral_constant<int, KEA_F16>{}, kNoRes{});
-        else if (plain && p.y_dtype == KEA_BF16) epilogue(std::integral_constant<int, KEA_BF16>{}, kNoRes{});
-        else if (plain && p.y_dtype == KEA_F32) epilogue(std::integral_constant<int, KEA_F32>{}, kNoRes{});
-        else epilogue(std::integral_constant<int, -1>{}, kNoRes{});
+        if (plain && p.y_dtype == KEA_F16) epilogue(std::integral_constant<int, KEA_F16>{}, kNoRes{}, kSiluAtRunTime{});
+        else if (plain && p.y_dtype == KEA_BF16) epilogue(std::integral_constant<int, KEA_BF16>{}, kNoRes{}, kSiluAtRunTime{});
+        else if (plain && p.y_dtype == KEA_F32) epilogue(std::integral_constant<int, KEA_F32>{}, kNoRes{}, kSiluAtRunTime{});
+        else epilogue(std::integral_constant<int, -1>{}, kNoRes{}, kSiluAtRunTime{});
         return;
     }
+    // Wider tiles: one copy per dtype, residual and SiLU, so the full-block path carries neither test nor a SiLU
+    // evaluated only to be discarded.
+    auto by_flags = [&](auto dt_tag) {
+        const bool silu = (p.flags & KEA_FLAG_SILU) != 0;
+        if (p.res) {
+            if (silu) epilogue(dt_tag, kRes{}, std::integral_constant<int, 1>{});
+            else epilogue(dt_tag, kRes{}, std::integral_constant<int, 0>{});
+        } else {
+            if (silu) epilogue(dt_tag, kNoRes{}, std::integral_constant<int, 1>{});
+            else epilogue(dt_tag, kNoRes{}, std::integral_constant<int, 0>{});
+        }
+    };
     if (plain && p.y_dtype == KEA_F16) {
-        if (p.res) epilogue(std::integral_constant<int, KEA_F16>{}, kRes{});
-        else epilogue(std::integral_constant<int, KEA_F16>{}, kNoRes{});
+        by_flags(std::integral_constant<int, KEA_F16>{});
     } else if (plain && p.y_dtype == KEA_BF16) {
-        if (p.res) epilogue(std::integral_constant<int, KEA_BF16>{}, kRes{});
-        else epilogue(std::integral_constant<int, KEA_BF16>{}, kNoRes{});
+        by_flags(std::integral_constant<int, KEA_BF16>{});
     } else if (plain && p.y_dtype == KEA_F32) {
-        if (p.res) epilogue(std::integral_constant<int, KEA_F32>{}, kRes{});
-        else epilogue(std::integral_constant<int, KEA_F32>{}, kNoRes{});
+        by_flags(std::integral_constant<int, KEA_F32>{});
     } else {
-        epilogue(std::integral_constant<int, -1>{}, kNoRes{});
+        epilogue(std::integral_constant<int, -1>{}, kNoRes{}, kSiluAtRunTime{});
     }
 }
 

@@ -200,6 +200,30 @@ def test_every_tile_gives_identical_results(wbits, parts):
         assert np.array_equal(acc, ref[1]), f"tile {tile}"
 
 
+def _at_odd_offset(t: torch.Tensor) -> torch.Tensor:
+    """A copy of contiguous t whose storage starts one element past an aligned address (2-byte aligned f16)."""
+    buf = torch.zeros(t.numel() + 1, dtype=t.dtype, device=DEV)
+    view = buf[1:].view(t.shape)
+    view.copy_(t)
+    assert view.data_ptr() % 4 == 2
+    return view
+
+
+@pytest.mark.parametrize("tile", [13, 14, 15, 18, 20])
+@pytest.mark.parametrize("parts", [1, 3])
+@torch.inference_mode()
+def test_f16_scales_at_odd_element_offsets_on_wave_split_tiles(tile, parts):
+    """The wave-split kernel loads f16 per-token scales, weight scales and bias as the aligned 32-bit word holding
+    each element and picks the half by address: vectors that start 2 bytes into a word give the oracle's bits."""
+    case = Case(1, parts, 37, 96, 2048, seed=tile + parts, bias=True)
+    qs, alpha, bias = _at_odd_offset(case.dqs), _at_odd_offset(case.dalpha), _at_odd_offset(case.dbias)
+    y = torch.full((case.m, case.n), float("nan"), device=DEV, dtype=torch.float16)
+    lowbit.gemm(1, case.dq, qs, case.words, case.n, case.k, alpha, bias, y, None,
+                config=kernels.GemmConfig(tile=tile, split=1))
+    torch.cuda.synchronize()
+    assert_parity(case, y.cpu(), None)
+
+
 @torch.inference_mode()
 def test_strided_output_rows_and_acc_only():
     case = Case(1, 1, 20, 100, 256, seed=44)
