@@ -190,22 +190,24 @@ def cold_bench(d, stream, launches: int = 1300) -> float:
     return us
 
 
-def launch_floors(d, stream, tile_name: str, reps: int = 10) -> dict:
+def launch_floors(d, stream, tile_name: str, reps: int = 10, shape=(M, N, K)) -> dict:
     """Per-launch microseconds of the launch-floor probes (include/kea_probe.h) on the GEMM's own grid: one
     workgroup per BM x BN tile of the chosen configuration, doing nothing, only loading its tile's operand bytes,
-    only storing its fp16 outputs, or both; graphs of 100 launches, timed as the GEMM is."""
+    only storing its fp16 outputs, or both; graphs of 100 launches, timed as the GEMM is. d holds the shape's q
+    (int8 [m][k]), native 1-bit words and fp16 y."""
     import ctypes
     import torch
     from kea_kernels import _hip
     L = _hip.lib()
+    m, n, k = shape
     bm, bn = (int(v) for v in tile_name.split()[0].split("x"))
     vp = ctypes.c_void_p
     y = torch.empty_like(d["y"])  # the probes' stores must not touch the GEMM's output (checked later)
-    out = {"tile": f"{bm}x{bn}", "workgroups": (M // bm) * (N // bn)}
+    out = {"tile": f"{bm}x{bn}", "workgroups": (m // bm) * (n // bn)}
     for kind, name in enumerate(("empty_us", "loads_us", "stores_us", "loads_stores_us")):
         def probe(i, kind=kind):
-            rc = L.kea_probe_floor(kind, M, N, K, bm, bn, vp(d["q"].data_ptr()), vp(d["words"].data_ptr()),
-                                   vp(y.data_ptr()), N, vp(torch.cuda.current_stream().cuda_stream))
+            rc = L.kea_probe_floor(kind, m, n, k, bm, bn, vp(d["q"].data_ptr()), vp(d["words"].data_ptr()),
+                                   vp(y.data_ptr()), n, vp(torch.cuda.current_stream().cuda_stream))
             _hip.check(rc, "kea_probe_floor")
         graph = capture(stream, probe, 100)
         replay_timed(stream, [graph])
@@ -213,10 +215,99 @@ def launch_floors(d, stream, tile_name: str, reps: int = 10) -> dict:
     return out
 
 
+def probes() -> None:
+    """--probes: what bounds the GEMMs, one JSON line per measurement.
+
+    * mfma: the int8 MFMA loop (kea_probe_mfma_i8_operands) at 1, 2, 4 and 8 waves per SIMD, on the fixed operand
+      pattern and on random bytes (the GEMM's kind of data), best of 5 launches;
+    * exchange: what handing data to the last-arriving workgroup of a group costs inside one launch
+      (kea_probe_exchange: writes only, + a relaxed arrival count, + an acquire-release count and the read), graphs of
+      100 launches, at the group sizes an in-launch split-K (4) and a whole-grid exchange need;
+    * config3_floors: the launch floors of config 3's grid (M = 1024 so the 128x128 tile divides it; N = 4096,
+      K = 1024) next to the GEMM on that grid with tile 11 (128x128)."""
+    import ctypes
+    import torch
+    from kea_kernels import _hip, lowbit
+    from kea_kernels.binary import bits, kernels
+    from kea_kernels.binary.kernels import GemmConfig
+    L = _hip.lib()
+    dev = torch.device("cuda", 0)
+    vp = ctypes.c_void_p
+    stream = torch.cuda.Stream(dev)
+    g = torch.Generator().manual_seed(0)
+
+    def best_of(fn, reps=5):
+        best = float("inf")
+        with torch.cuda.stream(stream):
+            for _ in range(reps + 1):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                fn()
+                b.record(stream)
+                torch.cuda.synchronize()
+                best = min(best, a.elapsed_time(b) * 1e-3)
+        return best
+
+    operands = {"pattern": None,
+                "random": torch.randint(-2 ** 31, 2 ** 31 - 1, (128, 4), generator=g, dtype=torch.int64)
+                .to(torch.int32).to(dev)}
+    out = torch.empty(2048 * 256, dtype=torch.int32, device=dev)
+    for data, ops_t in operands.items():
+        for blocks in (256, 512, 1024, 2048):
+            iters = 2000
+            def run(blocks=blocks, ops_t=ops_t):
+                rc = L.kea_probe_mfma_i8_operands(blocks, iters, vp(ops_t.data_ptr() if ops_t is not None else 0),
+                                                  vp(out.data_ptr()), vp(stream.cuda_stream))
+                _hip.check(rc, "kea_probe_mfma_i8_operands")
+            t = best_of(run)
+            print(json.dumps({"probe": "mfma", "operands": data, "waves_per_simd": blocks // 256,
+                              "tops": round(L.kea_probe_mfma_i8_ops(blocks, iters) / t / 1e12, 1)}), flush=True)
+
+    for wgs in (64, 256, 1024):
+        for nbytes in (1024, 16384):
+            words = nbytes // 16
+            slots = torch.zeros(wgs * words * 4, dtype=torch.int32, device=dev)
+            for group in sorted({4, wgs}):
+                counters = torch.zeros(-(-wgs // group), dtype=torch.int32, device=dev)
+                result = torch.zeros(1, dtype=torch.int32, device=dev)
+                row = {"probe": "exchange", "workgroups": wgs, "bytes_per_workgroup": nbytes, "group": group}
+                for kind, name in enumerate(("write_us", "count_us", "fenced_us")):
+                    def launch(i=0, kind=kind):
+                        rc = L.kea_probe_exchange(kind, wgs, words, group, vp(slots.data_ptr()),
+                                                  vp(counters.data_ptr()), vp(result.data_ptr()),
+                                                  vp(torch.cuda.current_stream().cuda_stream))
+                        _hip.check(rc, "kea_probe_exchange")
+                    graph = capture(stream, launch, 100)
+                    replay_timed(stream, [graph])
+                    row[name] = round(replay_timed(stream, [graph], 5) * 1000 / 500, 3)
+                with torch.cuda.stream(stream):
+                    result.zero_()
+                    launch(kind=2)
+                torch.cuda.synchronize()
+                row["fenced_sum_ok"] = (int(result.item()) & 0xFFFFFFFF) == (wgs * (wgs - 1) // 2) & 0xFFFFFFFF
+                print(json.dumps(row), flush=True)
+
+    m, n, k = 1024, 4096, 1024
+    q = torch.randint(-127, 128, (1, m, k), generator=g, dtype=torch.int8).to(dev)
+    qs = (torch.rand(1, m, generator=g) * 0.01 + 1e-3).half().to(dev)
+    codes = bits.pack_signs(torch.where(torch.rand(n, k, generator=g) < 0.5, -1, 1).to(torch.int8))
+    words = kernels.relayout_codes(codes, k, 1).to(dev)
+    alpha = (torch.rand(n, generator=g) * 0.09 + 0.01).half().to(dev)
+    y = torch.empty(m, n, dtype=torch.float16, device=dev)
+    row = {"probe": "config3_floors", "M": m, "N": n, "K": k}
+    row.update(launch_floors({"q": q, "words": words, "y": y}, stream, "128x128", shape=(m, n, k)))
+    gemm = capture(stream, lambda i: lowbit.gemm(1, q, qs, words, n, k, alpha, None, y, None,
+                                                 config=GemmConfig(11, 1)), 100)
+    replay_timed(stream, [gemm])
+    row["gemm_tile11_us"] = round(replay_timed(stream, [gemm], 10) * 1000 / 1000, 3)
+    print(json.dumps(row), flush=True)
+
+
 def measured_peaks(reps: int = 5) -> dict:
     """What this GPU sustains, for fractions against measured rather than published peaks: the dense int8 MFMA loop
-    of the library's probe (kea_probe_mfma_i8: 2048 workgroups of four waves, 8 independent 16x16x64 MFMA chains
-    each) and a 1 GiB device-to-device copy (read + write bytes). Best of `reps` event-timed launches each."""
+    of the library's probe (2048 workgroups of four waves, 8 independent 16x16x64 MFMA chains each) on its fixed
+    operand pattern and on random operand bytes (the kind of data a GEMM multiplies; the matrix cores sustain less on
+    it), and a 1 GiB device-to-device copy (read + write bytes). Best of `reps` event-timed launches each."""
     import ctypes
     import torch
     from kea_kernels import _hip
@@ -226,6 +317,8 @@ def measured_peaks(reps: int = 5) -> dict:
     blocks, iters = 2048, 2000
     out = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
     ops = L.kea_probe_mfma_i8_ops(blocks, iters)
+    g = torch.Generator().manual_seed(0)
+    random_words = torch.randint(-2 ** 31, 2 ** 31 - 1, (128, 4), generator=g, dtype=torch.int64).to(torch.int32).to(dev)
 
     def timed(fn):
         best = float("inf")
@@ -238,20 +331,24 @@ def measured_peaks(reps: int = 5) -> dict:
             best = min(best, a.elapsed_time(b) * 1e-3)
         return best
 
-    def mfma():
-        rc = L.kea_probe_mfma_i8(blocks, iters, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream.cuda_stream))
+    def mfma(operands):
+        rc = L.kea_probe_mfma_i8_operands(blocks, iters, ctypes.c_void_p(operands), ctypes.c_void_p(out.data_ptr()),
+                                          ctypes.c_void_p(stream.cuda_stream))
         if rc != 0:
             raise RuntimeError(f"kea_probe_mfma_i8: {L.kea_last_error().decode()}")
 
-    t_mfma = timed(mfma)
+    t_pattern = timed(lambda: mfma(None))
+    t_random = timed(lambda: mfma(random_words.data_ptr()))
     src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     t_copy = timed(lambda: dst.copy_(src))
     nbytes = 2 * src.numel() * 4
     del src, dst
-    return {"mfma_i8_tops": round(ops / t_mfma / 1e12, 1), "copy_gbs": round(nbytes / t_copy / 1e9, 1),
-            "method": "int8 MFMA loop (2048 WGs x 4 waves x 2000 x 8 v_mfma_i32_16x16x64_i8) and a 1 GiB "
-                      "device-to-device copy (read + write bytes), best of 5"}
+    return {"mfma_i8_tops": round(ops / t_pattern / 1e12, 1), "mfma_i8_tops_random": round(ops / t_random / 1e12, 1),
+            "copy_gbs": round(nbytes / t_copy / 1e9, 1),
+            "method": "int8 MFMA loop (2048 WGs x 4 waves x 2000 x 8 v_mfma_i32_16x16x64_i8) on the probe's fixed "
+                      "operand pattern and on random operand bytes, and a 1 GiB device-to-device copy (read + write "
+                      "bytes), best of 5; frac_of_measured uses the random-operand rate"}
 
 
 def cpu_model() -> str:
@@ -547,11 +644,17 @@ def main(argv=None) -> int:
     ap.add_argument("--sweep", default=None, metavar="PARTS",
                     help="only time every tile configuration at the chooser's shapes for these part counts "
                          "(e.g. 1,2,3; one JSON line per shape)")
+    ap.add_argument("--probes", action="store_true",
+                    help="only run the bounding probes: int8 MFMA rate by occupancy and operand data, the cost of a "
+                         "cross-workgroup exchange inside one launch, and config 3's launch floors")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache config-1 figure")
     ap.add_argument("--no-floors", action="store_true", help="skip the launch-floor probes")
     args = ap.parse_args(argv)
     if args.suite:
         suite()
+        return 0
+    if args.probes:
+        probes()
         return 0
     if args.sweep:
         sweep(tuple(int(v) for v in args.sweep.split(",")))
@@ -642,7 +745,7 @@ def main(argv=None) -> int:
         line["floors"] = floors
     if not args.no_peaks:
         peaks = measured_peaks()
-        measured = peaks["mfma_i8_tops"] if bound == "mfma" else peaks["copy_gbs"]
+        measured = peaks["mfma_i8_tops_random"] if bound == "mfma" else peaks["copy_gbs"]
         line["roofline"]["measured_peak"] = measured
         line["roofline"]["frac_of_measured"] = round(achieved / measured, 5)
         line["measured_peaks"] = peaks

@@ -19,8 +19,36 @@ extern "C" {
  * blocks in [1, 65536], iters in [1, 1 << 20]. */
 int kea_probe_mfma_i8(int64_t blocks, int64_t iters, int32_t *out, void *stream);
 
+/* The same loop on caller-supplied operands: `operands` is [128][4] int32 in device memory, 16-byte aligned (the A
+ * operand words of lanes 0-63, then the B operand words), or NULL for kea_probe_mfma_i8's fixed pattern. Random bytes
+ * measure the rate on data like a GEMM's: the matrix cores draw more power on them and the clock drops. */
+int kea_probe_mfma_i8_operands(int64_t blocks, int64_t iters, const int32_t *operands, int32_t *out, void *stream);
+
 /* The ops one kea_probe_mfma_i8 launch performs (0 for arguments it would reject). */
 int64_t kea_probe_mfma_i8_ops(int64_t blocks, int64_t iters);
+
+/* Keeps the stream busy for `ns` nanoseconds (one wavefront spinning on the device's constant-rate wall clock, so
+ * it always ends): enqueued in front of a timed region, it lets the host finish submitting the region's work before
+ * the region's start event executes, so host submission latency stays out of the measurement. ns in [0, 1e8]. */
+int kea_probe_spin(int64_t ns, void *stream);
+
+/* Cross-workgroup exchange: `workgroups` workgroups of 256 threads in groups of `group` consecutive ones (the last
+ * group may be shorter). Workgroup w writes `words` 16-byte words to its slot (slots: workgroups * words * 16 bytes,
+ * 16-byte aligned; word i = {w, i, w ^ i, 1}), then:
+ *   KEA_EXCHANGE_WRITE   nothing more (the cost of the writes alone);
+ *   KEA_EXCHANGE_COUNT   counts itself in on its group's counter with a relaxed device-scope atomic (no ordering:
+ *                        what the serialised arrivals on one address cost);
+ *   KEA_EXCHANGE_FENCED  counts itself in with an acquire-release device-scope atomic, and the group's last arriver
+ *                        reads the first component of every group member's last word and adds their sum to *result.
+ * This is the exchange an in-launch split-K reduction (group = the K slices of a tile) or a quantizer fused behind a
+ * GEMM (group = the column tiles of a row block) would need. counters: ceil(workgroups / group) uint32, zero before
+ * the first launch; the counting kinds leave them zero. After one FENCED launch *result has grown by the sum of
+ * 0 .. workgroups-1 (mod 2^32). workgroups and words in [1, 65536], group in [1, workgroups]. */
+#define KEA_EXCHANGE_WRITE 0
+#define KEA_EXCHANGE_COUNT 1
+#define KEA_EXCHANGE_FENCED 2
+int kea_probe_exchange(int kind, int64_t workgroups, int64_t words, int64_t group, void *slots, uint32_t *counters,
+                       uint32_t *result, void *stream);
 
 /* Launch floors of a GEMM-shaped grid: (n / bn) x (m / bm) workgroups of 256 threads, one per bm x bn output tile of
  * an m x n x k low-bit GEMM, as kea_lowbit_gemm launches them. What each workgroup does:
@@ -33,11 +61,6 @@ int64_t kea_probe_mfma_i8_ops(int64_t blocks, int64_t iters);
  * Requirements: bm, bn multiples of 16 in [16, 256]; m, n multiples of bm, bn (<= 2^20); k a multiple of 128
  * (<= 65536); bm * k + bn * k / 8 <= 160 KiB when loading; a, w 16-byte aligned; y 8-byte aligned, ldy >= n,
  * ldy % 4 == 0. */
-/* Keeps the stream busy for `ns` nanoseconds (one wavefront spinning on the device's constant-rate wall clock, so
- * it always ends): enqueued in front of a timed region, it lets the host finish submitting the region's work before
- * the region's start event executes, so host submission latency stays out of the measurement. ns in [0, 1e8]. */
-int kea_probe_spin(int64_t ns, void *stream);
-
 #define KEA_PROBE_EMPTY 0
 #define KEA_PROBE_LOADS 1
 #define KEA_PROBE_STORES 2

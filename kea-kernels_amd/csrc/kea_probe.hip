@@ -15,12 +15,18 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kProbeChains = 8;            // independent accumulators per wave: covers the MFMA dependency latency
 constexpr int64_t kOpsPerMfma = 16 * 16 * 64 * 2;
 
-// Each lane's operands are distinct, non-zero words so the products are not constant; the accumulators feed one
-// int32 per thread. Integer MFMA wraps (no saturation), so any iteration count is well defined.
-__global__ void __launch_bounds__(256) mfma_i8_loop(int iters, int32_t *out) {
+// Each lane's operands are distinct words: a fixed pattern of non-zero words, or (operands != nullptr) the caller's
+// [128][4] int32 words (a for lanes 0-63, then b), e.g. random bytes like a GEMM's data: the matrix cores draw more
+// power on such operands and the clock drops. The accumulators feed one int32 per thread. Integer MFMA wraps (no
+// saturation), so any iteration count is well defined.
+__global__ void __launch_bounds__(256) mfma_i8_loop(int iters, const v4i *operands, int32_t *out) {
     const int lane = threadIdx.x & 63;
-    const v4i a = {0x01020304 + lane, 0x05060708 - lane, 0x090A0B0C ^ lane, 0x0D0E0F10 + 3 * lane};
-    const v4i b = {0x11121314 - lane, 0x15161718 + lane, 0x191A1B1C ^ (lane << 8), 0x1D1E1F20 + 5 * lane};
+    v4i a = {0x01020304 + lane, 0x05060708 - lane, 0x090A0B0C ^ lane, 0x0D0E0F10 + 3 * lane};
+    v4i b = {0x11121314 - lane, 0x15161718 + lane, 0x191A1B1C ^ (lane << 8), 0x1D1E1F20 + 5 * lane};
+    if (operands) {
+        a = operands[lane];
+        b = operands[64 + lane];
+    }
     v4i acc[kProbeChains];
 #pragma unroll
     for (int c = 0; c < kProbeChains; ++c) acc[c] = (v4i){c, 0, 0, 0};
@@ -97,6 +103,42 @@ __global__ void __launch_bounds__(256) floor_kernel(FloorArgs f) {
     }
 }
 
+// ---- cross-workgroup exchange -------------------------------------------------------------------------------------
+// What it costs one launch to hand data from workgroups to the last-arriving workgroup of their group, the pattern an
+// in-launch split-K reduction or a quantizer fused after a GEMM would need. Workgroup w writes `words` uint4 to its
+// slot (word i = {w, i, w ^ i, 1}); then, by KIND, thread 0 counts the workgroup in on its group's counter. No
+// workgroup waits for another, so every launch ends.
+template <int KIND>
+__global__ void __launch_bounds__(256) exchange_kernel(uint4 *slots, int words, int group, uint32_t *counters,
+                                                       uint32_t *result) {
+    const int w = blockIdx.x, nwg = gridDim.x;
+    uint4 *mine = slots + (size_t)w * words;
+    for (int i = threadIdx.x; i < words; i += 256) mine[i] = make_uint4((unsigned)w, (unsigned)i, (unsigned)(w ^ i), 1u);
+    if constexpr (KIND == KEA_EXCHANGE_WRITE) {
+        return;
+    } else {
+        const int g = w / group, first = g * group, members = min(group, nwg - first);
+        __shared__ int last;
+        __syncthreads();  // every thread's slot words are written (and, at workgroup scope, ordered) before the count
+        if (threadIdx.x == 0) {
+            unsigned old;
+            if constexpr (KIND == KEA_EXCHANGE_FENCED)
+                old = __hip_atomic_fetch_add(counters + g, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            else
+                old = __hip_atomic_fetch_add(counters + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = old == (unsigned)members - 1;
+            if (last) __hip_atomic_store(counters + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if constexpr (KIND == KEA_EXCHANGE_FENCED) {
+            if (!last) return;
+            unsigned sum = 0;
+            for (int v = threadIdx.x; v < members; v += 256) sum += slots[(size_t)(first + v) * words + words - 1].x;
+            if (sum) atomicAdd(result, sum);
+        }
+    }
+}
+
 // Spins one wavefront on the constant-rate wall clock (s_memrealtime) until `ticks` have passed: always ends.
 __global__ void __launch_bounds__(64) spin_kernel(unsigned long long ticks) {
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
@@ -112,15 +154,21 @@ int64_t kea_probe_mfma_i8_ops(int64_t blocks, int64_t iters) {
     return blocks * 4 * iters * kProbeChains * kOpsPerMfma;
 }
 
-int kea_probe_mfma_i8(int64_t blocks, int64_t iters, int32_t *out, void *stream) {
+int kea_probe_mfma_i8_operands(int64_t blocks, int64_t iters, const int32_t *operands, int32_t *out, void *stream) {
     if (!probe_args_ok(blocks, iters))
         return kea::fail(KEA_EINVAL, "kea_probe_mfma_i8: blocks must be in [1, 65536] and iters in [1, 2^20]");
     if (!out) return kea::fail(KEA_EINVAL, "kea_probe_mfma_i8: out is null");
     if ((uintptr_t)out & 3) return kea::fail(KEA_EALIGN, "kea_probe_mfma_i8: out must be 4-byte aligned");
-    hipLaunchKernelGGL(mfma_i8_loop, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (int)iters, out);
+    if ((uintptr_t)operands & 15) return kea::fail(KEA_EALIGN, "kea_probe_mfma_i8: operands must be 16-byte aligned");
+    hipLaunchKernelGGL(mfma_i8_loop, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (int)iters,
+                       (const v4i *)operands, out);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_mfma_i8: ") + hipGetErrorString(e));
     return 0;
+}
+
+int kea_probe_mfma_i8(int64_t blocks, int64_t iters, int32_t *out, void *stream) {
+    return kea_probe_mfma_i8_operands(blocks, iters, nullptr, out, stream);
 }
 
 int kea_probe_spin(int64_t ns, void *stream) {
@@ -134,6 +182,30 @@ int kea_probe_spin(int64_t ns, void *stream) {
     hipLaunchKernelGGL(spin_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, ticks);
     e = hipGetLastError();
     if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_spin: ") + hipGetErrorString(e));
+    return 0;
+}
+
+int kea_probe_exchange(int kind, int64_t workgroups, int64_t words, int64_t group, void *slots, uint32_t *counters,
+                       uint32_t *result, void *stream) {
+    if (kind < KEA_EXCHANGE_WRITE || kind > KEA_EXCHANGE_FENCED)
+        return kea::fail(KEA_EINVAL, "kea_probe_exchange: kind must be 0 (write), 1 (count) or 2 (fenced)");
+    if (workgroups < 1 || workgroups > 65536 || words < 1 || words > 65536 || group < 1 || group > workgroups)
+        return kea::fail(KEA_EINVAL, "kea_probe_exchange: workgroups and words must be in [1, 65536], group in "
+                                     "[1, workgroups]");
+    if (!slots || ((uintptr_t)slots & 15)) return kea::fail(KEA_EALIGN, "kea_probe_exchange: slots must be 16-byte aligned");
+    if (kind != KEA_EXCHANGE_WRITE && (!counters || ((uintptr_t)counters & 3)))
+        return kea::fail(KEA_EINVAL, "kea_probe_exchange: counting kinds need 4-byte aligned counters");
+    if (kind == KEA_EXCHANGE_FENCED && (!result || ((uintptr_t)result & 3)))
+        return kea::fail(KEA_EINVAL, "kea_probe_exchange: the fenced kind needs a 4-byte aligned result");
+    hipStream_t st = (hipStream_t)stream;
+    void (*fn)(uint4 *, int, int, uint32_t *, uint32_t *) =
+        kind == KEA_EXCHANGE_WRITE ? exchange_kernel<KEA_EXCHANGE_WRITE>
+        : kind == KEA_EXCHANGE_COUNT ? exchange_kernel<KEA_EXCHANGE_COUNT>
+                                     : exchange_kernel<KEA_EXCHANGE_FENCED>;
+    hipLaunchKernelGGL(fn, dim3((unsigned)workgroups), dim3(256), 0, st, (uint4 *)slots, (int)words, (int)group,
+                       counters, result);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_exchange: ") + hipGetErrorString(e));
     return 0;
 }
 

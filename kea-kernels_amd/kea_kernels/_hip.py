@@ -85,6 +85,8 @@ SIGNATURES = {
     "kea_dwconv_quantize": (_i32, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _i64, _vp, _vp]),
     "kea_probe_mfma_i8": (_i32, [_i64, _i64, _vp, _vp]),
     "kea_probe_mfma_i8_ops": (_i64, [_i64, _i64]),
+    "kea_probe_mfma_i8_operands": (_i32, [_i64, _i64, _vp, _vp, _vp]),
+    "kea_probe_exchange": (_i32, [_i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "kea_probe_floor": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _i64, _vp]),
     "kea_probe_spin": (_i32, [_i64, _vp]),
     "kea_last_error": (_cp, []),

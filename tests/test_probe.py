@@ -39,16 +39,38 @@ def test_floor_and_spin_probe_arguments():
     assert L.kea_probe_spin(-1, None) == -1 and L.kea_probe_spin(100000001, None) == -1
 
 
+def test_operand_and_exchange_probe_arguments():
+    """The operand-fed MFMA loop and the exchange probe refuse bad arguments before any launch."""
+    L = _hip.lib()
+    vp = ctypes.c_void_p
+    assert L.kea_probe_mfma_i8_operands(1, 1, vp(8), vp(16), None) == -2       # operands not 16-byte aligned
+    assert b"operands" in L.kea_last_error()
+    assert L.kea_probe_mfma_i8_operands(0, 1, None, vp(16), None) == -1        # blocks
+    assert L.kea_probe_exchange(3, 64, 64, 4, vp(16), vp(16), vp(16), None) == -1  # kind
+    assert b"kind" in L.kea_last_error()
+    assert L.kea_probe_exchange(0, 0, 64, 1, vp(16), None, None, None) == -1      # workgroups
+    assert L.kea_probe_exchange(0, 64, 64, 65, vp(16), None, None, None) == -1    # group > workgroups
+    assert L.kea_probe_exchange(0, 64, 64, 4, vp(8), None, None, None) == -2      # slots alignment
+    assert L.kea_probe_exchange(1, 64, 64, 4, vp(16), None, None, None) == -1     # counting needs counters
+    assert L.kea_probe_exchange(2, 64, 64, 4, vp(16), vp(16), None, None) == -1   # fenced needs a result
+
+
 def _operand_bytes(words):
     """[64 lanes, 4 int32] -> [64, 16] bytes, little-endian."""
     return np.asarray(words, dtype=np.int64).astype(np.uint32).view(np.uint8).reshape(64, 16)
 
 
-def expected_checksums(iters: int) -> np.ndarray:
+def _pattern_words():
     lane = np.arange(64, dtype=np.int64)
-    a = _operand_bytes(np.stack([0x01020304 + lane, 0x05060708 - lane, 0x090A0B0C ^ lane, 0x0D0E0F10 + 3 * lane], 1))
-    b = _operand_bytes(np.stack([0x11121314 - lane, 0x15161718 + lane, 0x191A1B1C ^ (lane << 8),
-                                 0x1D1E1F20 + 5 * lane], 1))
+    a = np.stack([0x01020304 + lane, 0x05060708 - lane, 0x090A0B0C ^ lane, 0x0D0E0F10 + 3 * lane], 1)
+    b = np.stack([0x11121314 - lane, 0x15161718 + lane, 0x191A1B1C ^ (lane << 8), 0x1D1E1F20 + 5 * lane], 1)
+    return a, b
+
+
+def expected_checksums(iters: int, words=None) -> np.ndarray:
+    """Per-lane checksums of the probe: words = (a, b), each [64][4] int32 operand words (default: the pattern)."""
+    aw, bw = words if words is not None else _pattern_words()
+    a, b = _operand_bytes(aw), _operand_bytes(bw)
     A = np.zeros((16, 64), np.int64)
     B = np.zeros((64, 16), np.int64)
     for l in range(64):
@@ -76,3 +98,44 @@ def test_probe_checksum_matches_the_mfma_emulation():
     torch.cuda.synchronize()
     want = np.tile(expected_checksums(iters), blocks * 4)
     assert np.array_equal(out.cpu().numpy(), want)
+
+
+@pytest.mark.gpu
+def test_operand_fed_probe_checksum_on_random_operands():
+    L = _hip.lib()
+    dev = torch.device("cuda", 0)
+    g = np.random.default_rng(7)
+    words = g.integers(-2 ** 31, 2 ** 31, size=(128, 4), dtype=np.int64).astype(np.int32)
+    ops = torch.from_numpy(words).to(dev)
+    blocks, iters = 2, 7
+    out = torch.full((blocks * 256,), -1, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    rc = L.kea_probe_mfma_i8_operands(blocks, iters, ctypes.c_void_p(ops.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                      ctypes.c_void_p(stream.cuda_stream))
+    assert rc == 0, L.kea_last_error()
+    torch.cuda.synchronize()
+    want = np.tile(expected_checksums(iters, (words[:64], words[64:])), blocks * 4)
+    assert np.array_equal(out.cpu().numpy(), want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("workgroups,words,group", [(64, 64, 4), (300, 1024, 300), (257, 16, 5)])
+def test_exchange_probe_fenced_sum_and_counters(workgroups, words, group):
+    """The fenced exchange's last arrivers read every member's slot: after two launches the sum is twice
+    0 + 1 + ... + (workgroups - 1), and every group counter is back at zero."""
+    L = _hip.lib()
+    dev = torch.device("cuda", 0)
+    slots = torch.zeros(workgroups * words * 4, dtype=torch.int32, device=dev)
+    counters = torch.zeros(-(-workgroups // group), dtype=torch.int32, device=dev)
+    result = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    vp = ctypes.c_void_p
+    for kind in (1, 2, 2):
+        rc = L.kea_probe_exchange(kind, workgroups, words, group, vp(slots.data_ptr()), vp(counters.data_ptr()),
+                                  vp(result.data_ptr()), vp(stream.cuda_stream))
+        assert rc == 0, L.kea_last_error()
+    torch.cuda.synchronize()
+    assert int(result.item()) & 0xFFFFFFFF == (workgroups * (workgroups - 1)) & 0xFFFFFFFF
+    assert not counters.any()
+    last = slots.view(workgroups, words, 4)[:, -1].cpu().numpy()
+    assert np.array_equal(last[:, 0], np.arange(workgroups)) and np.array_equal(last[:, 1], np.full(workgroups, words - 1))
