@@ -134,6 +134,11 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
     // sinking the scale loads to their use in the epilogue, where their latency would stand alone.
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
+    // The epilogue's kernel arguments are pinned into scalar registers now, while the operand loads are in flight:
+    // read where they are used, each would be a kernel-argument round trip on the epilogue's critical path.
+    if constexpr (!SLICED)
+        asm volatile("" ::"s"(p.M), "s"(p.N), "s"(p.res), "s"(p.ldr), "s"(p.res_factor), "s"(p.y), "s"(p.ldy),
+                     "s"(p.flags), "s"(p.y_dtype), "s"(p.y_vec), "s"(p.acc));
 
     // ---- MFMAs: straight-line code over the wave's S k-steps ----
     v4i acc[P][RM][NT];
