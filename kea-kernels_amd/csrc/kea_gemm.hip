@@ -252,7 +252,7 @@ static int resolve(int wbits, int parts, int64_t m, int64_t n, int64_t k, int sp
         return KEA_OK;
     }
     const Tile &tl = kTiles[id - 1];
-    if (!tile_fits(wbits, parts, tl.rm, tl.rn, tl.wm, tl.wn))
+    if (!tile_fits(wbits, parts, tl.rm, tl.rn, tl.wm, tl.wn, tl.pw))
         return kea::fail(KEA_EINVAL, std::string("tile ") + kTiles[id - 1].name + " does not fit " +
                                          std::to_string(parts) + " activation parts");
     const long long J = wbits == 1 ? cdivl(k, 128) : cdivl(k, 64);
@@ -406,7 +406,7 @@ int gemm_prepare(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, i
     // Ring buffers actually used: a workgroup touches buffer s % NS for its stages s < nst, so with nst < NS only
     // the first nst buffers need LDS.
     const long long words_per_wg = std::min<long long>(4LL * qps, (long long)p.J);
-    const StageShape shape = stage_shape(wbits, parts, t.rm, t.rn, t.wm, t.wn);
+    const StageShape shape = stage_shape(wbits, parts, t.rm, t.rn, t.wm, t.wn, t.pw);
     const int nst = (int)cdivl(words_per_wg, shape.sw);
     int lds_bytes = std::min(shape.ns, nst) * shape.stage_bytes;
     if (gq) {
@@ -420,10 +420,10 @@ int gemm_prepare(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, i
         if (lds_bytes > kLdsBudget)
             return kea::fail(KEA_EINVAL, "too many weight-scale groups for one workgroup's LDS: use a larger ws_group");
     }
-    if (!kea::fits_dispatch(cdivl(n, bn), t.wm * t.wn * 64))
+    if (!kea::fits_dispatch(cdivl(n, bn), (t.wm * t.wn + t.pw) * 64))
         return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N or M");
     ls->grid = dim3((unsigned)cdivl(n, bn), (unsigned)cdivl(m, bm), (unsigned)s);
-    ls->block = dim3(t.wm * t.wn * 64);
+    ls->block = dim3((t.wm * t.wn + t.pw) * 64);
     ls->ring_fn = gq ? pick_group(wbits, parts, gq, tile, (k & 15) != 0)
                      : pick_kernel(wbits, parts, tile, s > 1, (k & 15) != 0);
     if (!ls->ring_fn) return kea::fail(KEA_EINVAL, "no kernel instance for this tile");
@@ -759,18 +759,18 @@ int kea_lowbit_gemm_slices(int wbits, const int8_t *q, int64_t part_stride, int6
     const Tile &t = kTiles[tile - 1];
     const int bm = t.wm * t.rm * 16, bn = t.wn * t.rn * 16;
     const long long words_per_wg = std::min<long long>(4LL * qps, (long long)p.J);
-    const StageShape shape = stage_shape(wbits, parts, t.rm, t.rn, t.wm, t.wn);
+    const StageShape shape = stage_shape(wbits, parts, t.rm, t.rn, t.wm, t.wn, t.pw);
     const int nst = (int)cdivl(words_per_wg, shape.sw);
     const int lds_bytes = std::min(shape.ns, nst) * shape.stage_bytes;
-    if (!kea::fits_dispatch(cdivl(n, bn), t.wm * t.wn * 64))
+    if (!kea::fits_dispatch(cdivl(n, bn), (t.wm * t.wn + t.pw) * 64))
         return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N");
     KernelFn fn = pick_kernel(wbits, parts, tile, true, false);
     if (lds_bytes > 65536) {
         hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
         if (e != hipSuccess) return kea::fail((int)e, std::string("LDS attribute refused: ") + hipGetErrorString(e));
     }
-    hipLaunchKernelGGL(fn, dim3((unsigned)cdivl(n, bn), (unsigned)cdivl(m, bm), (unsigned)s), dim3(t.wm * t.wn * 64),
-                       lds_bytes, (hipStream_t)stream, p);
+    hipLaunchKernelGGL(fn, dim3((unsigned)cdivl(n, bn), (unsigned)cdivl(m, bm), (unsigned)s),
+                       dim3((t.wm * t.wn + t.pw) * 64), lds_bytes, (hipStream_t)stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return kea::fail((int)e, std::string("slice launch failed: ") + hipGetErrorString(e));
     return KEA_OK;

@@ -39,8 +39,8 @@ constexpr int kMaxStages = KEA_MAX_STAGES;
 #ifndef KEA_FULL_PRM
 #define KEA_FULL_PRM 2
 #endif
-__host__ __device__ constexpr StageShape stage_shape(int wbits, int parts, int rm, int rn, int wm, int wn) {
-    const int nw = wm * wn, bm = wm * rm * 16, bn = wn * rn * 16;
+__host__ __device__ constexpr StageShape stage_shape(int wbits, int parts, int rm, int rn, int wm, int wn, int pw = 0) {
+    const int nw = pw > 0 ? pw : wm * wn, bm = wm * rm * 16, bn = wn * rn * 16;  // nw: the waves issuing copies
     const int sw = KEA_STAGE_K / (wbits == 1 ? 128 : 64);
     const int a_units = parts * bm * (KEA_STAGE_K / 16);
     const int b_words = (bn / 16) * sw;
@@ -53,9 +53,12 @@ __host__ __device__ constexpr StageShape stage_shape(int wbits, int parts, int r
     return StageShape{sw, stage, copies, ns};
 }
 
+// pw > 0: the workgroup has pw more waves that only issue the global->LDS copies of the ring (producer waves),
+// while the wm x wn compute waves only read LDS and run the MFMAs and the epilogue.
 struct Tile {
     int rm, rn, wm, wn;
     const char *name;
+    int pw = 0;
 };
 
 // Tile configurations (ids are 1-based in the ABI). Results are identical for every tile.
@@ -65,8 +68,8 @@ constexpr Tile kTiles[] = {
     {1, 2, 2, 2, "32x64 w2x2 r1x2"},   // 3
     {1, 1, 2, 2, "32x32 w2x2 r1x1"},   // 4
     {4, 1, 1, 4, "64x64 w1x4 r4x1"},   // 5
-    {8, 1, 1, 4, "128x64 w1x4 r8x1"},  // 6
-    {2, 4, 2, 2, "64x128 w2x2 r2x4"},  // 7
+    {4, 2, 2, 4, "128x128 w2x4 r4x2 p8", 8},  // 6: tile 11's compute waves and 8 producer waves
+    {4, 2, 1, 4, "64x128 w1x4 r4x2 p4", 4},   // 7: tile 8's compute waves and 4 producer waves
     {4, 2, 1, 4, "64x128 w1x4 r4x2"},  // 8
     {2, 2, 1, 4, "32x128 w1x4 r2x2"},  // 9
     {2, 4, 2, 4, "64x256 w2x4 r2x4"},  // 10
@@ -75,11 +78,14 @@ constexpr Tile kTiles[] = {
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
-// Register budget of a tile: accumulators plus double-buffered activation fragments (in 32-bit registers); and two
-// ring buffers of the tile's stage within the LDS a workgroup may allocate.
-constexpr bool tile_fits(int wbits, int parts, int rm, int rn, int wm, int wn) {
-    return parts * rm * rn * 4 + 2 * parts * rm * 4 <= 256 &&
-           2 * stage_shape(wbits, parts, rm, rn, wm, wn).stage_bytes <= kLdsBudget;
+// Register budget of a tile: accumulators plus double-buffered activation fragments (in 32-bit registers). Up to 8
+// waves per workgroup (two per SIMD) they may take 256 of a wave's 256; with more waves a SIMD holds three or four of
+// them in its 512 registers per lane, and the arrays must leave 64 of a wave's share to the rest of the kernel. Two
+// ring buffers of the tile's stage must fit the LDS a workgroup may allocate.
+constexpr bool tile_fits(int wbits, int parts, int rm, int rn, int wm, int wn, int pw = 0) {
+    const int waves = wm * wn + pw, per_simd = (waves + 3) / 4;
+    return parts * rm * rn * 4 + 2 * parts * rm * 4 <= (waves <= 8 ? 256 : 512 / per_simd - 64) &&
+           2 * stage_shape(wbits, parts, rm, rn, wm, wn, pw).stage_bytes <= kLdsBudget;
 }
 
 using KernelFn = void (*)(Params);

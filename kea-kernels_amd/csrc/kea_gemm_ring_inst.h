@@ -56,13 +56,18 @@ __device__ __forceinline__ void dma4(const void *g, void *lds_wave_base) {
 // last k-step of each group every lane folds that group's exact int32 sums into an FP32 running value:
 // r = fma(comb_P(acc - acc_at_previous_group_end), alpha[n][g], r). Group ends are fixed positions of the unrolled
 // stage, so the folding is straight-line code; accumulators are only read there.
-template <int WBITS, int P, int RM, int RN, int WM, int WN, bool SLICED, bool KTAIL, int GQ = 0>
-__global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
+//
+// PW > 0 (producer waves): waves NW .. NW + PW - 1 of the workgroup issue every copy and wait for them, and the NW
+// compute waves never wait on memory counters for the ring; the stage barriers hand the buffers between the two.
+template <int WBITS, int P, int RM, int RN, int WM, int WN, bool SLICED, bool KTAIL, int GQ = 0, int PW = 0>
+__global__ void __launch_bounds__((WM * WN + PW) * 64) gemm_kernel(Params p) {
     static_assert(GQ == 0 || GQ == 1 || GQ == 2 || GQ == 4, "groups of 64, 128 or 256 k");
     static_assert(GQ == 0 || !SLICED, "per-group scales run unsplit");
-    constexpr StageShape SHAPE = stage_shape(WBITS, P, RM, RN, WM, WN);
+    static_assert(PW == 0 || GQ == 0, "producer waves: no per-group scales");
+    constexpr StageShape SHAPE = stage_shape(WBITS, P, RM, RN, WM, WN, PW);
     constexpr int SW = SHAPE.sw, NS = SHAPE.ns;
-    constexpr int NW = WM * WN;                 // wavefronts
+    constexpr int NW = WM * WN;                 // compute wavefronts
+    constexpr int NI = PW > 0 ? PW : NW;        // wavefronts issuing the copies
     constexpr int BM = WM * RM * 16, BN = WN * RN * 16;
     constexpr int KW = WBITS == 1 ? 128 : 64;   // k per native word
     constexpr int KS = KW / 64;                 // MFMA k-steps per word
@@ -73,11 +78,11 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     constexpr int A_BYTES = A_UNITS * 16;
     constexpr int B_WORDS = (BN / 16) * SW;     // (tile, word) pairs per stage, 64 lanes each
     constexpr int STAGE_BYTES = A_BYTES + B_WORDS * 256;
-    constexpr int LA = A_UNITS / 64 / NW;       // activation copies per wavefront per stage
-    constexpr int LB = B_WORDS / NW;            // weight copies per wavefront per stage
+    constexpr int LA = A_UNITS / 64 / NI;       // activation copies per issuing wavefront per stage
+    constexpr int LB = B_WORDS / NI;            // weight copies per issuing wavefront per stage
     constexpr int L = LA + LB;
-    static_assert(A_UNITS % (64 * NW) == 0, "activation stage must split evenly over the wavefronts");
-    static_assert(B_WORDS % NW == 0, "weight stage must split evenly over the wavefronts");
+    static_assert(A_UNITS % (64 * NI) == 0, "activation stage must split evenly over the issuing wavefronts");
+    static_assert(B_WORDS % NI == 0, "weight stage must split evenly over the issuing wavefronts");
     static_assert(L * (NS - 1) < 64, "in-flight copies exceed the vmcnt range");
     static_assert(L == SHAPE.copies && STAGE_BYTES == SHAPE.stage_bytes, "host and device stage geometry differ");
     static_assert(NS >= 2, "at least double buffering");
@@ -86,6 +91,8 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
 
     // the wavefront index is uniform; readfirstlane tells the compiler so (wave-derived math then runs on SALU)
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool producer = PW > 0 && wave >= NW;  // wave-uniform
+    const int iw = PW > 0 ? (producer ? wave - NW : 0) : wave;  // index among the issuing waves
     const int wm = wave / WN, wn = wave % WN;
     const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
     const int nquads = (p.J + 3) >> 2;
@@ -106,7 +113,7 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     int a_koff[LA];
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
-        const int u = (i * NW + wave) * 64 + lane;
+        const int u = (i * NI + iw) * 64 + lane;
         const int row = u / CHS, chp = u - row * CHS;
         const int c = row / BM, r = row - c * BM;
         a_koff[i] = (chp ^ swz(r)) * 16;
@@ -125,17 +132,17 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
         if (k0 + SW * KW <= kend) {  // uniform: every unit of the stage is inside [0, kend)
             const int8_t *abase = p.q + k0;
 #pragma unroll
-            for (int i = 0; i < LA; ++i) dma16(abase + a_off[i], buf + (i * NW + wave) * 64 * 16);
+            for (int i = 0; i < LA; ++i) dma16(abase + a_off[i], buf + (i * NI + iw) * 64 * 16);
         } else {
 #pragma unroll
             for (int i = 0; i < LA; ++i) {
                 const uint32_t off = k0 + a_koff[i] < kend ? a_off[i] + (uint32_t)k0 : a_off[i] - (uint32_t)a_koff[i];
-                dma16(p.q + off, buf + (i * NW + wave) * 64 * 16);
+                dma16(p.q + off, buf + (i * NI + iw) * 64 * 16);
             }
         }
 #pragma unroll
         for (int i = 0; i < LB; ++i) {
-            const int b = i * NW + wave;             // wave-uniform
+            const int b = i * NI + iw;               // wave-uniform
             const int tt = b / SW, w = b - tt * SW;
             const int t = tile0 + tt, j = jstage + w;
             // words past the slice or past N are never used (their k are masked, their columns never stored)
@@ -298,6 +305,24 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     };
     static_assert(NS <= 8, "wait_stage covers up to 7 later stages");
 
+    // Producer waves: every copy of the ring, each stage waited for and handed over at the stage barrier; they take
+    // part in exactly the compute waves' barriers (nst of them) and leave before the epilogue.
+    if constexpr (PW > 0) {
+        if (producer) {
+#pragma unroll
+            for (int s = 0; s < NS - 1; ++s)
+                if (s < nst) issue(s);
+            for (int s = 0; s < nst - 1; ++s) {
+                wait_stage(min(NS - 2, nst - 1 - s));
+                stage_barrier();  // stage s is in LDS; the compute waves are done with stage s-1's buffer
+                if (s + NS - 1 < nst) issue(s + NS - 1);
+            }
+            wait_vmcnt<0>();
+            stage_barrier();
+            return;
+        }
+    }
+
     // Epilogue operands are fetched before the ring so their latency overlaps the main loads (the copies below are
     // issued after these loads, so the stage waits never depend on them).
     if constexpr (!SLICED) {
@@ -348,9 +373,11 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     };
     if constexpr (GQ > 0) alpha_load(0);
 
+    if constexpr (PW == 0) {
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s)
-        if (s < nst) issue(s);
+        for (int s = 0; s < NS - 1; ++s)
+            if (s < nst) issue(s);
+    }
 
     if constexpr (GQ > 0) {
         alpha_store(0);
@@ -364,14 +391,18 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     using plain_t = std::integral_constant<bool, false>;
     using masked_t = std::integral_constant<bool, true>;
     for (int s = 0; s < nst - 1; ++s) {
-        const int issued_after = min(NS - 2, nst - 1 - s);  // stages issued after s so far
-        wait_stage(issued_after);
+        if constexpr (PW == 0) {
+            const int issued_after = min(NS - 2, nst - 1 - s);  // stages issued after s so far
+            wait_stage(issued_after);
+        }
         stage_barrier();  // stage s is in LDS for every wavefront; stage s-1's buffer is free
-        if (s + NS - 1 < nst) issue(s + NS - 1);
+        if constexpr (PW == 0) {
+            if (s + NS - 1 < nst) issue(s + NS - 1);
+        }
         compute(s, plain_t{});
     }
     // the last stage (the host never launches an empty K range, so nst >= 1)
-    wait_vmcnt<0>();
+    if constexpr (PW == 0) wait_vmcnt<0>();
     stage_barrier();
     compute(nst - 1, masked_t{});
 
@@ -464,15 +495,15 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(Params p) {
     }
 }
 
-template <int WBITS, int P, int RM, int RN, int WM, int WN>
+template <int WBITS, int P, int RM, int RN, int WM, int WN, int PW>
 KernelFn pick_sliced(bool sliced) {
-    return sliced ? gemm_kernel<WBITS, P, RM, RN, WM, WN, true, false>
-                  : gemm_kernel<WBITS, P, RM, RN, WM, WN, false, false>;
+    return sliced ? gemm_kernel<WBITS, P, RM, RN, WM, WN, true, false, 0, PW>
+                  : gemm_kernel<WBITS, P, RM, RN, WM, WN, false, false, 0, PW>;
 }
 
-template <int WBITS, int P, int RM, int RN, int WM, int WN>
+template <int WBITS, int P, int RM, int RN, int WM, int WN, int PW>
 KernelFn pick_fit(bool sliced) {
-    if constexpr (tile_fits(WBITS, P, RM, RN, WM, WN)) return pick_sliced<WBITS, P, RM, RN, WM, WN>(sliced);
+    if constexpr (tile_fits(WBITS, P, RM, RN, WM, WN, PW)) return pick_sliced<WBITS, P, RM, RN, WM, WN, PW>(sliced);
     else return nullptr;
 }
 
@@ -480,7 +511,7 @@ KernelFn pick_fit(bool sliced) {
 template <int WBITS, int P, int I>
 KernelFn pick_index(bool sliced) {
     constexpr Tile t = kTiles[I];
-    return pick_fit<WBITS, P, t.rm, t.rn, t.wm, t.wn>(sliced);
+    return pick_fit<WBITS, P, t.rm, t.rn, t.wm, t.wn, t.pw>(sliced);
 }
 
 template <int WBITS, int P>

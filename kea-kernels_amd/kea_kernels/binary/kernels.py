@@ -86,3 +86,8 @@ class GemmConfig:
 
 def tile_count() -> int:
     return _hip.lib().kea_config_count()
+
+
+def config_name(tile: int) -> str:
+    """The library's name of tile id `tile` ("" for an unknown id)."""
+    return _hip.lib().kea_config_name(tile).decode()

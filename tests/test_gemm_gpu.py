@@ -192,12 +192,35 @@ def test_every_tile_gives_identical_results(wbits, parts):
     case = Case(wbits, parts, 70, 200, 1152, seed=31 + parts, bias=True)
     ref = None
     for tile in range(1, kernels.tile_count() + 1):
-        y, acc = case.run(config=kernels.GemmConfig(tile=tile, split=1))
+        try:
+            y, acc = case.run(config=kernels.GemmConfig(tile=tile, split=1))
+        except ValueError as e:
+            # the 16-wave producer tile keeps one part's accumulators within a quarter of a SIMD's registers
+            if parts > 1 and "does not fit" in str(e) and kernels.config_name(tile).endswith(" p8"):
+                continue
+            raise
         if ref is None:
             assert_parity(case, y, acc)
             ref = (y, acc)
         assert torch.equal(y.view(torch.int16), ref[0].view(torch.int16)), f"tile {tile}"
         assert np.array_equal(acc, ref[1]), f"tile {tile}"
+
+
+@pytest.mark.parametrize("wbits", [1, 2])
+@pytest.mark.parametrize("m,n,k", [(70, 200, 1152), (1000, 512, 256), (257, 4096, 4096), (130, 384, 2048)])
+@torch.inference_mode()
+def test_producer_wave_tiles_equal_their_compute_tiles(wbits, m, n, k):
+    """Tiles 6 and 7 are tiles 11 and 8 with waves that only issue the ring's copies: same bits, unsplit and split
+    (split-K slices and the masked last stage pass through the producer hand-over too)."""
+    assert kernels.config_name(6).endswith(" p8") and kernels.config_name(7).endswith(" p4")
+    case = Case(wbits, 1, m, n, k, seed=m + n + k, bias=True)
+    for producer, compute in ((6, 11), (7, 8)):
+        want_y, want_acc = case.run(config=kernels.GemmConfig(tile=compute, split=1))
+        for split in (1, 2, 3):
+            y, acc = case.run(config=kernels.GemmConfig(tile=producer, split=split))
+            assert torch.equal(y.view(torch.int16), want_y.view(torch.int16)), (producer, split)
+            assert np.array_equal(acc, want_acc), (producer, split)
+    assert_parity(case, want_y, want_acc)
 
 
 def _at_odd_offset(t: torch.Tensor) -> torch.Tensor:
