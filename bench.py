@@ -190,11 +190,11 @@ def cold_bench(d, stream, launches: int = 1300) -> float:
     return us
 
 
-def launch_floors(d, stream, tile_name: str, reps: int = 10, shape=(M, N, K)) -> dict:
+def launch_floors(d, stream, tile_name: str, reps: int = 10, shape=(M, N, K), waves: int = 4) -> dict:
     """Per-launch microseconds of the launch-floor probes (include/kea_probe.h) on the GEMM's own grid: one
-    workgroup per BM x BN tile of the chosen configuration, doing nothing, only loading its tile's operand bytes,
-    only storing its fp16 outputs, or both; graphs of 100 launches, timed as the GEMM is. d holds the shape's q
-    (int8 [m][k]), native 1-bit words and fp16 y."""
+    workgroup of `waves` waves per BM x BN tile of the chosen configuration, doing nothing, only loading its tile's
+    operand bytes, only storing its fp16 outputs, or both; graphs of 100 launches, timed as the GEMM is. d holds the
+    shape's q (int8 [m][k]), native 1-bit words and fp16 y."""
     import ctypes
     import torch
     from kea_kernels import _hip
@@ -203,11 +203,12 @@ def launch_floors(d, stream, tile_name: str, reps: int = 10, shape=(M, N, K)) ->
     bm, bn = (int(v) for v in tile_name.split()[0].split("x"))
     vp = ctypes.c_void_p
     y = torch.empty_like(d["y"])  # the probes' stores must not touch the GEMM's output (checked later)
-    out = {"tile": f"{bm}x{bn}", "workgroups": (m // bm) * (n // bn)}
+    out = {"tile": f"{bm}x{bn}", "workgroups": (m // bm) * (n // bn), "waves": waves}
     for kind, name in enumerate(("empty_us", "loads_us", "stores_us", "loads_stores_us")):
         def probe(i, kind=kind):
-            rc = L.kea_probe_floor(kind, m, n, k, bm, bn, vp(d["q"].data_ptr()), vp(d["words"].data_ptr()),
-                                   vp(y.data_ptr()), n, vp(torch.cuda.current_stream().cuda_stream))
+            rc = L.kea_probe_floor_waves(kind, m, n, k, bm, bn, waves, vp(d["q"].data_ptr()),
+                                         vp(d["words"].data_ptr()), vp(y.data_ptr()), n,
+                                         vp(torch.cuda.current_stream().cuda_stream))
             _hip.check(rc, "kea_probe_floor")
         graph = capture(stream, probe, 100)
         replay_timed(stream, [graph])
@@ -224,7 +225,8 @@ def probes() -> None:
       (kea_probe_exchange: writes only, + a relaxed arrival count, + an acquire-release count and the read), graphs of
       100 launches, at the group sizes an in-launch split-K (4) and a whole-grid exchange need;
     * config3_floors: the launch floors of config 3's grid (M = 1024 so the 128x128 tile divides it; N = 4096,
-      K = 1024) next to the GEMM on that grid with tile 11 (128x128)."""
+      K = 1024) with 4, 8 and 16 waves per workgroup, next to the GEMM on that grid with tile 11 (128x128, 8 waves)
+      and tile 6 (the same compute waves and 8 producer waves, 16 in all)."""
     import ctypes
     import torch
     from kea_kernels import _hip, lowbit
@@ -294,13 +296,17 @@ def probes() -> None:
     words = kernels.relayout_codes(codes, k, 1).to(dev)
     alpha = (torch.rand(n, generator=g) * 0.09 + 0.01).half().to(dev)
     y = torch.empty(m, n, dtype=torch.float16, device=dev)
-    row = {"probe": "config3_floors", "M": m, "N": n, "K": k}
-    row.update(launch_floors({"q": q, "words": words, "y": y}, stream, "128x128", shape=(m, n, k)))
-    gemm = capture(stream, lambda i: lowbit.gemm(1, q, qs, words, n, k, alpha, None, y, None,
-                                                 config=GemmConfig(11, 1)), 100)
-    replay_timed(stream, [gemm])
-    row["gemm_tile11_us"] = round(replay_timed(stream, [gemm], 10) * 1000 / 1000, 3)
-    print(json.dumps(row), flush=True)
+    gemm_us = {}
+    for tile in (11, 6):
+        gemm = capture(stream, lambda i, tile=tile: lowbit.gemm(1, q, qs, words, n, k, alpha, None, y, None,
+                                                                config=GemmConfig(tile, 1)), 100)
+        replay_timed(stream, [gemm])
+        gemm_us[tile] = round(replay_timed(stream, [gemm], 10) * 1000 / 1000, 3)
+    for waves in (4, 8, 16):
+        row = {"probe": "config3_floors", "M": m, "N": n, "K": k}
+        row.update(launch_floors({"q": q, "words": words, "y": y}, stream, "128x128", shape=(m, n, k), waves=waves))
+        row["gemm_tile11_us"], row["gemm_tile6_us"] = gemm_us[11], gemm_us[6]
+        print(json.dumps(row), flush=True)
 
 
 def measured_peaks(reps: int = 5) -> dict:
@@ -740,7 +746,8 @@ def main(argv=None) -> int:
                         "method": "every launch reads its own copy of q and the weight words, cycling through "
                                   ">= 768 MiB of copies (3x the last-level cache); HIP-graph replay"}
     if not args.no_floors:
-        floors = launch_floors(d, stream, _hip_config_name(cfg.tile))
+        name = _hip_config_name(cfg.tile)
+        floors = launch_floors(d, stream, name, waves=_config_waves(name))
         floors["gemm_us"] = round(ms_per_step * 1e3, 3)
         line["floors"] = floors
     if not args.no_peaks:
@@ -773,6 +780,18 @@ def main(argv=None) -> int:
 def _hip_config_name(tile: int) -> str:
     from kea_kernels import _hip
     return _hip.lib().kea_config_name(tile).decode()
+
+
+def _config_waves(name: str) -> int:
+    """Waves per workgroup of a tile from its name: "16x64 k/4" (wave-split: K over 4 waves) or
+    "128x128 w2x4 r4x2" (LDS ring: 2 x 4 waves)."""
+    for field in name.split()[1:]:
+        if field.startswith("k/"):
+            return int(field[2:])
+        if field.startswith("w"):
+            a, b = field[1:].split("x")
+            return int(a) * int(b)
+    raise ValueError(f"no wave count in tile name {name!r}")
 
 
 if __name__ == "__main__":

@@ -50,7 +50,7 @@ int kea_probe_spin(int64_t ns, void *stream);
 int kea_probe_exchange(int kind, int64_t workgroups, int64_t words, int64_t group, void *slots, uint32_t *counters,
                        uint32_t *result, void *stream);
 
-/* Launch floors of a GEMM-shaped grid: (n / bn) x (m / bm) workgroups of 256 threads, one per bm x bn output tile of
+/* Launch floors of a GEMM-shaped grid: (n / bn) x (m / bm) workgroups of four wave64s, one per bm x bn output tile of
  * an m x n x k low-bit GEMM, as kea_lowbit_gemm launches them. What each workgroup does:
  *   KEA_PROBE_EMPTY    nothing (the dispatch and completion cost of the grid);
  *   KEA_PROBE_LOADS    copies its tile's operand bytes into LDS - the bm activation rows of a (int8 [m][k], bm * k
@@ -66,6 +66,11 @@ int kea_probe_exchange(int kind, int64_t workgroups, int64_t words, int64_t grou
 #define KEA_PROBE_STORES 2
 int kea_probe_floor(int kind, int64_t m, int64_t n, int64_t k, int bm, int bn, const int8_t *a, const uint32_t *w,
                     uint16_t *y, int64_t ldy, void *stream);
+
+/* kea_probe_floor with `waves` wave64s per workgroup (in [1, 16]; kea_probe_floor uses 4). A workgroup's copies into
+ * LDS go faster when more of its waves issue them, so a GEMM tile's floor is measured at the tile's own wave count. */
+int kea_probe_floor_waves(int kind, int64_t m, int64_t n, int64_t k, int bm, int bn, int waves, const int8_t *a,
+                          const uint32_t *w, uint16_t *y, int64_t ldy, void *stream);
 
 #ifdef __cplusplus
 }

@@ -64,7 +64,7 @@ typedef __attribute__((address_space(1))) const void *gptr_t;
 typedef __attribute__((address_space(3))) void *lptr_t;
 
 template <int KIND>
-__global__ void __launch_bounds__(256) floor_kernel(FloorArgs f) {
+__global__ void __launch_bounds__(1024) floor_kernel(FloorArgs f) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     if constexpr (KIND == KEA_PROBE_EMPTY) {
         return;
@@ -76,7 +76,7 @@ __global__ void __launch_bounds__(256) floor_kernel(FloorArgs f) {
             const int8_t *abase = f.a + (long long)m0 * f.k;
             const uint8_t *wbase = f.w + (long long)n0 * (f.k / 8);
             // unit u of the tile: activation units first, then weight units; a wave's 64 lanes fill 1 KiB of LDS
-            for (int base = wave * 64; base < f.a_units + f.w_units; base += 256) {
+            for (int base = wave * 64; base < f.a_units + f.w_units; base += (int)blockDim.x) {
                 const int u = base + lane;
                 if (u < f.a_units) {
                     const int r = u / row_units, c = u - r * row_units;
@@ -93,7 +93,7 @@ __global__ void __launch_bounds__(256) floor_kernel(FloorArgs f) {
         if constexpr (KIND & KEA_PROBE_STORES) {
             const int groups = f.bn / 4, total = f.bm * groups;
             const int lds_words = (f.a_units + f.w_units) * 2;  // 8-byte words in LDS (data kinds with loads)
-            for (int g = threadIdx.x; g < total; g += 256) {
+            for (int g = threadIdx.x; g < total; g += (int)blockDim.x) {
                 const int r = g / groups, c = (g - r * groups) * 4;
                 uint2 v = make_uint2(0u, 0u);
                 if constexpr (KIND & KEA_PROBE_LOADS) v = ((const uint2 *)lds)[g % lds_words];
@@ -211,6 +211,12 @@ int kea_probe_exchange(int kind, int64_t workgroups, int64_t words, int64_t grou
 
 int kea_probe_floor(int kind, int64_t m, int64_t n, int64_t k, int bm, int bn, const int8_t *a, const uint32_t *w,
                     uint16_t *y, int64_t ldy, void *stream) {
+    return kea_probe_floor_waves(kind, m, n, k, bm, bn, 4, a, w, y, ldy, stream);
+}
+
+int kea_probe_floor_waves(int kind, int64_t m, int64_t n, int64_t k, int bm, int bn, int waves, const int8_t *a,
+                          const uint32_t *w, uint16_t *y, int64_t ldy, void *stream) {
+    if (waves < 1 || waves > 16) return kea::fail(KEA_EINVAL, "kea_probe_floor: waves must be in [1, 16]");
     if (kind < KEA_PROBE_EMPTY || kind > (KEA_PROBE_LOADS | KEA_PROBE_STORES))
         return kea::fail(KEA_EINVAL, "kea_probe_floor: kind must be 0 (empty), 1 (loads), 2 (stores) or 3 (both)");
     if (bm < 16 || bm > 256 || bm % 16 || bn < 16 || bn > 256 || bn % 16)
@@ -236,7 +242,7 @@ int kea_probe_floor(int kind, int64_t m, int64_t n, int64_t k, int bm, int bn, c
         hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_floor: ") + hipGetErrorString(e));
     }
-    hipLaunchKernelGGL(fn, grid, dim3(256), (size_t)lds, st, f);
+    hipLaunchKernelGGL(fn, grid, dim3((unsigned)waves * 64), (size_t)lds, st, f);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_floor: ") + hipGetErrorString(e));
     return 0;

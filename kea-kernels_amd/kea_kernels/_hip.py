@@ -88,6 +88,7 @@ SIGNATURES = {
     "kea_probe_mfma_i8_operands": (_i32, [_i64, _i64, _vp, _vp, _vp]),
     "kea_probe_exchange": (_i32, [_i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "kea_probe_floor": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _i64, _vp]),
+    "kea_probe_floor_waves": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _vp]),
     "kea_probe_spin": (_i32, [_i64, _vp]),
     "kea_last_error": (_cp, []),
     "kea_version": (_i32, []),

@@ -37,6 +37,9 @@ def test_floor_and_spin_probe_arguments():
     assert L.kea_probe_floor(1, 256, 256, 65536, 256, 256, vp(16), vp(16), None, 256, None) == -1  # LDS
     assert b"LDS" in L.kea_last_error()
     assert L.kea_probe_spin(-1, None) == -1 and L.kea_probe_spin(100000001, None) == -1
+    assert L.kea_probe_floor_waves(0, 128, 4096, 1024, 32, 32, 0, None, None, None, 4096, None) == -1  # waves
+    assert L.kea_probe_floor_waves(0, 128, 4096, 1024, 32, 32, 17, None, None, None, 4096, None) == -1
+    assert b"waves" in L.kea_last_error()
 
 
 def test_operand_and_exchange_probe_arguments():
