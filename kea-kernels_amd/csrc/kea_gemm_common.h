@@ -204,6 +204,9 @@ __device__ __forceinline__ void load_col_scales(const Params &p, int nb, EpiOper
     }
 }
 
+// The GLU of a column pair (value, gate): value * sigmoid(gate), the one expression every epilogue uses.
+__device__ __forceinline__ float glu_pair(float value, float gate) { return value * (1.0f / (1.0f + expf(-gate))); }
+
 // The epilogue of 4 consecutive columns nb..nb+3 of row m from exact accumulators a[c][r].
 template <int P>
 __device__ __forceinline__ void epilogue4(const Params &p, int m, int nb, const int (*a)[4], const EpiOperands &e) {
@@ -216,7 +219,7 @@ __device__ __forceinline__ void epilogue4(const Params &p, int m, int nb, const 
             if (p.res) v[r] = e.res[r] + v[r] * p.res_factor;
         }
         if (p.flags & KEA_FLAG_GLU) {  // column pairs (value, gate): value * sigmoid(gate)
-            const float u[2] = {v[0] * (1.0f / (1.0f + expf(-v[1]))), v[2] * (1.0f / (1.0f + expf(-v[3])))};
+            const float u[2] = {glu_pair(v[0], v[1]), glu_pair(v[2], v[3])};
             store2(p, (long long)m * p.ldy + nb / 2, nb, u);
         } else {
             store4(p, (long long)m * p.ldy + nb, nb, v);
@@ -229,14 +232,15 @@ __device__ __forceinline__ void epilogue4(const Params &p, int m, int nb, const 
     }
 }
 
-// epilogue4 for a plain output (no GLU pairs, no raw accumulators) of compile-time dtype DT whose 4 columns are all
-// inside N with a vector-aligned y: the same values, one vector store at yrow + nb (yrow: the row's first element),
-// no per-lane selection. RES: the residual is applied (Params::res is set). SILU: 1 / 0 the SiLU is / is not applied
-// (known at compile time: a run-time flag makes the compiler evaluate the SiLU for every output and select), -1: as
-// Params::flags says.
-template <int P, int DT, bool RES, bool SMALL, int SILU = -1>
+// epilogue4 for an output without raw accumulators, of compile-time dtype DT, whose 4 columns are all inside N with a
+// vector-aligned y: the same values, one vector store at yrow + nb (yrow: the row's first element), no per-lane
+// selection. RES: the residual is applied (Params::res is set). SILU: 1 / 0 the SiLU is / is not applied (known at
+// compile time: a run-time flag makes the compiler evaluate the SiLU for every output and select), -1: as
+// Params::flags says. GLU: the two column pairs become two outputs at yrow + nb / 2 (no residual, no SiLU).
+template <int P, int DT, bool RES, bool SMALL, int SILU = -1, bool GLU = false>
 __device__ __forceinline__ void epilogue4_full(const Params &p, void *yrow, int nb, const int (*a)[4],
                                                const EpiOperands &e) {
+    static_assert(!GLU || (!RES && SILU == 0), "the GLU output takes neither a residual nor the SiLU");
     const int flags = SILU < 0 ? p.flags : SILU ? (p.flags | KEA_FLAG_SILU) : (p.flags & ~KEA_FLAG_SILU);
     float v[4];
 #pragma unroll
@@ -250,7 +254,16 @@ __device__ __forceinline__ void epilogue4_full(const Params &p, void *yrow, int 
             if constexpr (RES) v[r] = e.res[r] + v[r] * p.res_factor;
         }
     }
-    if constexpr (DT == KEA_F32) {
+    if constexpr (GLU) {
+        const float u0 = glu_pair(v[0], v[1]), u1 = glu_pair(v[2], v[3]);
+        if constexpr (DT == KEA_F32) {
+            *(float2 *)((float *)yrow + nb / 2) = make_float2(u0, u1);
+        } else {
+            const uint32_t h0 = DT == KEA_F16 ? to_f16_bits(u0) : to_bf16_bits(u0);
+            const uint32_t h1 = DT == KEA_F16 ? to_f16_bits(u1) : to_bf16_bits(u1);
+            *(uint32_t *)((uint16_t *)yrow + nb / 2) = h0 | (h1 << 16);
+        }
+    } else if constexpr (DT == KEA_F32) {
         *(float4 *)((float *)yrow + nb) = make_float4(v[0], v[1], v[2], v[3]);
     } else {
         uint16_t h[4];

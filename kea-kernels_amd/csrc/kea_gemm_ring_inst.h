@@ -410,15 +410,16 @@ __global__ void __launch_bounds__((WM * WN + PW) * 64) gemm_kernel(Params p) {
     // DT >= 0: the output dtype as a compile-time constant; then 16x16 tiles wholly inside [M, N) take a path without
     // per-lane bounds or dtype selection (the tile test is wave-uniform). DT < 0: the general epilogue.
     constexpr bool SMALL = RM * RN <= 2;
-    auto epilogue = [&](auto dt_tag, auto res_tag, auto silu_tag) {
+    auto epilogue = [&](auto dt_tag, auto res_tag, auto silu_tag, auto glu_tag) {
         constexpr int DT = decltype(dt_tag)::value;
         constexpr bool RES = decltype(res_tag)::value;
         constexpr int SILU = decltype(silu_tag)::value;
+        constexpr bool GLU = decltype(glu_tag)::value;
 #pragma unroll
         for (int i = 0; i < RM; ++i) {
             const int mt = m0 + (wm * RM + i) * 16, m = mt + (lane & 15);
             if (m >= p.M) continue;
-            void *yrow = (int8_t *)p.y + (long long)m * p.ldy * (DT == KEA_F32 ? 4 : 2);
+            void *yrow = (int8_t *)p.y + (long long)m * p.ldy * (DT == KEA_F32 ? 4 : 2);  // unused when DT < 0
 #pragma unroll
             for (int jn = 0; jn < RN; ++jn) {
                 const int nt = n0 + (wn * RN + jn) * 16, nb = nt + (lane >> 4) * 4;
@@ -447,7 +448,7 @@ __global__ void __launch_bounds__((WM * WN + PW) * 64) gemm_kernel(Params p) {
                         epilogue4_groups<P>(p, m, nb, a, racc[i][jn], e);
                     } else if constexpr (DT >= 0) {
                         if (mt + 16 <= p.M && nt + 16 <= p.N) {
-                            epilogue4_full<P, DT, RES, SMALL, SILU>(p, yrow, nb, a, e);
+                            epilogue4_full<P, DT, RES, SMALL, SILU, GLU>(p, yrow, nb, a, e);
                             continue;
                         }
                         epilogue4<P>(p, m, nb, a, e);
@@ -458,18 +459,31 @@ __global__ void __launch_bounds__((WM * WN + PW) * 64) gemm_kernel(Params p) {
             }
         }
     };
-    // plain outputs (no GLU pairs, no raw accumulators, vector-aligned y) branch once on the dtype
-    const bool plain = !SLICED && GQ == 0 && p.y && !p.acc && !(p.flags & KEA_FLAG_GLU) && p.y_vec;
+    // Outputs without raw accumulators and with a vector-aligned y branch once on the dtype (and GLU outputs, which
+    // take neither residual nor SiLU, on the GLU); the rest take the general epilogue.
+    const bool glu = (p.flags & KEA_FLAG_GLU) != 0;
+    const bool plain = !SLICED && GQ == 0 && p.y && !p.acc && p.y_vec && !glu;
+    const bool plain_glu = !SLICED && GQ == 0 && p.y && !p.acc && p.y_vec && glu && !p.res;
     using kRes = std::true_type;
     using kNoRes = std::false_type;
+    using kGlu = std::true_type;
+    using kNoGlu = std::false_type;
     using kSiluAtRunTime = std::integral_constant<int, -1>;
+    using kNoSilu = std::integral_constant<int, 0>;
+    using kGeneral = std::integral_constant<int, -1>;
+    if (plain_glu) {
+        if (p.y_dtype == KEA_F32) epilogue(std::integral_constant<int, KEA_F32>{}, kNoRes{}, kNoSilu{}, kGlu{});
+        else if (p.y_dtype == KEA_F16) epilogue(std::integral_constant<int, KEA_F16>{}, kNoRes{}, kNoSilu{}, kGlu{});
+        else epilogue(std::integral_constant<int, KEA_BF16>{}, kNoRes{}, kNoSilu{}, kGlu{});
+        return;
+    }
     // Tiles of one or two 16x16 blocks per wave (the small-M shapes) keep one epilogue copy per dtype with the
     // residual, bias and SiLU tested at run time: separate copies measured slower there (config 1: 4.13 vs 4.27 us).
     if constexpr (SMALL) {
-        if (plain && p.y_dtype == KEA_F16) epilogue(std::integral_constant<int, KEA_F16>{}, kNoRes{}, kSiluAtRunTime{});
-        else if (plain && p.y_dtype == KEA_BF16) epilogue(std::integral_constant<int, KEA_BF16>{}, kNoRes{}, kSiluAtRunTime{});
-        else if (plain && p.y_dtype == KEA_F32) epilogue(std::integral_constant<int, KEA_F32>{}, kNoRes{}, kSiluAtRunTime{});
-        else epilogue(std::integral_constant<int, -1>{}, kNoRes{}, kSiluAtRunTime{});
+        if (plain && p.y_dtype == KEA_F16) epilogue(std::integral_constant<int, KEA_F16>{}, kNoRes{}, kSiluAtRunTime{}, kNoGlu{});
+        else if (plain && p.y_dtype == KEA_BF16) epilogue(std::integral_constant<int, KEA_BF16>{}, kNoRes{}, kSiluAtRunTime{}, kNoGlu{});
+        else if (plain && p.y_dtype == KEA_F32) epilogue(std::integral_constant<int, KEA_F32>{}, kNoRes{}, kSiluAtRunTime{}, kNoGlu{});
+        else epilogue(kGeneral{}, kNoRes{}, kSiluAtRunTime{}, kNoGlu{});
         return;
     }
     // Wider tiles: one copy per dtype, residual and SiLU, so the full-block path carries neither test nor a SiLU
@@ -477,11 +491,11 @@ __global__ void __launch_bounds__((WM * WN + PW) * 64) gemm_kernel(Params p) {
     auto by_flags = [&](auto dt_tag) {
         const bool silu = (p.flags & KEA_FLAG_SILU) != 0;
         if (p.res) {
-            if (silu) epilogue(dt_tag, kRes{}, std::integral_constant<int, 1>{});
-            else epilogue(dt_tag, kRes{}, std::integral_constant<int, 0>{});
+            if (silu) epilogue(dt_tag, kRes{}, std::integral_constant<int, 1>{}, kNoGlu{});
+            else epilogue(dt_tag, kRes{}, kNoSilu{}, kNoGlu{});
         } else {
-            if (silu) epilogue(dt_tag, kNoRes{}, std::integral_constant<int, 1>{});
-            else epilogue(dt_tag, kNoRes{}, std::integral_constant<int, 0>{});
+            if (silu) epilogue(dt_tag, kNoRes{}, std::integral_constant<int, 1>{}, kNoGlu{});
+            else epilogue(dt_tag, kNoRes{}, kNoSilu{}, kNoGlu{});
         }
     };
     if (plain && p.y_dtype == KEA_F16) {
@@ -491,7 +505,7 @@ __global__ void __launch_bounds__((WM * WN + PW) * 64) gemm_kernel(Params p) {
     } else if (plain && p.y_dtype == KEA_F32) {
         by_flags(std::integral_constant<int, KEA_F32>{});
     } else {
-        epilogue(std::integral_constant<int, -1>{}, kNoRes{}, kSiluAtRunTime{});
+        epilogue(kGeneral{}, kNoRes{}, kSiluAtRunTime{}, kNoGlu{});
     }
 }
 

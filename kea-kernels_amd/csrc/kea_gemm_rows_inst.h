@@ -225,7 +225,7 @@ __global__ void __launch_bounds__(NW * 64) rows_kernel(const float *x, const uin
     wsplit_mfma<WBITS, P, 1, NT, S, WPW>(wv, af, acc);
     wsplit_share<P, 1, NT>(red + wave * PART, lane, acc);
     __syncthreads();
-    const bool plain = p.y && !p.acc && !p.res && !(p.flags & KEA_FLAG_GLU) && p.y_vec;
+    const bool plain = p.y && !p.acc && !p.res && p.y_vec;
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
         const int jn = wave + NW * u;

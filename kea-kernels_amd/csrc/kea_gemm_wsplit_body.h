@@ -123,9 +123,9 @@ __device__ __forceinline__ void wsplit_block_sum(const int32_t *red, int i, int 
 }
 
 // The epilogue of row m, columns nb .. nb + 3 of the block at (mt, nt) of an M x N output: for a whole block of a
-// plain output (`plain`: no residual, GLU pairs or raw accumulators; e.bias holds kNoBias without a bias) one vector
-// store, from a copy specialised on the dtype and the SiLU flag, so no SiLU or residual is evaluated only to be
-// discarded; else the general epilogue.
+// plain output (`plain`: no residual or raw accumulators; e.bias holds kNoBias without a bias) one vector store, from
+// a copy specialised on the dtype and on the SiLU flag or the GLU pairs, so no SiLU or residual is evaluated only to
+// be discarded; else the general epilogue.
 template <int P>
 __device__ __forceinline__ void wsplit_epilogue(const Params &p, bool plain, int M, int N, int m, int mt, int nt,
                                                 int nb, const int (&a)[P][4], const EpiOperands &e) {
@@ -133,7 +133,11 @@ __device__ __forceinline__ void wsplit_epilogue(const Params &p, bool plain, int
         const bool silu = (p.flags & KEA_FLAG_SILU) != 0;
         uint16_t *y16 = (uint16_t *)p.y + (long long)m * p.ldy;
         float *y32 = (float *)p.y + (long long)m * p.ldy;
-        if (p.y_dtype == KEA_F16) {
+        if (p.flags & KEA_FLAG_GLU) {  // the library refuses GLU with the SiLU
+            if (p.y_dtype == KEA_F16) epilogue4_full<P, KEA_F16, false, false, 0, true>(p, y16, nb, a, e);
+            else if (p.y_dtype == KEA_BF16) epilogue4_full<P, KEA_BF16, false, false, 0, true>(p, y16, nb, a, e);
+            else epilogue4_full<P, KEA_F32, false, false, 0, true>(p, y32, nb, a, e);
+        } else if (p.y_dtype == KEA_F16) {
             if (silu) epilogue4_full<P, KEA_F16, false, false, 1>(p, y16, nb, a, e);
             else epilogue4_full<P, KEA_F16, false, false, 0>(p, y16, nb, a, e);
         } else if (p.y_dtype == KEA_BF16) {

@@ -149,7 +149,7 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
     __syncthreads();
 
     // ---- epilogue: block b = wave + NW * u of the tile ----
-    const bool plain = !SLICED && p.y && !p.acc && !p.res && !(p.flags & KEA_FLAG_GLU) && p.y_vec;
+    const bool plain = !SLICED && p.y && !p.acc && !p.res && p.y_vec;
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
         const int b = wave + NW * u;

@@ -223,6 +223,36 @@ def test_producer_wave_tiles_equal_their_compute_tiles(wbits, m, n, k):
     assert_parity(case, want_y, want_acc)
 
 
+@pytest.mark.parametrize("wbits,parts", [(1, 1), (2, 2)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
+@torch.inference_mode()
+def test_glu_fast_epilogue_equals_the_general_one_on_every_tile(wbits, parts, out_dtype):
+    """GLU outputs of whole blocks take a compile-time epilogue when y rows are vector-aligned; an odd row stride
+    sends every block through the general epilogue. Both must give the same bits, on every tile (partial row and
+    column blocks included: M = 70, 200 output pairs)."""
+    case = Case(wbits, parts, 70, 400, 1152, seed=90 + parts, bias=True)
+    want = None
+    for tile in range(1, kernels.tile_count() + 1):
+        outs = []
+        for ldy in (200, 201):
+            y = torch.full((70, ldy), float("nan"), device=DEV, dtype=out_dtype)
+            try:
+                lowbit.gemm(wbits, case.dq, case.dqs, case.words, 400, 1152, case.dalpha, case.dbias, y, None,
+                            glu=True, config=kernels.GemmConfig(tile=tile, split=1))
+            except ValueError as e:
+                if parts > 1 and "does not fit" in str(e) and kernels.config_name(tile).endswith(" p8"):
+                    break
+                raise
+            torch.cuda.synchronize()
+            outs.append(y[:, :200].contiguous().view(torch.int16 if out_dtype != torch.float32 else torch.int32))
+        if not outs:
+            continue
+        assert torch.equal(outs[0], outs[1]), f"tile {tile}: fast and general GLU epilogues differ"
+        if want is None:
+            want = outs[0]
+        assert torch.equal(outs[0], want), f"tile {tile}"
+
+
 def _at_odd_offset(t: torch.Tensor) -> torch.Tensor:
     """A copy of contiguous t whose storage starts one element past an aligned address (2-byte aligned f16)."""
     buf = torch.zeros(t.numel() + 1, dtype=t.dtype, device=DEV)
