@@ -113,6 +113,20 @@ int kea_logmel_normalize(const float *spec_dev, int64_t batch, int64_t bins, int
                          const float *fb_dev, const int32_t *lo_dev, const int32_t *hi_dev, int64_t mels, float log_eps,
                          float std_eps, float *y_dev, void *stream);
 
+/* kea_logmel_normalize on a frame-major spectrum: spec interleaved complex [batch][ld_f][bins] (ld_f >= frames), as a
+ * real FFT along the last dimension of kea_stft_frames' output leaves it. */
+int kea_logmel_normalize_frames(const float *spec_dev, int64_t batch, int64_t bins, int64_t frames, int64_t ld_f,
+                                const float *fb_dev, const int32_t *lo_dev, const int32_t *hi_dev, int64_t mels,
+                                float log_eps, float std_eps, float *y_dev, void *stream);
+
+/* The frames torch.stft transforms for center = True, pad_mode "constant", with NeMo's pre-emphasis applied first:
+ * audio [batch][samples] -> frames [batch][1 + samples / hop][n_fft],
+ *   frames[b][f][j] = window[j] * x[b][f * hop + j - n_fft / 2],
+ *   x[b][0] = audio[b][0], x[b][i] = audio[b][i] - preemph * audio[b][i - 1], zero outside [0, samples),
+ * window [n_fft] (the analysis window zero-padded to n_fft, as torch.stft pads it). Even n_fft <= 65536. */
+int kea_stft_frames(const float *audio_dev, int64_t batch, int64_t samples, float preemph, const float *window_dev,
+                    int64_t n_fft, int64_t hop, float *frames_dev, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -539,17 +539,43 @@ bias_relu_flatten_kernel(const float *x, const float *bias, float *y, int C, int
     y[idx] = fmaxf(x[((b * C + c) * H + t) * W + f] + bias[c], 0.f);
 }
 
+// STFT frames as torch.stft builds them for center = True, pad_mode "constant": frame f of clip b is the window times
+// the pre-emphasised audio from f * hop - n_fft / 2, zero outside the clip. One thread per frame element; the
+// pre-emphasis is the same two roundings (product, then difference) as a[i] - preemph * a[i-1] in FP32.
+__global__ void __launch_bounds__(256)
+stft_frames_kernel(const float *audio, long long samples, float preemph, const float *window, int n_fft, int hop,
+                   long long frames, float *out) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long per_clip = frames * n_fft;
+    const long long b = blockIdx.y;
+    if (idx >= per_clip) return;
+    const long long f = idx / n_fft;
+    const int j = (int)(idx - f * n_fft);
+    const long long i = f * hop + j - n_fft / 2;
+    const float *a = audio + b * samples;
+    float x = 0.f;
+    if (i == 0) {
+        x = a[0];
+    } else if (i > 0 && i < samples) {
+        const float prev = preemph * a[i - 1];
+        x = a[i] - prev;
+    }
+    out[b * per_clip + idx] = window[j] * x;
+}
+
 // Log-mel features with per-feature normalisation over time, one workgroup per (clip, mel bin):
 //   v[t] = log(sum_{k in [lo, hi)} fb[m][k] * (re^2 + im^2)[k][t] + log_eps)       (the filter's nonzero bins only)
 //   y[t] = (v[t] - mean) / (std + std_eps),  mean over the frames, std with the n - 1 divisor
-// spec: interleaved complex [B][bins][ld_t]; y: [B][mels][frames]. Thread th owns frames th, th + 256, ...: it writes
-// v, re-reads its own elements for the variance and the normalisation (no barrier between those passes).
+// spec: interleaved complex, element (bin k, frame t) of clip b at b * bstride + k * kstride + t * tstride (bin-major
+// [B][bins][ld_t] or frame-major [B][ld_f][bins]); y: [B][mels][frames]. Thread th owns frames th, th + 256, ...: it
+// writes v, re-reads its own elements for the variance and the normalisation (no barrier between those passes).
 __global__ void __launch_bounds__(256)
-logmel_normalize_kernel(const float2 *spec, int bins, int frames, long long ld_t, const float *fb, const int *lo,
-                        const int *hi, int mels, float log_eps, float std_eps, float *y) {
+logmel_normalize_kernel(const float2 *spec, int bins, int frames, long long kstride, long long tstride,
+                        long long bstride, const float *fb, const int *lo, const int *hi, int mels, float log_eps,
+                        float std_eps, float *y) {
     __shared__ float red[2][4];
     const int m = blockIdx.x, b = blockIdx.y, th = threadIdx.x, wave = th >> 6;
-    const float2 *sb = spec + (long long)b * bins * ld_t;
+    const float2 *sb = spec + (long long)b * bstride;
     float *yr = y + ((long long)b * mels + m) * frames;
     const int k0 = lo[m], k1 = hi[m];
     float sum = 0.f;
@@ -563,7 +589,7 @@ logmel_normalize_kernel(const float2 *spec, int bins, int frames, long long ld_t
                 for (int i = 0; i < 4; ++i) {
                     const int t = t0 + th + 256 * i;
                     c[kk][i] = make_float2(0.f, 0.f);
-                    if (k + kk < k1 && t < frames) c[kk][i] = sb[(long long)(k + kk) * ld_t + t];
+                    if (k + kk < k1 && t < frames) c[kk][i] = sb[(long long)(k + kk) * kstride + t * tstride];
                 }
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
@@ -784,20 +810,56 @@ int kea_bias_relu_flatten(const float *x, const float *bias, float *y, int64_t b
     return KEA_OK;
 }
 
+namespace {
+int logmel_launch(const float *spec, int64_t batch, int64_t bins, int64_t frames, int64_t kstride, int64_t tstride,
+                  int64_t bstride, const float *fb, const int32_t *lo, const int32_t *hi, int64_t mels, float log_eps,
+                  float std_eps, float *y, void *stream) {
+    if (batch == 0) return KEA_OK;
+    if (!spec || !fb || !lo || !hi || !y) return kea::fail(KEA_EINVAL, "null pointer");
+    if ((uintptr_t)spec & 7) return kea::fail(KEA_EALIGN, "spec must be 8-byte aligned (interleaved complex)");
+    hipLaunchKernelGGL(logmel_normalize_kernel, dim3((unsigned)mels, (unsigned)batch), dim3(256), 0,
+                       (hipStream_t)stream, (const float2 *)spec, (int)bins, (int)frames, (long long)kstride,
+                       (long long)tstride, (long long)bstride, fb, lo, hi, (int)mels, log_eps, std_eps, y);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("logmel launch failed: ") + hipGetErrorString(e));
+    return KEA_OK;
+}
+}  // namespace
+
 int kea_logmel_normalize(const float *spec, int64_t batch, int64_t bins, int64_t frames, int64_t ld_t,
                          const float *fb, const int32_t *lo, const int32_t *hi, int64_t mels, float log_eps,
                          float std_eps, float *y, void *stream) {
     if (batch < 0 || batch > 65535 || bins < 1 || frames < 1 || ld_t < frames || mels < 1 || mels > 65535 ||
         bins * ld_t > ((int64_t)1 << 40))
         return kea::fail(KEA_EINVAL, "bad sizes");
+    return logmel_launch(spec, batch, bins, frames, ld_t, 1, bins * ld_t, fb, lo, hi, mels, log_eps, std_eps, y,
+                         stream);
+}
+
+int kea_logmel_normalize_frames(const float *spec, int64_t batch, int64_t bins, int64_t frames, int64_t ld_f,
+                                const float *fb, const int32_t *lo, const int32_t *hi, int64_t mels, float log_eps,
+                                float std_eps, float *y, void *stream) {
+    if (batch < 0 || batch > 65535 || bins < 1 || frames < 1 || ld_f < frames || mels < 1 || mels > 65535 ||
+        bins * ld_f > ((int64_t)1 << 40))
+        return kea::fail(KEA_EINVAL, "bad sizes");
+    return logmel_launch(spec, batch, bins, frames, 1, bins, bins * ld_f, fb, lo, hi, mels, log_eps, std_eps, y,
+                         stream);
+}
+
+int kea_stft_frames(const float *audio, int64_t batch, int64_t samples, float preemph, const float *window,
+                    int64_t n_fft, int64_t hop, float *frames_out, void *stream) {
+    if (batch < 0 || batch > 65535 || samples < 1 || n_fft < 2 || n_fft > 65536 || n_fft % 2 || hop < 1 ||
+        samples > ((int64_t)1 << 40))
+        return kea::fail(KEA_EINVAL, "bad sizes: batch in [0, 65535], samples >= 1, even n_fft in [2, 65536], hop >= 1");
     if (batch == 0) return KEA_OK;
-    if (!spec || !fb || !lo || !hi || !y) return kea::fail(KEA_EINVAL, "null pointer");
-    if ((uintptr_t)spec & 7) return kea::fail(KEA_EALIGN, "spec must be 8-byte aligned (interleaved complex)");
-    hipLaunchKernelGGL(logmel_normalize_kernel, dim3((unsigned)mels, (unsigned)batch), dim3(256), 0,
-                       (hipStream_t)stream, (const float2 *)spec, (int)bins, (int)frames, (long long)ld_t, fb, lo, hi,
-                       (int)mels, log_eps, std_eps, y);
+    if (!audio || !window || !frames_out) return kea::fail(KEA_EINVAL, "null pointer");
+    const int64_t frames = 1 + samples / hop, per_clip = frames * n_fft;
+    const int64_t blocks = (per_clip + 255) / 256;
+    if (blocks > 0x7fffffff) return kea::fail(KEA_EINVAL, "too many frames for one launch");
+    hipLaunchKernelGGL(stft_frames_kernel, dim3((unsigned)blocks, (unsigned)batch), dim3(256), 0, (hipStream_t)stream,
+                       audio, (long long)samples, preemph, window, (int)n_fft, (int)hop, (long long)frames, frames_out);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return kea::fail((int)e, std::string("logmel launch failed: ") + hipGetErrorString(e));
+    if (e != hipSuccess) return kea::fail((int)e, std::string("stft frames launch failed: ") + hipGetErrorString(e));
     return KEA_OK;
 }
 

@@ -79,6 +79,8 @@ SIGNATURES = {
                                  _vp, _vp]),
     "kea_glu_dwconv_quantize": (_i32, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _i64, _vp, _vp]),
     "kea_logmel_normalize": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _f32, _f32, _vp, _vp]),
+    "kea_logmel_normalize_frames": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _f32, _f32, _vp, _vp]),
+    "kea_stft_frames": (_i32, [_vp, _i64, _i64, _f32, _vp, _i64, _i64, _vp, _vp]),
     "kea_subsample_front": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
     "kea_dwconv2d_s2": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "kea_bias_relu_flatten": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),

@@ -169,12 +169,17 @@ def encoded_length(frames: int) -> int:
 class Preprocessor:
     """audio [B, S] FP32 -> normalised log-mel [B, n_mels, frames]: pre-emphasis, |STFT|^2 (Hann 400 / hop 160 /
     n_fft 512, centred), mel projection, log(x + 2^-24), per-feature mean / std normalisation over time.
-    fused: everything after the STFT in one kernel (kea_logmel_normalize, each filter's nonzero bins only)."""
+    fused: the pre-emphasised, windowed frames in one kernel (kea_stft_frames, the frames torch.stft transforms),
+    torch's real FFT of them, then everything after the FFT in one kernel reading the frame-major spectrum
+    (kea_logmel_normalize_frames, each filter's nonzero bins only)."""
 
     def __init__(self, cfg: EncoderConfig, device, *, fused: bool = False):
         self.cfg = cfg
         self.fused = fused
         self.window = torch.hann_window(cfg.win_length, periodic=False, dtype=torch.float32, device=device)
+        left = (cfg.n_fft - cfg.win_length) // 2                 # torch.stft centres a short window in n_fft
+        self.window_nfft = torch.zeros(cfg.n_fft, dtype=torch.float32, device=device)
+        self.window_nfft[left:left + cfg.win_length] = self.window
         fb = mel_filterbank(cfg)
         self.fb = torch.from_numpy(fb).float().to(device)
         nz = fb != 0
@@ -183,22 +188,35 @@ class Preprocessor:
         self.lo = torch.from_numpy(lo.astype(np.int32)).to(device)
         self.hi = torch.from_numpy(hi.astype(np.int32)).to(device)
 
+    def stft_frames(self, audio: Tensor) -> Tensor:
+        """audio [B, S] FP32 -> the windowed frames [B, 1 + S // hop, n_fft] that torch.stft (center = True,
+        constant padding) transforms, of the pre-emphasised audio (kea_stft_frames)."""
+        cfg = self.cfg
+        if audio.dim() != 2 or audio.dtype != torch.float32 or not audio.is_contiguous():
+            raise ValueError("audio must be a contiguous FP32 tensor [batch, samples]")
+        b, samples = audio.shape
+        out = torch.empty(b, 1 + samples // cfg.hop_length, cfg.n_fft, device=audio.device, dtype=torch.float32)
+        rc = _hip.lib().kea_stft_frames(audio.data_ptr(), b, samples, cfg.preemph, self.window_nfft.data_ptr(),
+                                        cfg.n_fft, cfg.hop_length, out.data_ptr(), _hip.stream_handle(audio.device))
+        _hip.check(rc, "kea_stft_frames")
+        return out
+
     def __call__(self, audio: Tensor) -> Tensor:
         cfg = self.cfg
+        frames = frames_for(cfg, audio.shape[1])
+        if self.fused:
+            spec = torch.fft.rfft(self.stft_frames(audio.contiguous()), dim=-1)   # [B, frames', bins]
+            b, ld_f, bins = spec.shape
+            y = torch.empty(b, cfg.feat_in, frames, device=audio.device, dtype=torch.float32)
+            rc = _hip.lib().kea_logmel_normalize_frames(torch.view_as_real(spec).data_ptr(), b, bins, frames, ld_f,
+                                                        self.fb.data_ptr(), self.lo.data_ptr(), self.hi.data_ptr(),
+                                                        cfg.feat_in, 2.0 ** -24, 1e-5, y.data_ptr(),
+                                                        _hip.stream_handle(audio.device))
+            _hip.check(rc, "kea_logmel_normalize_frames")
+            return y
         x = torch.cat([audio[:, :1], audio[:, 1:] - cfg.preemph * audio[:, :-1]], dim=1)
         spec = torch.stft(x, n_fft=cfg.n_fft, hop_length=cfg.hop_length, win_length=cfg.win_length,
                           window=self.window, center=True, pad_mode="constant", return_complex=True)
-        frames = frames_for(cfg, audio.shape[1])
-        if self.fused:
-            spec = spec.contiguous()
-            b, bins, ld_t = spec.shape
-            y = torch.empty(b, cfg.feat_in, frames, device=audio.device, dtype=torch.float32)
-            rc = _hip.lib().kea_logmel_normalize(torch.view_as_real(spec).data_ptr(), b, bins, frames, ld_t,
-                                                 self.fb.data_ptr(), self.lo.data_ptr(), self.hi.data_ptr(),
-                                                 cfg.feat_in, 2.0 ** -24, 1e-5, y.data_ptr(),
-                                                 _hip.stream_handle(audio.device))
-            _hip.check(rc, "kea_logmel_normalize")
-            return y
         power = torch.view_as_real(spec[:, :, :frames]).pow(2).sum(-1)          # [B, bins, frames]
         mel = torch.matmul(self.fb, power)                                     # [B, mels, frames]
         logmel = torch.log(mel + 2.0 ** -24)

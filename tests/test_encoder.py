@@ -11,7 +11,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from kea_kernels import encoder as E
+from kea_kernels import _hip, encoder as E
 from oracle import oracle as O
 
 
@@ -470,6 +470,57 @@ def test_fused_logmel_matches_pytorch(b, samples):
     ref = (logmel - logmel.mean(2, keepdim=True)) / (logmel.std(2, keepdim=True) + 1e-5)
     assert got.shape == ref.shape
     assert float((got - ref).abs().max()) < 1e-4
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,samples", [(1, 160000), (3, 48000), (2, 16001), (1, 300), (2, 1), (1, 159)])
+@torch.inference_mode()
+def test_stft_frames_give_torch_stft_spectrum_bitwise(b, samples):
+    """kea_stft_frames' frames, through torch's real FFT, are the spectrum torch.stft returns for the pre-emphasised
+    audio (centred, constant padding, Hann 400 in n_fft 512), bit for bit and frame-major; the frame-major log-mel
+    kernel then gives the bin-major one's output bit for bit."""
+    cfg = E.EncoderConfig()
+    audio = torch.randn(b, samples, generator=torch.Generator().manual_seed(samples + b)).cuda()
+    pre = E.Preprocessor(cfg, "cuda", fused=True)
+    frames = pre.stft_frames(audio)
+    assert frames.shape == (b, 1 + samples // cfg.hop_length, cfg.n_fft)
+    x = torch.cat([audio[:, :1], audio[:, 1:] - cfg.preemph * audio[:, :-1]], dim=1)
+    ref = torch.stft(x, n_fft=cfg.n_fft, hop_length=cfg.hop_length, win_length=cfg.win_length, window=pre.window,
+                     center=True, pad_mode="constant", return_complex=True)
+    got = torch.fft.rfft(frames, dim=-1)
+    assert torch.equal(torch.view_as_real(got), torch.view_as_real(ref.transpose(1, 2)))
+    n = E.frames_for(cfg, samples)
+    if n == 0:
+        return
+    lib, stream = _hip.lib(), _hip.stream_handle(audio.device)
+    spec = ref.contiguous()
+    y_bins = torch.empty(b, cfg.feat_in, n, device="cuda")
+    y_frames = torch.full_like(y_bins, float("nan"))
+    _hip.check(lib.kea_logmel_normalize(torch.view_as_real(spec).data_ptr(), b, spec.shape[1], n, spec.shape[2],
+                                        pre.fb.data_ptr(), pre.lo.data_ptr(), pre.hi.data_ptr(), cfg.feat_in,
+                                        2.0 ** -24, 1e-5, y_bins.data_ptr(), stream), "kea_logmel_normalize")
+    _hip.check(lib.kea_logmel_normalize_frames(torch.view_as_real(got).data_ptr(), b, got.shape[2], n, got.shape[1],
+                                               pre.fb.data_ptr(), pre.lo.data_ptr(), pre.hi.data_ptr(), cfg.feat_in,
+                                               2.0 ** -24, 1e-5, y_frames.data_ptr(), stream),
+               "kea_logmel_normalize_frames")
+    assert torch.equal(y_frames, y_bins)
+    assert torch.equal(pre(audio), y_bins)
+
+
+def test_stft_and_logmel_entry_points_check_sizes_before_any_launch():
+    """The framing and frame-major log-mel entry points refuse sizes they cannot run before touching the GPU."""
+    L = _hip.lib()
+    vp = ctypes.c_void_p
+    assert L.kea_stft_frames(vp(16), 1, 1000, 0.97, vp(16), 511, 160, vp(16), None) == -1     # odd n_fft
+    assert b"n_fft" in L.kea_last_error()
+    assert L.kea_stft_frames(vp(16), 1, 0, 0.97, vp(16), 512, 160, vp(16), None) == -1        # no samples
+    assert L.kea_stft_frames(vp(16), 1, 1000, 0.97, vp(16), 512, 0, vp(16), None) == -1       # hop
+    assert L.kea_stft_frames(vp(16), 70000, 1000, 0.97, vp(16), 512, 160, vp(16), None) == -1  # batch
+    assert L.kea_stft_frames(None, 1, 1000, 0.97, vp(16), 512, 160, vp(16), None) == -1       # null audio
+    assert L.kea_stft_frames(None, 0, 1000, 0.97, None, 512, 160, None, None) == 0             # empty batch
+    args = (vp(16), 1, 257, 10, 9, vp(16), vp(16), vp(16), 80, 2.0 ** -24, 1e-5, vp(16), None)
+    assert L.kea_logmel_normalize_frames(*args) == -1                                           # ld_f < frames
+    assert L.kea_logmel_normalize_frames(vp(12), *args[1:4], 10, *args[5:]) == -2               # alignment
 
 
 def test_fused_launchers_check_parameters_before_any_call():
