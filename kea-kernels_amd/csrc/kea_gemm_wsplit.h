@@ -26,6 +26,9 @@ constexpr WsplitTile kWsplitTiles[] = {
     {1, 2, 4, "16x32 k/4"},
     {2, 8, 4, "32x128 k/4"},
     {1, 4, 8, "16x64 k/8"},
+    {1, 2, 8, "16x32 k/8"},
+    {1, 1, 8, "16x16 k/8"},
+    {1, 1, 4, "16x16 k/4"},
 };
 constexpr int kNumWsplitTiles = sizeof(kWsplitTiles) / sizeof(kWsplitTiles[0]);
 
@@ -43,14 +46,17 @@ inline int wsplit_steps(int wbits, long long steps, int nw) {
 }
 
 // Registers a wave of the tile needs for `s` steps (operands + accumulators, 32-bit), and whether that fits the
-// register file share of one wave (nw = 4: one wave per SIMD; nw = 8: two).
+// register file share of one wave (nw = 4: one wave per SIMD; nw = 8: two), with room left for addresses and
+// temporaries.
+constexpr int wsplit_reg_budget(int nw) { return nw == 4 ? 320 : 160; }
+
 // LDS bytes of the partial-sum exchange: nw waves x parts x rm x nt blocks of 64 lanes x 4 int32.
 inline int wsplit_lds_bytes(int parts, const WsplitTile &t) { return t.nw * parts * t.rm * t.nt * 1024; }
 
 inline bool wsplit_fits(int wbits, int parts, const WsplitTile &t, int s) {
     const int words = wbits == 1 ? s / 2 : s;
     const int regs = parts * t.rm * s * 4 + t.nt * words + parts * t.rm * t.nt * 4;
-    return regs <= (t.nw == 4 ? 320 : 160) && wsplit_lds_bytes(parts, t) <= 160 * 1024;
+    return regs <= wsplit_reg_budget(t.nw) && wsplit_lds_bytes(parts, t) <= 160 * 1024;
 }
 
 using WsplitFn = void (*)(const int8_t *, const uint32_t *, const void *, const void *, int, int, int, int, int,

@@ -186,7 +186,7 @@ template <int WBITS, int P, int RM, int NT, int NW, int S, bool SLICED, bool RAG
 WsplitFn pick_fit() {
     constexpr int words = WBITS == 1 ? S / 2 : S;
     constexpr int regs = P * RM * S * 4 + NT * words + P * RM * NT * 4;
-    if constexpr (regs <= (NW == 4 ? 320 : 160) && NW * P * RM * NT * 1024 <= 160 * 1024)
+    if constexpr (regs <= wsplit_reg_budget(NW) && NW * P * RM * NT * 1024 <= 160 * 1024)
         return wsplit_kernel<WBITS, P, RM, NT, NW, S, SLICED, RAGGED>;
     else
         return nullptr;
@@ -202,17 +202,15 @@ WsplitFn pick_s(int s) {
     }
 }
 
-template <int WBITS, int P, bool SLICED, bool RAGGED>
+// The instance for kWsplitTiles[tile] (nullptr for an unknown index), one case per table entry.
+template <int WBITS, int P, bool SLICED, bool RAGGED, int T = 0>
 WsplitFn pick_tile(int tile, int s) {
-    switch (tile) {
-        case 0: return pick_s<WBITS, P, 1, 8, 4, SLICED, RAGGED>(s);
-        case 1: return pick_s<WBITS, P, 2, 4, 4, SLICED, RAGGED>(s);
-        case 2: return pick_s<WBITS, P, 1, 4, 4, SLICED, RAGGED>(s);
-        case 3: return pick_s<WBITS, P, 1, 8, 8, SLICED, RAGGED>(s);
-        case 4: return pick_s<WBITS, P, 2, 4, 8, SLICED, RAGGED>(s);
-        case 5: return pick_s<WBITS, P, 1, 2, 4, SLICED, RAGGED>(s);
-        case 6: return pick_s<WBITS, P, 2, 8, 4, SLICED, RAGGED>(s);
-        default: return pick_s<WBITS, P, 1, 4, 8, SLICED, RAGGED>(s);
+    if constexpr (T < kNumWsplitTiles) {
+        constexpr WsplitTile t = kWsplitTiles[T];
+        if (tile == T) return pick_s<WBITS, P, t.rm, t.nt, t.nw, SLICED, RAGGED>(s);
+        return pick_tile<WBITS, P, SLICED, RAGGED, T + 1>(tile, s);
+    } else {
+        return nullptr;
     }
 }
 

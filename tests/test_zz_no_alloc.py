@@ -51,7 +51,8 @@ def test_noalloc_equals_the_workspace_entry_point_on_successive_calls():
     # (wbits, m, n, k, config, split): ring tile 32x32 split 4, then smaller: a wave-split tile whose K range needs
     # two slices, a ring split of 2, and the two producer-wave tiles split 3 and 2; every call uses the scratch
     # array (workspace > 0)
-    cases = [(2, 96, 1024, 8192, 4, 4), (1, 40, 512, 8192, kernels.tile_count() - 2, 0), (2, 24, 300, 4096, 4, 2),
+    wsplit_16x32 = next(t for t in range(1, kernels.tile_count() + 1) if kernels.config_name(t) == "16x32 k/4")
+    cases = [(2, 96, 1024, 8192, 4, 4), (1, 40, 512, 8192, wsplit_16x32, 0), (2, 24, 300, 4096, 4, 2),
              (1, 70, 512, 4096, 6, 3), (2, 50, 256, 2048, 7, 2)]
     for i, (wbits, m, n, k, config, split) in enumerate(cases):
         need = L.kea_lowbit_gemm_workspace(wbits, 1, m, n, k, 0, split, config)
