@@ -195,8 +195,9 @@ def test_every_tile_gives_identical_results(wbits, parts):
         try:
             y, acc = case.run(config=kernels.GemmConfig(tile=tile, split=1))
         except ValueError as e:
-            # the 16-wave producer tile keeps one part's accumulators within a quarter of a SIMD's registers
-            if parts > 1 and "does not fit" in str(e) and kernels.config_name(tile).endswith(" p8"):
+            # a tile whose registers hold one part's operands and accumulators only (the 16-wave producer tile, the
+            # widest eight-wave tiles) refuses more parts; at one part every tile must run
+            if parts > 1 and "does not fit" in str(e):
                 continue
             raise
         if ref is None:
@@ -240,7 +241,7 @@ def test_glu_fast_epilogue_equals_the_general_one_on_every_tile(wbits, parts, ou
                 lowbit.gemm(wbits, case.dq, case.dqs, case.words, 400, 1152, case.dalpha, case.dbias, y, None,
                             glu=True, config=kernels.GemmConfig(tile=tile, split=1))
             except ValueError as e:
-                if parts > 1 and "does not fit" in str(e) and kernels.config_name(tile).endswith(" p8"):
+                if parts > 1 and "does not fit" in str(e):  # one-part tiles, as in the every-tile test
                     break
                 raise
             torch.cuda.synchronize()
