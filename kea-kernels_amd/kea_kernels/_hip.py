@@ -142,6 +142,10 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 
 def stream_handle(device: torch.device) -> int:
+    """torch's current stream on `device`; ValueError for a device that is not a GPU (the kernels would read host
+    pointers as device addresses)."""
+    if device.type != "cuda":
+        raise ValueError(f"the kernels run on the GPU: tensors on {device} cannot be launched on")
     return torch.cuda.current_stream(device).cuda_stream
 
 

@@ -194,6 +194,8 @@ class Preprocessor:
         cfg = self.cfg
         if audio.dim() != 2 or audio.dtype != torch.float32 or not audio.is_contiguous():
             raise ValueError("audio must be a contiguous FP32 tensor [batch, samples]")
+        if audio.device != self.window_nfft.device:
+            raise ValueError(f"audio is on {audio.device}, the preprocessor on {self.window_nfft.device}")
         b, samples = audio.shape
         out = torch.empty(b, 1 + samples // cfg.hop_length, cfg.n_fft, device=audio.device, dtype=torch.float32)
         rc = _hip.lib().kea_stft_frames(audio.data_ptr(), b, samples, cfg.preemph, self.window_nfft.data_ptr(),

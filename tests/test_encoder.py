@@ -556,6 +556,22 @@ def test_fused_launchers_check_parameters_before_any_call():
         E.norm_quantize(torch.zeros(1, t, d), ln_k, ln_short, 1)
 
 
+def test_fused_preprocessor_refuses_host_and_mismatched_audio_before_any_call():
+    """The framing kernel's launcher refuses audio that is not contiguous FP32 [B, S], on another device than its
+    window, or on the host (no GPU pointer to launch on), before any C call."""
+    cfg = E.EncoderConfig()
+    pre = E.Preprocessor(cfg, "cpu", fused=True)
+    with pytest.raises(ValueError, match="FP32"):
+        pre.stft_frames(torch.zeros(1, 1600, dtype=torch.float64))
+    with pytest.raises(ValueError, match="contiguous"):
+        pre.stft_frames(torch.zeros(1600, 2).t())
+    with pytest.raises(ValueError, match="GPU"):
+        pre.stft_frames(torch.zeros(1, 1600))
+    pre.window_nfft = pre.window_nfft.to("meta")
+    with pytest.raises(ValueError, match="preprocessor on meta"):
+        pre.stft_frames(torch.zeros(1, 1600))
+
+
 def test_graph_cache_limits_and_eager_paths_on_cpu():
     with pytest.raises(ValueError, match="max_graphs"):
         E.EncoderGraphCache(None, max_graphs=0)
