@@ -178,6 +178,30 @@ def test_ragged_k_with_garbage_padding(wbits, k):
     assert_parity(case, y, acc, out_dtype=torch.float32)
 
 
+@pytest.mark.parametrize("wbits", [1, 2])
+@pytest.mark.parametrize("m,n,k,parts", [(1, 1030, 1100, 1), (5, 37, 17, 3), (16, 2560, 640, 2), (40, 300, 4100, 1)])
+@torch.inference_mode()
+def test_every_wave_split_tile_on_ragged_small_m_shapes(wbits, m, n, k, parts):
+    """Each wave-split tile (its K range cut over 4 or 8 waves, N tails of one 16-column block or less) against the
+    oracle at the small-M shapes the narrow tiles serve: one row, ragged K with garbage padding, N not a multiple of
+    16, several activation parts."""
+    case = Case(wbits, parts, m, n, k, seed=m + n + k + wbits, bias=True, pad_garbage=True)
+    ran = 0
+    for tile in range(1, kernels.tile_count() + 1):
+        if " k/" not in kernels.config_name(tile):
+            continue
+        try:
+            y, acc = case.run(out_dtype=torch.float32, config=kernels.GemmConfig(tile=tile, split=0))
+        except ValueError as e:
+            # tiles whose registers cannot hold this many parts, and K % 16 != 0 ranges too long for one workgroup
+            if "does not fit" in str(e) or "unsplit K range" in str(e):
+                continue
+            raise
+        assert_parity(case, y, acc, out_dtype=torch.float32)
+        ran += 1
+    assert ran >= 3  # at least three tiles take every one of these shapes
+
+
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
 @torch.inference_mode()
 def test_silu_epilogue_within_tolerance(out_dtype):
