@@ -566,16 +566,14 @@ stft_frames_kernel(const float *audio, long long samples, float preemph, const f
 // Log-mel features with per-feature normalisation over time, one workgroup per (clip, mel bin):
 //   v[t] = log(sum_{k in [lo, hi)} fb[m][k] * (re^2 + im^2)[k][t] + log_eps)       (the filter's nonzero bins only)
 //   y[t] = (v[t] - mean) / (std + std_eps),  mean over the frames, std with the n - 1 divisor
-// spec: interleaved complex, element (bin k, frame t) of clip b at b * bstride + k * kstride + t * tstride (bin-major
-// [B][bins][ld_t] or frame-major [B][ld_f][bins]); y: [B][mels][frames]. Thread th owns frames th, th + 256, ...: it
+// spec: interleaved complex [B][bins][ld_t]; y: [B][mels][frames]. Thread th owns frames th, th + 256, ...: it
 // writes v, re-reads its own elements for the variance and the normalisation (no barrier between those passes).
 __global__ void __launch_bounds__(256)
-logmel_normalize_kernel(const float2 *spec, int bins, int frames, long long kstride, long long tstride,
-                        long long bstride, const float *fb, const int *lo, const int *hi, int mels, float log_eps,
-                        float std_eps, float *y) {
+logmel_normalize_kernel(const float2 *spec, int bins, int frames, long long ld_t, const float *fb, const int *lo,
+                        const int *hi, int mels, float log_eps, float std_eps, float *y) {
     __shared__ float red[2][4];
     const int m = blockIdx.x, b = blockIdx.y, th = threadIdx.x, wave = th >> 6;
-    const float2 *sb = spec + (long long)b * bstride;
+    const float2 *sb = spec + (long long)b * bins * ld_t;
     float *yr = y + ((long long)b * mels + m) * frames;
     const int k0 = lo[m], k1 = hi[m];
     float sum = 0.f;
@@ -589,7 +587,7 @@ logmel_normalize_kernel(const float2 *spec, int bins, int frames, long long kstr
                 for (int i = 0; i < 4; ++i) {
                     const int t = t0 + th + 256 * i;
                     c[kk][i] = make_float2(0.f, 0.f);
-                    if (k + kk < k1 && t < frames) c[kk][i] = sb[(long long)(k + kk) * kstride + t * tstride];
+                    if (k + kk < k1 && t < frames) c[kk][i] = sb[(long long)(k + kk) * ld_t + t];
                 }
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
@@ -601,6 +599,70 @@ logmel_normalize_kernel(const float2 *spec, int bins, int frames, long long kstr
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            const int t = t0 + th + 256 * i;
+            if (t < frames) {
+                const float v = logf(acc[i] + log_eps);
+                yr[t] = v;
+                sum = sum + v;
+            }
+        }
+    }
+    sum = wave_sum(sum);
+    if ((th & 63) == 0) red[0][wave] = sum;
+    __syncthreads();
+    const float mean = ((red[0][0] + red[0][1]) + (red[0][2] + red[0][3])) / (float)frames;
+    float sq = 0.f;
+    for (int t = th; t < frames; t += 256) {
+        const float d = yr[t] - mean;
+        sq = __builtin_fmaf(d, d, sq);
+    }
+    sq = wave_sum(sq);
+    if ((th & 63) == 0) red[1][wave] = sq;
+    __syncthreads();
+    const float var = ((red[1][0] + red[1][1]) + (red[1][2] + red[1][3])) / (float)(frames > 1 ? frames - 1 : 1);
+    const float inv = 1.0f / (sqrtf(var) + std_eps);
+    for (int t = th; t < frames; t += 256) yr[t] = (yr[t] - mean) * inv;
+}
+
+// The same features from a frame-major spectrum ([B][ld_f][bins], the real FFT of kea_stft_frames' rows). A filter's
+// band of a frame is a few contiguous bins, so the band of kChunk frames is staged through LDS as power values,
+// read with consecutive bins on consecutive lanes; each thread then sums its frames' powers in the order of
+// logmel_normalize_kernel (increasing k, one fma per bin) and the normalisation is the same code, so both layouts give
+// the same bits. Bands wider than kBand bins are staged kBand bins at a time.
+constexpr int kChunk = 512, kBand = 16;
+__global__ void __launch_bounds__(256)
+logmel_normalize_frames_kernel(const float2 *spec, int bins, int frames, long long ld_f, const float *fb,
+                               const int *lo, const int *hi, int mels, float log_eps, float std_eps, float *y) {
+    __shared__ float pw[kBand * (kChunk + 1)];  // [bin of the band][frame], rows padded against bank conflicts
+    __shared__ float red[2][4];
+    const int m = blockIdx.x, b = blockIdx.y, th = threadIdx.x, wave = th >> 6;
+    const float2 *sb = spec + (long long)b * ld_f * bins;
+    float *yr = y + ((long long)b * mels + m) * frames;
+    const int k0 = lo[m], k1 = hi[m];
+    float sum = 0.f;
+    for (int t0 = 0; t0 < frames; t0 += kChunk) {
+        const int nf = min(kChunk, frames - t0);
+        float acc[kChunk / 256];
+#pragma unroll
+        for (int i = 0; i < kChunk / 256; ++i) acc[i] = 0.f;
+        for (int kc = k0; kc < k1; kc += kBand) {
+            const int w = min(kBand, k1 - kc);
+            __syncthreads();  // the previous band's readers are done
+            for (int e = th; e < nf * w; e += 256) {
+                const int f = e / w, kk = e - f * w;
+                const float2 c = sb[(long long)(t0 + f) * bins + kc + kk];
+                pw[kk * (kChunk + 1) + f] = c.x * c.x + c.y * c.y;
+            }
+            __syncthreads();
+            for (int kk = 0; kk < w; ++kk) {
+                const float wt = fb[m * bins + kc + kk];
+#pragma unroll
+                for (int i = 0; i < kChunk / 256; ++i)
+                    acc[i] = __builtin_fmaf(wt, pw[kk * (kChunk + 1) + th + 256 * i], acc[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kChunk / 256; ++i) {
             const int t = t0 + th + 256 * i;
             if (t < frames) {
                 const float v = logf(acc[i] + log_eps);
@@ -810,21 +872,6 @@ int kea_bias_relu_flatten(const float *x, const float *bias, float *y, int64_t b
     return KEA_OK;
 }
 
-namespace {
-int logmel_launch(const float *spec, int64_t batch, int64_t bins, int64_t frames, int64_t kstride, int64_t tstride,
-                  int64_t bstride, const float *fb, const int32_t *lo, const int32_t *hi, int64_t mels, float log_eps,
-                  float std_eps, float *y, void *stream) {
-    if (batch == 0) return KEA_OK;
-    if (!spec || !fb || !lo || !hi || !y) return kea::fail(KEA_EINVAL, "null pointer");
-    if ((uintptr_t)spec & 7) return kea::fail(KEA_EALIGN, "spec must be 8-byte aligned (interleaved complex)");
-    hipLaunchKernelGGL(logmel_normalize_kernel, dim3((unsigned)mels, (unsigned)batch), dim3(256), 0,
-                       (hipStream_t)stream, (const float2 *)spec, (int)bins, (int)frames, (long long)kstride,
-                       (long long)tstride, (long long)bstride, fb, lo, hi, (int)mels, log_eps, std_eps, y);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return kea::fail((int)e, std::string("logmel launch failed: ") + hipGetErrorString(e));
-    return KEA_OK;
-}
-}  // namespace
 
 int kea_logmel_normalize(const float *spec, int64_t batch, int64_t bins, int64_t frames, int64_t ld_t,
                          const float *fb, const int32_t *lo, const int32_t *hi, int64_t mels, float log_eps,
@@ -832,8 +879,15 @@ int kea_logmel_normalize(const float *spec, int64_t batch, int64_t bins, int64_t
     if (batch < 0 || batch > 65535 || bins < 1 || frames < 1 || ld_t < frames || mels < 1 || mels > 65535 ||
         bins * ld_t > ((int64_t)1 << 40))
         return kea::fail(KEA_EINVAL, "bad sizes");
-    return logmel_launch(spec, batch, bins, frames, ld_t, 1, bins * ld_t, fb, lo, hi, mels, log_eps, std_eps, y,
-                         stream);
+    if (batch == 0) return KEA_OK;
+    if (!spec || !fb || !lo || !hi || !y) return kea::fail(KEA_EINVAL, "null pointer");
+    if ((uintptr_t)spec & 7) return kea::fail(KEA_EALIGN, "spec must be 8-byte aligned (interleaved complex)");
+    hipLaunchKernelGGL(logmel_normalize_kernel, dim3((unsigned)mels, (unsigned)batch), dim3(256), 0,
+                       (hipStream_t)stream, (const float2 *)spec, (int)bins, (int)frames, (long long)ld_t, fb, lo, hi,
+                       (int)mels, log_eps, std_eps, y);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("logmel launch failed: ") + hipGetErrorString(e));
+    return KEA_OK;
 }
 
 int kea_logmel_normalize_frames(const float *spec, int64_t batch, int64_t bins, int64_t frames, int64_t ld_f,
@@ -842,8 +896,15 @@ int kea_logmel_normalize_frames(const float *spec, int64_t batch, int64_t bins, 
     if (batch < 0 || batch > 65535 || bins < 1 || frames < 1 || ld_f < frames || mels < 1 || mels > 65535 ||
         bins * ld_f > ((int64_t)1 << 40))
         return kea::fail(KEA_EINVAL, "bad sizes");
-    return logmel_launch(spec, batch, bins, frames, 1, bins, bins * ld_f, fb, lo, hi, mels, log_eps, std_eps, y,
-                         stream);
+    if (batch == 0) return KEA_OK;
+    if (!spec || !fb || !lo || !hi || !y) return kea::fail(KEA_EINVAL, "null pointer");
+    if ((uintptr_t)spec & 7) return kea::fail(KEA_EALIGN, "spec must be 8-byte aligned (interleaved complex)");
+    hipLaunchKernelGGL(logmel_normalize_frames_kernel, dim3((unsigned)mels, (unsigned)batch), dim3(256), 0,
+                       (hipStream_t)stream, (const float2 *)spec, (int)bins, (int)frames, (long long)ld_f, fb, lo, hi,
+                       (int)mels, log_eps, std_eps, y);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return kea::fail((int)e, std::string("logmel launch failed: ") + hipGetErrorString(e));
+    return KEA_OK;
 }
 
 int kea_stft_frames(const float *audio, int64_t batch, int64_t samples, float preemph, const float *window,

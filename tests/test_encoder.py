@@ -507,6 +507,37 @@ def test_stft_frames_give_torch_stft_spectrum_bitwise(b, samples):
     assert torch.equal(pre(audio), y_bins)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("frames,ld,seed", [(700, 703, 1), (1, 1, 2), (513, 520, 3)])
+@torch.inference_mode()
+def test_frame_major_logmel_equals_bin_major_on_wide_bands(frames, ld, seed):
+    """kea_logmel_normalize_frames (bands staged through LDS 16 bins at a time, 512 frames at a time) against
+    kea_logmel_normalize on the transposed spectrum, bit for bit, with filter bands of 0 to 40 bins."""
+    g = torch.Generator().manual_seed(seed)
+    b, bins, mels = 2, 257, 9
+    spec_f = torch.randn(b, ld, bins, 2, generator=g)
+    lo = torch.randint(0, bins, (mels,), generator=g, dtype=torch.int32)
+    width = torch.tensor([0, 1, 5, 12, 16, 17, 31, 40, 3], dtype=torch.int32)
+    hi = torch.minimum(lo + width, torch.tensor(bins, dtype=torch.int32))
+    fb = torch.zeros(mels, bins)
+    for m in range(mels):
+        fb[m, lo[m]:hi[m]] = torch.rand(int(hi[m] - lo[m]), generator=g) + 0.01
+    spec_b = spec_f.transpose(1, 2).contiguous()   # [b][bins][ld][2]
+    dev = "cuda"
+    spec_f, spec_b, fb, lo, hi = (t.to(dev) for t in (spec_f, spec_b, fb, lo, hi))
+    lib, stream = _hip.lib(), _hip.stream_handle(torch.device(dev))
+    y_b = torch.full((b, mels, frames), float("nan"), device=dev)
+    y_f = torch.full_like(y_b, float("nan"))
+    _hip.check(lib.kea_logmel_normalize(spec_b.data_ptr(), b, bins, frames, ld, fb.data_ptr(), lo.data_ptr(),
+                                        hi.data_ptr(), mels, 2.0 ** -24, 1e-5, y_b.data_ptr(), stream), "bin-major")
+    _hip.check(lib.kea_logmel_normalize_frames(spec_f.data_ptr(), b, bins, frames, ld, fb.data_ptr(), lo.data_ptr(),
+                                               hi.data_ptr(), mels, 2.0 ** -24, 1e-5, y_f.data_ptr(), stream),
+               "frame-major")
+    torch.cuda.synchronize()
+    assert torch.equal(y_f, y_b)
+    assert not torch.isnan(y_f).any()
+
+
 def test_stft_and_logmel_entry_points_check_sizes_before_any_launch():
     """The framing and frame-major log-mel entry points refuse sizes they cannot run before touching the GPU."""
     L = _hip.lib()
