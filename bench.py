@@ -226,7 +226,9 @@ def probes() -> None:
       100 launches, at the group sizes an in-launch split-K (4) and a whole-grid exchange need;
     * config3_floors: the launch floors of config 3's grid (M = 1024 so the 128x128 tile divides it; N = 4096,
       K = 1024) with 4, 8 and 16 waves per workgroup, next to the GEMM on that grid with tile 11 (128x128, 8 waves)
-      and tile 6 (the same compute waves and 8 producer waves, 16 in all)."""
+      and tile 6 (the same compute waves and 8 producer waves, 16 in all);
+    * config1_floors: the launch floors of config 1's shape on grids of 16x16 to 128x128 tiles and 1 to 8 waves per
+      workgroup (how the cost of moving the operands depends on the grid)."""
     import ctypes
     import torch
     from kea_kernels import _hip, lowbit
@@ -306,6 +308,13 @@ def probes() -> None:
         row = {"probe": "config3_floors", "M": m, "N": n, "K": k}
         row.update(launch_floors({"q": q, "words": words, "y": y}, stream, "128x128", shape=(m, n, k), waves=waves))
         row["gemm_tile11_us"], row["gemm_tile6_us"] = gemm_us[11], gemm_us[6]
+        print(json.dumps(row), flush=True)
+
+    host, d = make_inputs(dev)
+    for tile, waves in (("16x16", 4), ("16x32", 4), ("16x64", 1), ("16x64", 2), ("16x64", 4), ("16x64", 8),
+                        ("16x128", 4), ("16x128", 8), ("32x128", 4), ("64x128", 4), ("128x128", 8)):
+        row = {"probe": "config1_floors", "M": M, "N": N, "K": K}
+        row.update(launch_floors(d, stream, tile, waves=waves))
         print(json.dumps(row), flush=True)
 
 
