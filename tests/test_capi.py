@@ -170,6 +170,19 @@ def test_tile_and_split_tables_are_pure_functions():
         assert ws == (s * m * n * 4 if s > 1 else 0)
 
 
+def test_every_tile_table_entry_is_the_chooser_pick_and_resolves():
+    """Each entry of the measured tile table (csrc/kea_gemm_table.h) is what the chooser returns at that swept shape,
+    and the library resolves it there (registers, LDS and K range fit; no silent fall-back to another tile)."""
+    L = _hip.lib()
+    text = (Path(__file__).resolve().parents[1] / "kea-kernels_amd" / "csrc" / "kea_gemm_table.h").read_text()
+    entries = [tuple(int(v) for v in e) for e in re.findall(r"\{(\d+), (\d+), (\d+), (\d+), (\d+), (\d+)\},", text)]
+    assert len(entries) >= 300
+    for wbits, parts, n, k, m, tile in entries:
+        assert 1 <= tile <= L.kea_config_count()
+        assert L.kea_lowbit_gemm_tile(wbits, parts, m, n, k) == tile, (wbits, parts, n, k, m, tile)
+        assert L.kea_lowbit_gemm_workspace(wbits, parts, m, n, k, 0, 0, tile) >= 0, _hip.last_error()
+
+
 def test_plan_refuses_what_the_direct_call_refuses():
     """kea_lowbit_gemm_plan returns NULL (with the same message) on arguments kea_lowbit_gemm refuses; nothing is
     launched and no device is touched."""
