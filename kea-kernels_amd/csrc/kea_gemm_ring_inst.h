@@ -208,11 +208,15 @@ __global__ void __launch_bounds__((WM * WN + PW) * 64) gemm_kernel(Params p) {
         }
     };
 
-    // One stage of MFMAs: straight-line code (no accumulator ever passes a control-flow merge; merges made the
-    // compiler emit AGPR copy chains). Operand reads from LDS run ahead of the MFMAs: narrow tiles (P * RM <= 2, few
-    // MFMAs per k-step) issue every read of the stage before the first MFMA, so a stage pays one LDS latency instead
-    // of one per k-step; wider tiles read k-step t + 1 while the MFMAs of step t run. MASKED (the last stage) zeroes
-    // the weights at k >= kend: per 16-byte group of a lane's operand, or per byte for KTAIL.
+    // One stage of MFMAs: straight-line code. No accumulator may pass a control-flow merge (an `if` around MFMAs, a
+    // loop whose trip count is not a compile-time constant): at such merges the compiler emitted AGPR copy chains, and
+    // those builds returned wrong values in accumulator component 0. The masked last stage is therefore a separate
+    // instantiation rather than a branch inside the loop; after any change here, run the every-tile and every-split
+    // GPU tests, which compare every tile and split with the oracle. Operand reads from LDS run ahead of the MFMAs:
+    // narrow tiles (P * RM <= 2, few MFMAs per k-step) issue every read of the stage before the first MFMA, so a stage
+    // pays one LDS latency instead of one per k-step; wider tiles read k-step t + 1 while the MFMAs of step t run.
+    // MASKED (the last stage) zeroes the weights at k >= kend: per 16-byte group of a lane's operand, or per byte for
+    // KTAIL.
     auto compute = [&](int s, auto masked_tag) {
         constexpr bool MASKED = decltype(masked_tag)::value;
         const int8_t *buf = lds + (s % NS) * STAGE_BYTES;
