@@ -8,7 +8,6 @@ nemo_toolkit, so here load() ends with formats.build_nemo's RuntimeError after e
 """
 from __future__ import annotations
 
-import contextlib
 import os
 from dataclasses import dataclass, field
 from pathlib import Path
@@ -34,15 +33,14 @@ class Transcript:
 @dataclass
 class Model:
     """A loaded model: `nemo` is the NeMo model whose quantized linears run on this library's kernels. close() (or
-    leaving the context manager) undoes what load() set up."""
+    leaving the context manager) runs `undo`, what load() registered to restore, latest first."""
     nemo: object
     name: str
     kind: str
     mode: str
     export: str
     device: torch.device
-    _stack: contextlib.ExitStack = field(repr=False)
-    _featurizer: dict = field(repr=False, default_factory=dict)
+    undo: list = field(repr=False, default_factory=list)
     closed: bool = False
 
     def transcribe(self, audio, **kwargs):
@@ -106,12 +104,17 @@ def load(path, device="cuda", mode: str | None = None, *, verify: bool = True) -
     torch.cuda.set_device(device)
     with torch.inference_mode():
         nemo = _BUILDERS[info.kind](info.export, manifest, device, mode).eval()
-        featurizer = nemo.preprocessor.featurizer
-        saved = {key: getattr(featurizer, key) for key in _FEATURIZER_OVERRIDES}
-        for key, value in _FEATURIZER_OVERRIDES.items():
-            setattr(featurizer, key, value)
+        undo = [_override_featurizer(nemo.preprocessor.featurizer)]
         torch.cuda.synchronize(device)
-    return Model(nemo, info.name, info.kind, mode, str(info.export), device, contextlib.ExitStack(), saved)
+    return Model(nemo, info.name, info.kind, mode, str(info.export), device, undo)
+
+
+def _override_featurizer(featurizer):
+    """Sets the deterministic feature options and returns the callable that puts the previous values back."""
+    saved = {key: getattr(featurizer, key) for key in _FEATURIZER_OVERRIDES}
+    for key, value in _FEATURIZER_OVERRIDES.items():
+        setattr(featurizer, key, value)
+    return lambda: [setattr(featurizer, key, value) for key, value in saved.items()]
 
 
 def close(model: Model) -> None:
@@ -120,10 +123,8 @@ def close(model: Model) -> None:
         return
     if torch.cuda.is_initialized():
         torch.cuda.synchronize(model.device)
-    model._stack.close()
-    featurizer = model.nemo.preprocessor.featurizer
-    for key, value in model._featurizer.items():
-        setattr(featurizer, key, value)
+    while model.undo:
+        model.undo.pop()()
     model.closed = True
 
 

@@ -95,16 +95,17 @@ class _Nemo:
 
 
 def test_closed_model_and_idempotent_close():
-    import contextlib
     calls = []
-    stack = contextlib.ExitStack()
-    stack.callback(lambda: calls.append("undo"))
-    m = model.Model(_Nemo(), "kea-b", "binary", "x2", "/x", torch.device("cpu"), stack, {"dither": 0.5})
+    featurizer = _Nemo.preprocessor.featurizer
+    featurizer.dither = 0.5
+    undo = [lambda: calls.append("first"), model._override_featurizer(featurizer), lambda: calls.append("last")]
+    assert featurizer.dither == 0.0 and featurizer.pad_to == 0
+    m = model.Model(_Nemo(), "kea-b", "binary", "x2", "/x", torch.device("cpu"), undo)
     with m:
         pass
-    assert m.closed and calls == ["undo"] and _Nemo.preprocessor.featurizer.dither == 0.5
+    assert m.closed and calls == ["last", "first"] and featurizer.dither == 0.5
     m.close()
-    assert calls == ["undo"]
+    assert calls == ["last", "first"]
     with pytest.raises(ValueError, match="closed"):
         kea_kernels.transcribe(m, np.zeros(480, np.float32))
 
