@@ -108,8 +108,11 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
     }
     // the operand loads go out before anything that needs a kernel argument outside the preloaded ones
     __builtin_amdgcn_sched_barrier(0);
-    // epilogue scales of the blocks this wave finishes: raw words now, converted in the epilogue
+    // epilogue scales of the blocks this wave finishes: raw words now, converted in the epilogue; and their residual
+    // values, which would otherwise be a memory round trip after the reduction (the residual may be y itself: each
+    // element is read here and written later by this same lane, so in-place updates stay exact)
     uint32_t rs[UB][3], ra[UB][4], rb[UB][4];
+    float rr[UB][4];
     if constexpr (!SLICED) {
 #pragma unroll
         for (int u = 0; u < UB; ++u) {
@@ -128,6 +131,7 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
 #pragma unroll
                 for (int r = 0; r < 4; ++r) rb[u][r] = 0u;
             }
+            if (p.res) load_residual(p, m, nb, rr[u]);
         }
     }
     // Every load above is issued before the first instruction that waits. The memory clobber keeps the compiler from
@@ -175,7 +179,10 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
                 e.alpha[r] = raw_to_f32(ra[u][r], ws16, ws, (uint32_t)n);
                 e.bias[r] = bias ? raw_to_f32(rb[u][r], b16, bias, (uint32_t)n) : kNoBias;
             }
-            load_residual(p, m, nb, e.res);
+            if (p.res) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) e.res[r] = rr[u][r];
+            }
             wsplit_epilogue<P>(p, plain, M, N, m, mt, nt, nb, a, e);
         }
     }
