@@ -40,6 +40,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "kea-kernels_amd"))
 sys.path.insert(0, str(ROOT))
 
+import kea_probes  # noqa: E402  (the benchmark's probe library, include/kea_probe.h; loaded on first use)
+
 M, N, K = 128, 4096, 1024
 OPS = 2 * M * N * K
 # algorithmic HBM bytes per launch: A + W (1 bit) + alpha (fp16) + per-token scales (fp16) + Y (fp16)
@@ -74,11 +76,10 @@ def replay_timed(stream, graphs, passes: int = 1) -> float:
     """Milliseconds of `passes` back-to-back replays of `graphs` on `stream`, between HIP events recorded on that
     stream; a bounded spin kernel runs first so the replays are queued before the start event executes."""
     import torch
-    from kea_kernels import _hip
     with torch.cuda.stream(stream):
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        _hip.check(_hip.lib().kea_probe_spin(SPIN_NS, stream.cuda_stream), "kea_probe_spin")
+        kea_probes.check(kea_probes.lib().kea_probe_spin(SPIN_NS, stream.cuda_stream), "kea_probe_spin")
         start.record(stream)
         for _ in range(passes):
             for graph in graphs:
@@ -102,12 +103,11 @@ def queued_timed(stream, fn, steps: int, host_us: float) -> float:
     recorded on that stream. The calls are queued behind a bounded spin kernel that outlasts their submission
     (host_us per call, doubled), so the GPU runs them back to back with no host gaps and no graph boundaries."""
     import torch
-    from kea_kernels import _hip
     spin = int(min(100e6, SPIN_NS + 2e3 * host_us * steps))
     with torch.cuda.stream(stream):
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        _hip.check(_hip.lib().kea_probe_spin(spin, stream.cuda_stream), "kea_probe_spin")
+        kea_probes.check(kea_probes.lib().kea_probe_spin(spin, stream.cuda_stream), "kea_probe_spin")
         start.record(stream)
         for i in range(steps):
             fn(i)
@@ -197,8 +197,7 @@ def launch_floors(d, stream, tile_name: str, reps: int = 10, shape=(M, N, K), wa
     shape's q (int8 [m][k]), native 1-bit words and fp16 y."""
     import ctypes
     import torch
-    from kea_kernels import _hip
-    L = _hip.lib()
+    L = kea_probes.lib()
     m, n, k = shape
     bm, bn = (int(v) for v in tile_name.split()[0].split("x"))
     vp = ctypes.c_void_p
@@ -209,7 +208,7 @@ def launch_floors(d, stream, tile_name: str, reps: int = 10, shape=(M, N, K), wa
             rc = L.kea_probe_floor_waves(kind, m, n, k, bm, bn, waves, vp(d["q"].data_ptr()),
                                          vp(d["words"].data_ptr()), vp(y.data_ptr()), n,
                                          vp(torch.cuda.current_stream().cuda_stream))
-            _hip.check(rc, "kea_probe_floor")
+            kea_probes.check(rc, "kea_probe_floor")
         graph = capture(stream, probe, 100)
         replay_timed(stream, [graph])
         out[name] = round(replay_timed(stream, [graph], reps) * 1000 / (100 * reps), 3)
@@ -231,10 +230,10 @@ def probes() -> None:
       workgroup (how the cost of moving the operands depends on the grid)."""
     import ctypes
     import torch
-    from kea_kernels import _hip, lowbit
+    from kea_kernels import lowbit
     from kea_kernels.binary import bits, kernels
     from kea_kernels.binary.kernels import GemmConfig
-    L = _hip.lib()
+    L = kea_probes.lib()
     dev = torch.device("cuda", 0)
     vp = ctypes.c_void_p
     stream = torch.cuda.Stream(dev)
@@ -262,7 +261,7 @@ def probes() -> None:
             def run(blocks=blocks, ops_t=ops_t):
                 rc = L.kea_probe_mfma_i8_operands(blocks, iters, vp(ops_t.data_ptr() if ops_t is not None else 0),
                                                   vp(out.data_ptr()), vp(stream.cuda_stream))
-                _hip.check(rc, "kea_probe_mfma_i8_operands")
+                kea_probes.check(rc, "kea_probe_mfma_i8_operands")
             t = best_of(run)
             print(json.dumps({"probe": "mfma", "operands": data, "waves_per_simd": blocks // 256,
                               "tops": round(L.kea_probe_mfma_i8_ops(blocks, iters) / t / 1e12, 1)}), flush=True)
@@ -280,7 +279,7 @@ def probes() -> None:
                         rc = L.kea_probe_exchange(kind, wgs, words, group, vp(slots.data_ptr()),
                                                   vp(counters.data_ptr()), vp(result.data_ptr()),
                                                   vp(torch.cuda.current_stream().cuda_stream))
-                        _hip.check(rc, "kea_probe_exchange")
+                        kea_probes.check(rc, "kea_probe_exchange")
                     graph = capture(stream, launch, 100)
                     replay_timed(stream, [graph])
                     row[name] = round(replay_timed(stream, [graph], 5) * 1000 / 500, 3)
@@ -325,8 +324,7 @@ def measured_peaks(reps: int = 5) -> dict:
     it), and a 1 GiB device-to-device copy (read + write bytes). Best of `reps` event-timed launches each."""
     import ctypes
     import torch
-    from kea_kernels import _hip
-    L = _hip.lib()
+    L = kea_probes.lib()
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream(dev)
     blocks, iters = 2048, 2000
@@ -349,8 +347,7 @@ def measured_peaks(reps: int = 5) -> dict:
     def mfma(operands):
         rc = L.kea_probe_mfma_i8_operands(blocks, iters, ctypes.c_void_p(operands), ctypes.c_void_p(out.data_ptr()),
                                           ctypes.c_void_p(stream.cuda_stream))
-        if rc != 0:
-            raise RuntimeError(f"kea_probe_mfma_i8: {L.kea_last_error().decode()}")
+        kea_probes.check(rc, "kea_probe_mfma_i8_operands")
 
     t_pattern = timed(lambda: mfma(None))
     t_random = timed(lambda: mfma(random_words.data_ptr()))

@@ -16,14 +16,14 @@
  *
  * Reference interfaces replaced (paths relative to the reference checkout, kk/ = src/kea_kernels/):
  *   kea_lowbit_gemm    <- the NVRTC kernel entry `b1_dot_*` (kk/binary/kernels.py:556-565) launched by
- *                         kk/binary/layer.py:182-201 and kk/binary/layer_parts.py:322-340, the fallback
+ *                         kk/binary/layer.py:182-201 and kk/binary/layer_parts.py:112-130, the fallback
  *                         `b1_fallback` (kk/binary/kernels.py:619-637), and the ternary Triton `_int8_dot` +
  *                         `_finish` pair (kk/ternary/fused_kernels.py:53-120, kk/ternary/kernels.py:122-137)
  *   kea_b1_relayout_host / kea_b1_unlayout_host
  *                      <- `relayout` / `unlayout` (kk/binary/kernels.py:730-752), re-targeted to the gfx950
  *                         native word layout described below
  *   kea_t2_relayout_host / kea_t2_unlayout_host
- *                      <- the int32 `packed_t` words of PackedLinear (kk/ternary/runtime.py:182-184) and the
+ *                      <- the int32 `packed_t` words of PackedLinear (kk/ternary/runtime.py:33-35) and the
  *                         one-time `_expand` (kk/ternary/encoder4.py:51-61): the 2-bit codes stay resident
  *   kea_quantize       <- `b1_quantize` (kk/binary/kernels.py:578-616) and the Triton `_quantize`
  *                         (kk/ternary/fused_kernels.py:31-50), with LayerNorm / input SiLU fused
@@ -259,52 +259,6 @@ int kea_quantize(const void *x_dev, int x_dtype, int64_t xb, int64_t xt, int64_t
                  int64_t m, int64_t k, int parts,
                  const float *norm_w_dev, const float *norm_b_dev, float eps, int input_silu,
                  int8_t *q_dev, int64_t ldq, void *qs_dev, int qs_dtype, void *stream);
-
-/* ---------------------------------------------------------------------------------------------------------
- * Row-quantizing GEMM: the activation quantizer and kea_lowbit_gemm in one launch, for the small-M calls whose time
- * is set by launches. Each workgroup quantizes the FP32 rows of its 16-row tile into `parts` residual int8 parts in
- * registers (f32 scales) and multiplies them as kea_lowbit_gemm does; codes and scales are bitwise those of the
- * two-launch path named per mode, so y is bitwise that path's result:
- *   KEA_ROWS_PLAIN  rows x                                  = kea_quantize (no LayerNorm, no SiLU), then the GEMM
- *   KEA_ROWS_NORM   LayerNorm0(x)                           = kea_quantize with norm0_w / norm0_b / eps0
- *   KEA_ROWS_NORM2  x_out = LayerNorm0(x) is stored, then LayerNorm1(x_out) = kea_norm_quantize
- *   KEA_ROWS_MERGE  the key-split attention output left in a kea_relpos_attention_ws workspace (x = workspace,
- *                   ws_bytes its size, heads its heads, k = heads * 128; m = batch * t) = kea_attention_merge_quantize
- * The reference runs the quantizer as its own kernel before the GEMM (m1_quantize_parts / b1_quantize then b1_dot,
- * kk/binary/kernels.py:567-616 and :556-565; the row fusions of kk/ternary/row_fusion.py:121-152 quantize the next
- * projection's input at the end of the previous one); this entry point has no counterpart there.
- *   k = 1024 for every mode; KEA_ROWS_PLAIN also k = 2048 and 4096 (the whole row is held by one workgroup's waves).
- *   x 16-byte aligned rows (ldx % 4 == 0, ldx >= k); LayerNorm parameters FP32 [k], 16-byte aligned; x_out [m][ld_out]
- *   likewise, not overlapping x. y must not overlap x (other workgroups still read x while y is written); y may be the
- *   residual itself. parts 1..3 (fewer where the registers do not fit: KEA_EINVAL says so). Epilogue arguments
- *   (wscale, bias, y, flags, residual) as kea_lowbit_gemm_residual, per-channel scales only. config 0 = the library's
- *   choice, else a wave-split tile id whose blocks are 16 rows.
- * --------------------------------------------------------------------------------------------------------- */
-#define KEA_ROWS_PLAIN 0
-#define KEA_ROWS_NORM 1
-#define KEA_ROWS_NORM2 2
-#define KEA_ROWS_MERGE 3
-
-typedef struct kea_rows {
-    int mode;                          /* KEA_ROWS_* */
-    const float *x;                    /* FP32 rows [m][ldx]; KEA_ROWS_MERGE: the attention workspace */
-    int64_t ldx;
-    const float *norm0_w, *norm0_b;    /* NORM, NORM2 */
-    float eps0;
-    float *x_out;                      /* NORM2: LayerNorm0(x) [m][ld_out] */
-    int64_t ld_out;
-    const float *norm1_w, *norm1_b;    /* NORM2 */
-    float eps1;
-    int heads;                         /* MERGE */
-    int64_t ws_bytes;                  /* MERGE */
-} kea_rows;
-
-int kea_lowbit_gemm_rows(int wbits, const kea_rows *rows, int parts,
-                         const uint32_t *w_dev, int64_t n, int64_t k,
-                         const void *wscale_dev, int ws_dtype, const void *bias_dev, int bias_dtype,
-                         void *y_dev, int y_dtype, int64_t ldy,
-                         const float *residual_dev, int64_t ldr, float factor,
-                         int64_t m, int flags, int config, void *stream);
 
 /* Message of the calling thread's last failure ("" if none). */
 const char *kea_last_error(void);

@@ -1,8 +1,9 @@
-/* Measurement helpers of libkea_hip.so: kernels that measure what the MI355X sustains, so that benchmark figures can be
- * stated against measured peaks as well as against the published ones. They have no counterpart in the reference
- * (which quotes no measured peaks); their callers are the benchmark and the tests. Same conventions as
- * kea_lowbit.h: device pointers, a hipStream_t as void*, 0 on success, negative on a contract violation (nothing
- * launched, message in kea_last_error()), positive hipError_t on a launch failure. */
+/* Measurement helpers of libkea_probe.so, the benchmark's own library (kea-kernels_amd/kea_probes/, built with
+ * libkea_hip.so but not linked into it): kernels that measure what the MI355X sustains, so that benchmark figures can
+ * be stated against measured peaks and launch floors as well as against the published peaks. They have no counterpart
+ * in the reference (which quotes no measured peaks); their callers are bench.py and the tests. Same conventions as
+ * kea_lowbit.h: device pointers, a hipStream_t as void*, 0 on success, negative KEA_E* status on a contract violation
+ * (nothing launched, message in kea_probe_last_error()), positive hipError_t on a launch failure. */
 #ifndef KEA_PROBE_H
 #define KEA_PROBE_H
 
@@ -11,6 +12,9 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* Message of the calling thread's last probe failure ("" if none). */
+const char *kea_probe_last_error(void);
 
 /* Dense int8 matrix-core loop: `blocks` workgroups of four wave64s, each wave issuing `iters` rounds of eight
  * independent v_mfma_i32_16x16x64_i8 (32768 int8 ops each) on register operands, then one int32 per thread to

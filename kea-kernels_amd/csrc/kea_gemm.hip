@@ -30,11 +30,9 @@
 #include "kea_epilogue.h"
 #include "kea_gemm_common.h"
 #include "kea_gemm_ring.h"
-#include "kea_gemm_rows.h"
 #include "kea_gemm_table.h"
 #include "kea_gemm_wsplit.h"
 #include "kea_internal.h"
-#include "kea_merge.h"
 
 namespace kea {
 
@@ -588,133 +586,7 @@ int kea_lowbit_gemm_residual(int wbits, const int8_t *q, int64_t part_stride, in
 
 }  // extern "C"
 
-namespace {
-
-// Whether the byte ranges [a, a + na) and [b, b + nb) share a byte.
-bool overlaps(const void *a, int64_t na, const void *b, int64_t nb) {
-    const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
-    return na > 0 && nb > 0 && a0 < b0 + (uint64_t)nb && b0 < a0 + (uint64_t)na;
-}
-
-bool aligned16(const void *v) { return ((uintptr_t)v & 15) == 0; }
-
-// The row-quantizing tile for k: four waves of 4 k-steps at k = 1024 (16x32 up to n = 1024, else 16x64), eight waves
-// of 4 or 8 k-steps (16x64) at k = 2048 / 4096. Index into kWsplitTiles.
-int rows_tile(int64_t n, int64_t k) {
-    if (k == 1024) return n <= 1024 ? 5 : 2;
-    return 7;
-}
-
-}  // namespace
-
 extern "C" {
-
-int kea_lowbit_gemm_rows(int wbits, const kea_rows *rows, int parts, const uint32_t *w, int64_t n, int64_t k,
-                         const void *wscale, int ws_dtype, const void *bias, int bias_dtype, void *y, int y_dtype,
-                         int64_t ldy, const float *residual, int64_t ldr, float factor, int64_t m, int flags,
-                         int config, void *stream) {
-    if (!rows) return kea::fail(KEA_EINVAL, "rows is required");
-    const int mode = rows->mode;
-    if (mode < KEA_ROWS_PLAIN || mode > KEA_ROWS_MERGE) return kea::fail(KEA_EINVAL, "unknown rows mode");
-    if (wbits != 1 && wbits != 2) return kea::fail(KEA_EINVAL, "wbits must be 1 or 2");
-    if (parts < 1 || parts > 3) return kea::fail(KEA_EINVAL, "parts must be 1, 2 or 3");
-    if (m < 0 || n < 1 || m > INT32_MAX || n > INT32_MAX) return kea::fail(KEA_EINVAL, "bad sizes");
-    if (k != 1024 && !(mode == KEA_ROWS_PLAIN && (k == 2048 || k == 4096)))
-        return kea::fail(KEA_EINVAL, "k must be 1024 (KEA_ROWS_PLAIN: 1024, 2048 or 4096)");
-    if (config && (config <= kNumTiles || config > kNumTiles + kNumWsplitTiles))
-        return kea::fail(KEA_EINVAL, "config must be 0 or a wave-split tile id");
-    if (flags & ~(KEA_FLAG_SILU | KEA_FLAG_ORDER | KEA_FLAG_GLU)) return kea::fail(KEA_EINVAL, "unknown flags");
-    const bool glu = (flags & KEA_FLAG_GLU) != 0;
-    if (glu && ((flags & KEA_FLAG_SILU) || residual || (n & 1)))
-        return kea::fail(KEA_EINVAL, "GLU pairs need an even n, no SiLU and no residual");
-    if (!w || !wscale || !y) return kea::fail(KEA_EINVAL, "w, wscale and y are required");
-    if (ws_dtype != KEA_F32 && ws_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "wscale dtype must be f32 or f16");
-    if (bias && bias_dtype != KEA_F32 && bias_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "bias dtype must be f32 or f16");
-    if (y_dtype != KEA_F32 && y_dtype != KEA_F16 && y_dtype != KEA_BF16)
-        return kea::fail(KEA_EINVAL, "y dtype must be f32, f16 or bf16");
-    const int64_t ycols = glu ? n / 2 : n;
-    if (ldy < ycols) return kea::fail(KEA_EINVAL, glu ? "ldy < n / 2" : "ldy < n");
-    if (residual && ldr < n) return kea::fail(KEA_EINVAL, "ldr < n");
-
-    const int idx = config ? config - kNumTiles - 1 : rows_tile(n, k);
-    const WsplitTile &wt = kWsplitTiles[idx];
-    const int s = (int)(k / 64 / wt.nw);
-    const RowsFn fn = wt.rm != 1 || (int64_t)s * wt.nw * 64 != k ? nullptr
-                    : parts == 1 ? kea::rows_pick_p1(wbits, mode, idx, s)
-                    : parts == 2 ? kea::rows_pick_p2(wbits, mode, idx, s)
-                                 : kea::rows_pick_p3(wbits, mode, idx, s);
-    if (!fn)
-        return kea::fail(KEA_EINVAL, std::string("no row-quantizing kernel for tile ") + wt.name + " with " +
-                                         std::to_string(parts) + " parts in this mode at k = " + std::to_string(k));
-    if (m == 0) return KEA_OK;
-
-    // the source rows (or the attention workspace) and the buffers written while other workgroups still read them
-    const int esz = y_dtype == KEA_F32 ? 4 : 2;
-    const int64_t ybytes = ((m - 1) * ldy + ycols) * esz;
-    int64_t xbytes;
-    if (mode == KEA_ROWS_MERGE) {
-        if (rows->heads < 1 || (int64_t)rows->heads * 128 != k)
-            return kea::fail(KEA_EINVAL, "KEA_ROWS_MERGE needs k = heads * 128");
-        xbytes = kea::split_ws_floats(m, rows->heads) * 4;
-        if (!rows->x || rows->ws_bytes < xbytes)
-            return kea::fail(KEA_ESPACE, "attention workspace too small: need " + std::to_string(xbytes) + " bytes");
-    } else {
-        if (!rows->x) return kea::fail(KEA_EINVAL, "x is required");
-        if (rows->ldx < k || (rows->ldx & 3)) return kea::fail(KEA_EINVAL, "ldx must be >= k and a multiple of 4");
-        xbytes = ((m - 1) * rows->ldx + k) * 4;
-    }
-    if (!aligned16(rows->x) || !aligned16(w)) return kea::fail(KEA_EALIGN, "x and w must be 16-byte aligned");
-    if (mode == KEA_ROWS_NORM || mode == KEA_ROWS_NORM2) {
-        if (!rows->norm0_w || !rows->norm0_b) return kea::fail(KEA_EINVAL, "norm0_w and norm0_b are required");
-        if (!aligned16(rows->norm0_w) || !aligned16(rows->norm0_b))
-            return kea::fail(KEA_EALIGN, "LayerNorm parameters must be 16-byte aligned");
-    }
-    if (mode == KEA_ROWS_NORM2) {
-        if (!rows->norm1_w || !rows->norm1_b || !rows->x_out)
-            return kea::fail(KEA_EINVAL, "norm1_w, norm1_b and x_out are required");
-        if (!aligned16(rows->norm1_w) || !aligned16(rows->norm1_b) || !aligned16(rows->x_out))
-            return kea::fail(KEA_EALIGN, "LayerNorm parameters and x_out must be 16-byte aligned");
-        if (rows->ld_out < k || (rows->ld_out & 3))
-            return kea::fail(KEA_EINVAL, "ld_out must be >= k and a multiple of 4");
-        const int64_t obytes = ((m - 1) * rows->ld_out + k) * 4;
-        if (overlaps(rows->x_out, obytes, rows->x, xbytes) || overlaps(rows->x_out, obytes, y, ybytes))
-            return kea::fail(KEA_EINVAL, "x_out must not overlap x or y");
-    }
-    if (overlaps(y, ybytes, rows->x, xbytes)) return kea::fail(KEA_EINVAL, "y must not overlap the source rows");
-    if (!kea::fits_dispatch(cdivl(n, wt.nt * 16), wt.nw * 64) || !kea::fits_dispatch(cdivl(m, 16), 1))
-        return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N or M");
-
-    Params p{};
-    p.w = w; p.ws = wscale; p.ws_dtype = ws_dtype;
-    p.bias = bias; p.bias_dtype = bias_dtype;
-    p.y = y; p.ldy = ldy; p.y_dtype = y_dtype;
-    p.res = residual; p.ldr = ldr; p.res_factor = factor;
-    p.M = (int)m; p.N = (int)n; p.K = (int)k;
-    p.J = (int)(wbits == 1 ? cdivl(k, 128) : cdivl(k, 64));
-    p.NT = (int)cdivl(n, 16);
-    p.flags = flags;
-    const int yv = glu ? 2 : 4;
-    p.y_vec = (ldy % yv == 0) && ((uintptr_t)y % (yv * esz) == 0);
-    p.ws_vec = ((uintptr_t)wscale % (ws_dtype == KEA_F16 ? 8 : 16)) == 0;
-    p.bias_vec = bias && ((uintptr_t)bias % (bias_dtype == KEA_F16 ? 8 : 16)) == 0;
-    p.nw0 = rows->norm0_w; p.nb0 = rows->norm0_b; p.eps0 = rows->eps0;
-    p.nw1 = rows->norm1_w; p.nb1 = rows->norm1_b; p.eps1 = rows->eps1;
-    p.x_out = rows->x_out; p.ld_out = rows->ld_out;
-    p.heads = rows->heads;
-
-    const int lds = kea::rows_lds_bytes(parts, wt, s);
-    if (lds > 65536) {
-        const hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-        if (e != hipSuccess) return kea::fail((int)e, std::string("LDS attribute refused: ") + hipGetErrorString(e));
-    }
-    const int meta = (ws_dtype == KEA_F16 ? 2 : 0) | (bias && bias_dtype == KEA_F16 ? 4 : 0);
-    const dim3 grid((unsigned)cdivl(n, wt.nt * 16), (unsigned)cdivl(m, 16));
-    hipLaunchKernelGGL(fn, grid, dim3(wt.nw * 64), lds, (hipStream_t)stream, rows->x, w, wscale, (int)m, (int)n,
-                       (int)k, mode == KEA_ROWS_MERGE ? 0 : (int)rows->ldx, meta, p);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return kea::fail((int)e, std::string("gemm launch failed: ") + hipGetErrorString(e));
-    return KEA_OK;
-}
 
 int kea_lowbit_gemm_slices(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts,
                            const uint32_t *w, int64_t n, int64_t k, int64_t m, int split, int config,

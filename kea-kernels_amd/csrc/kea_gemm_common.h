@@ -42,12 +42,6 @@ struct Params {
     int gp_shift;   // log2 of the padded group count held in LDS (a power of two >= the groups the stages span)
     int ws_vec, bias_vec;  // 1: per-channel scales / bias allow aligned 4-element vector loads
     int steps_per_slice;   // wave-split kernel: k-steps of 64 per workgroup (one K slice)
-    // row-quantizing kernel: LayerNorm parameters, the stored LayerNorm0 output, the attention workspace's heads
-    const float *nw0, *nb0, *nw1, *nb1;
-    float eps0, eps1;
-    float *x_out;
-    long long ld_out;
-    int heads;
 };
 
 // 1-bit: plane (4h + d) of a native word -> four int8 weights. Stored bits are inverted signs, so after the mask

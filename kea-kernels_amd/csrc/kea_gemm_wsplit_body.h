@@ -1,7 +1,5 @@
-// The parts of the wave-split GEMM that do not depend on where the activation fragments come from, shared by the
-// int8-input kernel (kea_gemm_wsplit_inst.h) and the kernel that quantizes FP32 rows itself (kea_gemm_rows_inst.h):
-// the weight loads, the MFMA sequence, the exact LDS reduction over the waves and the epilogue dispatch of one
-// 16x16 block. Every function is force-inlined over compile-time shapes, so the arrays stay in registers.
+// The building blocks of the wave-split GEMM (kea_gemm_wsplit_inst.h): the weight loads, the MFMA sequence, the exact
+// LDS reduction over the waves and the epilogue dispatch of one 16x16 block. Every function is force-inlined over compile-time shapes, so the arrays stay in registers.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -2,7 +2,7 @@
 //
 // The export layouts are the reference's on-disk formats (kk/binary/bits.py:3-5, kk/formats.py:5-7); the native
 // layouts are this library's own (declared in include/kea_lowbit.h). Their role matches the reference's one-time
-// `relayout` (kk/binary/kernels.py:730-742) and the ternary `packed_t` transposition (kk/ternary/runtime.py:182-184):
+// `relayout` (kk/binary/kernels.py:730-742) and the ternary `packed_t` transposition (kk/ternary/runtime.py:33-35):
 // rearrange the codes once so that the GEMM reads each wavefront's weights with one coalesced 128-bit load per lane
 // and expands them to int8 MFMA operands with a mask and a byte permute.
 #include <cstdint>

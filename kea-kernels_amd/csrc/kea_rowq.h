@@ -1,5 +1,6 @@
-// The per-element step of the residual int8 activation quantizer, shared by the quantizer kernels (kea_quantize.hip)
-// and the GEMM that quantizes its FP32 rows itself (kea_gemm_rows_inst.h), so both produce the same codes.
+// The per-element step of the residual int8 activation quantizer, shared by the quantizer kernels of kea_quantize.hip
+// (the plain row quantizer and the fused LayerNorm / GLU-convolution / attention-merge quantizers), so all of them
+// produce the same codes.
 // Translation units that include it are built with -ffp-contract=off.
 #pragma once
 

@@ -26,16 +26,6 @@ DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 # (name, restype, argtypes) of every exported function
 _i32, _i64, _vp, _f32, _cp = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_char_p
 
-ROWS_PLAIN, ROWS_NORM, ROWS_NORM2, ROWS_MERGE = 0, 1, 2, 3
-
-
-class Rows(ctypes.Structure):
-    """struct kea_rows: the FP32 source rows of kea_lowbit_gemm_rows and the quantizer in front of its GEMM."""
-    _fields_ = [("mode", _i32), ("x", _vp), ("ldx", _i64), ("norm0_w", _vp), ("norm0_b", _vp), ("eps0", _f32),
-                ("x_out", _vp), ("ld_out", _i64), ("norm1_w", _vp), ("norm1_b", _vp), ("eps1", _f32),
-                ("heads", _i32), ("ws_bytes", _i64)]
-
-
 SIGNATURES = {
     "kea_b1_native_words": (_i64, [_i64, _i64]),
     "kea_t2_native_words": (_i64, [_i64, _i64]),
@@ -55,8 +45,6 @@ SIGNATURES = {
     "kea_lowbit_gemm_residual": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _vp, _i32,
                                         _i64, _vp, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _i32, _i32, _i32, _vp,
                                         _i64, _vp, _i64, _f32, _vp]),
-    "kea_lowbit_gemm_rows": (_i32, [_i32, ctypes.POINTER(Rows), _i32, _vp, _i64, _i64, _vp, _i32, _vp, _i32, _vp,
-                                    _i32, _i64, _vp, _i64, _f32, _i64, _i32, _i32, _vp]),
     "kea_lowbit_gemm_slices": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _vp]),
     "kea_lowbit_slices_finish": (_i32, [_vp, _i32, _i32, _i64, _i64, _vp, _i32, _i64, _vp, _i32, _vp, _i32, _vp,
                                         _i32, _i64, _vp, _i64, _i32, _vp]),
@@ -85,13 +73,6 @@ SIGNATURES = {
     "kea_dwconv2d_s2": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "kea_bias_relu_flatten": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "kea_dwconv_quantize": (_i32, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _i64, _vp, _vp]),
-    "kea_probe_mfma_i8": (_i32, [_i64, _i64, _vp, _vp]),
-    "kea_probe_mfma_i8_ops": (_i64, [_i64, _i64]),
-    "kea_probe_mfma_i8_operands": (_i32, [_i64, _i64, _vp, _vp, _vp]),
-    "kea_probe_exchange": (_i32, [_i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
-    "kea_probe_floor": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _i64, _vp]),
-    "kea_probe_floor_waves": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _vp]),
-    "kea_probe_spin": (_i32, [_i64, _vp]),
     "kea_last_error": (_cp, []),
     "kea_version": (_i32, []),
 }

@@ -67,7 +67,7 @@ def _aligned(q: Tensor, k: int) -> tuple[Tensor, int]:
 
 def dot_parts(layer: Int8MmaLayer, q: Tensor, qs: Tensor, ldq: int, m: int, y: Tensor | None, *, silu: bool = False,
               config=None, order: int = 0, parts: int = 3, acc_out: Tensor | None = None) -> None:
-    """The P-part launch (kk/binary/layer_parts.py:322-340): y[:m] from q int8 [P, m, ldq] and qs [P, m]."""
+    """The P-part launch (kk/binary/layer_parts.py:112-130): y[:m] from q int8 [P, m, ldq] and qs [P, m]."""
     n, k = layer.out_features, layer.in_features
     if q.shape[0] != parts:
         raise ValueError(f"q must hold {parts} parts")

@@ -24,11 +24,8 @@ fused HIP kernels of include/kea_encoder.h (the reference's Triton relative_atte
 also applies the SiLU and quantizes for W_pw2 (kea_glu_dwconv_quantize). The four residual projections (W2 of both
 FFs, W_out, W_pw2) add the residual in their GEMM epilogue, in place (the reference's row_fusions,
 kk/ternary/row_fusion.py:121-152); the quantizers run as row kernels between the GEMMs (kea_quantize,
-kea_norm_quantize, kea_attention_merge_quantize), 17 launches a layer. With rows=True every projection but W_pw2
-quantizes its own FP32 input rows inside the GEMM launch instead (kea_lowbit_gemm_rows): W1 through its LayerNorm (at
-a layer boundary also the previous layer's output LayerNorm, which it stores as the new residual stream), W2 from W1's
-output, W_qkv and W_pw1 through theirs, W_out from the key-split attention halves: 10 launches a layer, the same bits,
-but slower (see FastConformerEncoder). The subsampling convolutions are PyTorch on the GPU.
+kea_norm_quantize, kea_attention_merge_quantize), 17 launches a layer. The subsampling convolutions are PyTorch on
+the GPU.
 With fused=False the same model runs with separate quantizers, the residual in the GEMM epilogue
 (kea_lowbit_gemm_residual) and PyTorch attention, GLU and convolution. The quantized linears have no bias
 (Q/K/V must be bias-free to fuse, kk/binary/provider.py:230-244).
@@ -435,21 +432,12 @@ class FastConformerEncoder:
     """audio [B, S] -> encoder output [B, T', d]. parts = int8 activation parts of every quantized linear (1 = the
     Kea-B x1 mode); dense=True swaps the quantized linears for FP32 dense matmuls (the parity reference);
     fused=False runs attention and the GLU + depthwise convolution as PyTorch ops instead of the fused HIP kernels
-    (the dense twin always does). rows=True (fused only): the projections quantize their FP32 input rows inside the
-    GEMM launch (lowbit.gemm_rows) where M <= ROWS_MAX_M, 10 launches a layer instead of 17, the same bits. It is off
-    by default because it is slower on MI355X: every workgroup quantizes its whole 16-row tile on the vector ALU
-    (16 x K elements at about a dozen instructions each, 64 lanes a clock per CU: 1.3-5 us), which costs more than
-    the separate quantizer launch it replaces (about 2.5 us in a graph); measured 3.1 ms against 1.8 ms per clip at
-    batch 1."""
-
-    # Largest M (batch x frames) at which rows=True applies.
-    ROWS_MAX_M = 256
+    (the dense twin always does)."""
 
     def __init__(self, weights: dict, cfg: EncoderConfig = EncoderConfig(), device="cuda", *, parts: int = 1,
-                 dense: bool = False, fused: bool = True, rows: bool = False):
+                 dense: bool = False, fused: bool = True):
         self.cfg, self.parts, self.dense = cfg, parts, dense
         self.fused = fused and not dense
-        self.rows = rows and self.fused
         self._sub_out = None
         self.device = device = torch.device(device)
         if device.type == "cuda" and device.index is None:
@@ -704,70 +692,6 @@ class FastConformerEncoder:
                          out_norm=fp["norm_out"])
         return x, xq
 
-    def _rows_gemm(self, name: str, x: Tensor, m: int, *, y: Tensor | None = None, norm=None, next_norm=None,
-                   x_out: Tensor | None = None, merge: tuple | None = None, silu: bool = False, glu: bool = False,
-                   residual_factor: float | None = None) -> Tensor:
-        """The quantized linear `name` on FP32 rows x ([m, K] or [B, T, K]; with merge = (B, T), the key-split
-        attention workspace of relpos_attention(..., merged=False)), quantized inside the GEMM launch
-        (lowbit.gemm_rows) through norm (and next_norm, storing x_out = norm(x)) where the library has that kernel,
-        else by the separate quantizer first (the same bits). residual_factor: y += factor * linear(x) in place (y
-        is the residual stream [m, N]); else y is allocated."""
-        layer = self._layer(name)
-        n, k = layer.out_features, layer.in_features
-        if y is None:
-            y = torch.empty(m, n // 2 if glu else n, device=self.device, dtype=torch.float32)
-        residual = None if residual_factor is None else y
-        mode = (_hip.ROWS_MERGE if merge is not None else _hip.ROWS_NORM2 if next_norm is not None
-                else _hip.ROWS_NORM if norm is not None else _hip.ROWS_PLAIN)
-        rows = x if merge is not None else x.reshape(m, k)
-        if lowbit.rows_supported(layer.WBITS, mode, self.parts, n, k):
-            lowbit.gemm_rows(layer.WBITS, rows, layer.words, n, k, layer.scale, layer.bias, y, m=m, parts=self.parts,
-                             norm=norm, next_norm=next_norm, x_out=None if x_out is None else x_out.view(m, k),
-                             merge_heads=self.cfg.heads if merge is not None else 0, residual=residual,
-                             residual_factor=1.0 if residual_factor is None else residual_factor, silu=silu, glu=glu)
-            return y
-        if merge is not None:
-            q, qs = attention_merge_quantize(x, merge[0], merge[1], self.cfg.heads, self.parts)
-        elif next_norm is not None:
-            _, q, qs = norm_quantize(rows.view(1, m, k), norm, next_norm, self.parts, out=x_out.view(1, m, k))
-        else:
-            q, qs = self._quantize(rows, norm=norm)
-        lowbit.gemm(layer.WBITS, q, qs, layer.words, n, k, layer.scale, layer.bias, y, None, m=m, silu=silu, glu=glu,
-                    residual=residual, residual_factor=1.0 if residual_factor is None else residual_factor)
-        return y
-
-    def _layer_quantizing_rows(self, i: int, r: Tensor, pos: Tensor) -> Tensor:
-        """Layer i with every projection but W_pw2 quantizing its own input rows in the GEMM launch: 10 launches
-        (W1, W2, W_qkv, attention, W_out, W_pw1, GLU-convolution quantizer, W_pw2, W1, W2). r: the layer's input
-        before the previous layer's output LayerNorm (the subsampled features for layer 0). Returns this layer's
-        residual stream before its own output LayerNorm, which the next layer's W1 applies and stores."""
-        fp = self.layers[i]
-        pre = f"encoder.layers.{i}."
-        b, t, d = r.shape
-        m = b * t
-        if i == 0:
-            x = r
-            y = self._rows_gemm(pre + "feed_forward1.linear1", x, m, norm=fp["norm_feed_forward1"], silu=True)
-        else:
-            x = torch.empty_like(r)
-            y = self._rows_gemm(pre + "feed_forward1.linear1", r, m, norm=self.layers[i - 1]["norm_out"],
-                                next_norm=fp["norm_feed_forward1"], x_out=x, silu=True)
-        x2 = x.view(m, d)
-        self._rows_gemm(pre + "feed_forward1.linear2", y, m, y=x2, residual_factor=0.5)
-        qkv = self._rows_gemm(pre + "self_attn.qkv", x, m, norm=fp["norm_self_att"]).view(b, t, -1)
-        ws = self._attention_ws(b, t) if d // self.cfg.heads == 128 else None
-        if ws is not None:
-            relpos_attention(qkv, pos, fp["u"], fp["v"], self.cfg.heads, workspace=ws, merged=False)
-            self._rows_gemm(pre + "self_attn.linear_out", ws, m, y=x2, merge=(b, t), residual_factor=1.0)
-        else:
-            self._rows_gemm(pre + "self_attn.linear_out", self.attention(qkv, pos, fp["u"], fp["v"]), m, y=x2,
-                            residual_factor=1.0)
-        u = self._rows_gemm(pre + "conv.pointwise_conv1", x, m, norm=fp["norm_conv"], glu=True).view(b, t, -1)
-        self._block(pre + "conv.pointwise_conv2", *dwconv_quantize(u, fp["dw_w"], fp["dw_b"], self.parts), x, 1.0)
-        y = self._rows_gemm(pre + "feed_forward2.linear1", x, m, norm=fp["norm_feed_forward2"], silu=True)
-        self._rows_gemm(pre + "feed_forward2.linear2", y, m, y=x2, residual_factor=0.5)
-        return x
-
     def layer(self, i: int, x: Tensor, pos: Tensor, xq=None) -> Tensor | tuple:
         """One layer. Fused (quantized, fused=True): returns (x, xq) with x updated in place and xq = (q, qs) the
         next layer's quantized input (None after the last layer). Otherwise returns the layer output."""
@@ -794,11 +718,6 @@ class FastConformerEncoder:
         if self.cfg.xscaling and not self.fused:  # the fused subsampling applies it in its output linear
             x = x * math.sqrt(self.cfg.d_model)
         pos = self.positions(x.shape[1])
-        if self.rows and x.shape[0] * x.shape[1] <= self.ROWS_MAX_M:
-            for i in range(self.cfg.layers):
-                x = self._layer_quantizing_rows(i, x, pos[i])
-            out_norm = self.layers[-1]["norm_out"]  # its quantization is not used
-            return norm_quantize(x, out_norm, out_norm, 1, out=x)[0]
         xq = None
         for i in range(self.cfg.layers):
             out = self.layer(i, x, pos[i], xq)

@@ -117,9 +117,20 @@ def read_manifest(directory: Path) -> dict:
     return json.loads(path.read_text())
 
 
+# bytes per element of the safetensors dtype strings
+_ST_DTYPE_BYTES = {"BOOL": 1, "U8": 1, "I8": 1, "F8_E4M3": 1, "F8_E5M2": 1, "U16": 2, "I16": 2, "F16": 2, "BF16": 2,
+                   "U32": 4, "I32": 4, "F32": 4, "U64": 8, "I64": 8, "F64": 8}
+
+
 def safetensors_header(path: Path) -> dict:
     """The header of a safetensors file without reading any tensor: its first 8 bytes are the little-endian length of
-    a UTF-8 JSON object mapping each tensor name to {"dtype", "shape", "data_offsets"}, plus "__metadata__"."""
+    a UTF-8 JSON object mapping each tensor name to {"dtype", "shape", "data_offsets"}, plus "__metadata__".
+
+    The header is checked against the file as a safetensors reader checks it before handing out tensors: a JSON
+    object; every tensor's byte range [begin, end) relative to the data buffer holds exactly its elements; the ranges,
+    in order, tile the buffer from 0 to its end with no gap or overlap; and the buffer ends where the file ends (a
+    truncated or extended file is rejected here, also when no SHA-256 is checked)."""
+    path = Path(path)
     with open(path, "rb") as handle:
         raw = handle.read(8)
         if len(raw) != 8:
@@ -127,11 +138,46 @@ def safetensors_header(path: Path) -> dict:
         (length,) = struct.unpack("<Q", raw)
         if length > (64 << 20):
             raise ValueError(f"{path}: implausible safetensors header length {length}")
-        header = handle.read(length)
+        text = handle.read(length)
+    if len(text) != length:
+        raise ValueError(f"{path}: truncated safetensors header")
     try:
-        return json.loads(header)
+        header = json.loads(text)
     except ValueError as exc:
         raise ValueError(f"{path}: unreadable safetensors header") from exc
+    if not isinstance(header, dict):
+        raise ValueError(f"{path}: the safetensors header is not a JSON object")
+    data_bytes = path.stat().st_size - 8 - length
+    ranges = []
+    for name, info in header.items():
+        if name == "__metadata__":
+            if info is not None and not isinstance(info, dict):
+                raise ValueError(f"{path}: __metadata__ is not a JSON object")
+            continue
+        if not isinstance(info, dict):
+            raise ValueError(f"{path}: tensor {name!r} has no dtype/shape/data_offsets")
+        dtype, shape, offsets = info.get("dtype"), info.get("shape"), info.get("data_offsets")
+        if (dtype not in _ST_DTYPE_BYTES or not isinstance(shape, list)
+                or not all(isinstance(d, int) and d >= 0 for d in shape)
+                or not isinstance(offsets, list) or len(offsets) != 2
+                or not all(isinstance(o, int) for o in offsets)):
+            raise ValueError(f"{path}: tensor {name!r} has an invalid dtype, shape or data_offsets")
+        begin, end = offsets
+        count = 1
+        for d in shape:
+            count *= d
+        if not 0 <= begin <= end or end - begin != count * _ST_DTYPE_BYTES[dtype]:
+            raise ValueError(f"{path}: tensor {name!r}: data_offsets {offsets} do not hold a {dtype} {shape}")
+        ranges.append((begin, end, name))
+    position = 0
+    for begin, end, name in sorted(ranges):
+        if begin != position:
+            raise ValueError(f"{path}: tensor {name!r} starts at byte {begin} of the data, expected {position}")
+        position = end
+    if position != data_bytes:
+        raise ValueError(f"{path}: the tensors cover {position} data bytes but the file holds {data_bytes} "
+                         "(truncated or corrupt)")
+    return header
 
 
 # describe(): one handler per manifest format

@@ -3,8 +3,7 @@
 `gemm` is the single launch path of every operator in this package (binary.layer, binary.layer_parts,
 ternary.fused_kernels): it checks tensors, resolves the split-K workspace from torch's caching allocator (as the
 reference does for its L2 workspace, kk/binary/layer.py:194-195) and enqueues kea_lowbit_gemm on the current stream.
-`quantize` enqueues kea_quantize; `gemm_rows` the GEMM that quantizes its FP32 rows itself (kea_lowbit_gemm_rows).
-None of them synchronizes the host.
+`quantize` enqueues kea_quantize. None of them synchronizes the host.
 """
 from __future__ import annotations
 
@@ -306,83 +305,3 @@ def quantize(x: Tensor, rows: tuple, m: int, k: int, parts: int, *, norm=None, i
                                  qs.data_ptr(), _hip.dtype_code(qs_dtype), _hip.stream_handle(x.device))
     _hip.check(rc, "kea_quantize")
     return q, qs, ldq
-
-
-def gemm_rows(wbits: int, x: Tensor, words: Tensor, n: int, k: int, wscale: Tensor, bias: Tensor | None, y: Tensor,
-              *, m: int | None = None, parts: int = 1, norm=None, next_norm=None, x_out: Tensor | None = None,
-              merge_heads: int = 0, residual: Tensor | None = None, residual_factor: float = 1.0,
-              silu: bool = False, glu: bool = False, order: int = 0, config: int = 0) -> None:
-    """gemm() of activations quantized in the same launch (kea_lowbit_gemm_rows), bitwise the two-launch result:
-      x FP32 [>= m, >= k] rows            -> the parts-part quantization of x           (as quantize(x))
-      norm                                -> of norm(x)                                 (as quantize(x, norm=norm))
-      norm, next_norm, x_out              -> x_out = norm(x) stored, then of next_norm(x_out) (as norm_quantize)
-      merge_heads = H, x the attention workspace of relpos_attention(..., merged=False) over m = B * T rows
-                                          -> of the merged attention output             (as attention_merge_quantize)
-    k = 1024 (plain rows: also 2048, 4096); f32 scales. y [>= m, >= N] (glu: N / 2) must not overlap x; residual and
-    the epilogue flags as gemm()."""
-    device = x.device
-    L = _hip.lib()
-    r = _hip.Rows()
-    if merge_heads:
-        if norm is not None or next_norm is not None or x_out is not None:
-            raise ValueError("merge_heads takes no LayerNorm and no x_out")
-        if m is None:
-            raise ValueError("merge_heads needs m (batch * T)")
-        if not x.is_contiguous():
-            raise ValueError("the attention workspace must be contiguous")
-        r.mode, r.heads, r.ws_bytes = _hip.ROWS_MERGE, int(merge_heads), x.numel() * x.element_size()
-    else:
-        if x.dtype != torch.float32 or x.dim() != 2 or x.stride(1) != 1 or x.shape[1] < k:
-            raise ValueError(f"x must be a row-major FP32 [M, >= {k}] view")
-        m = x.shape[0] if m is None else m
-        if m > x.shape[0]:
-            raise ValueError(f"m = {m} exceeds the {x.shape[0]} rows of x")
-        r.ldx = x.stride(0)
-        r.mode = _hip.ROWS_PLAIN
-        if next_norm is not None or x_out is not None:
-            if norm is None or next_norm is None or x_out is None:
-                raise ValueError("a stored LayerNorm needs norm, next_norm and x_out")
-            if x_out.dtype != torch.float32 or x_out.dim() != 2 or x_out.stride(1) != 1 or x_out.shape[0] < m \
-                    or x_out.shape[1] < k:
-                raise ValueError(f"x_out must be a row-major FP32 [>= {m}, >= {k}] view")
-            r.mode, r.x_out, r.ld_out = _hip.ROWS_NORM2, x_out.data_ptr(), x_out.stride(0)
-        elif norm is not None:
-            r.mode = _hip.ROWS_NORM
-    r.x = x.data_ptr()
-    # (parameter copies made here are freed after the enqueue: the caching allocator reuses them only for later work
-    # on this stream)
-    if norm is not None:
-        w0, b0, r.eps0 = _norm_params(norm, k, device)
-        r.norm0_w, r.norm0_b = w0.data_ptr(), b0.data_ptr()
-    if next_norm is not None:
-        w1, b1, r.eps1 = _norm_params(next_norm, k, device)
-        r.norm1_w, r.norm1_b = w1.data_ptr(), b1.data_ptr()
-    if wscale.dtype not in _SCALE_DTYPES or not wscale.is_contiguous() or wscale.numel() < n:
-        raise ValueError(f"weight scales must be contiguous f32 or f16 [{n}]")
-    if bias is not None and (bias.dtype not in _SCALE_DTYPES or not bias.is_contiguous() or bias.numel() != n):
-        raise ValueError("bias must be contiguous f32 or f16 [N]")
-    _check_words(words, n, k, wbits)
-    ny = n // 2 if glu else n
-    if y.dim() != 2 or y.shape[0] < m or y.shape[1] < ny or y.stride(1) != 1:
-        raise ValueError(f"y must be a row-major [>= {m}, >= {ny}] view")
-    if residual is not None and (residual.dtype != torch.float32 or residual.dim() != 2 or residual.shape[0] < m
-                                 or residual.shape[1] < n or residual.stride(1) != 1):
-        raise ValueError(f"residual must be a row-major FP32 [>= {m}, >= {n}] view")
-    _on(device, words, wscale, bias, y, residual, x_out)
-    rc = L.kea_lowbit_gemm_rows(
-        wbits, ctypes.byref(r), parts, words.data_ptr(), n, k, wscale.data_ptr(), _hip.dtype_code(wscale.dtype),
-        _hip.ptr(bias), _hip.dtype_code(bias.dtype) if bias is not None else 0, y.data_ptr(),
-        _hip.dtype_code(y.dtype), y.stride(0), _hip.ptr(residual), residual.stride(0) if residual is not None else 0,
-        float(residual_factor), m, int(silu) | (2 * int(order)) | (4 * int(glu)), int(config),
-        _hip.stream_handle(device))
-    _hip.check(rc, "kea_lowbit_gemm_rows")
-
-
-@functools.lru_cache(maxsize=256)
-def rows_supported(wbits: int, mode: int, parts: int, n: int, k: int) -> bool:
-    """Whether kea_lowbit_gemm_rows has a kernel for this weight width, KEA_ROWS_* mode, part count and shape (asked
-    of the library with m = 0, which checks everything but the buffers and launches nothing)."""
-    r = _hip.Rows(mode=mode, heads=k // 128)
-    rc = _hip.lib().kea_lowbit_gemm_rows(wbits, ctypes.byref(r), parts, 16, n, k, 16, _hip.F32, None, 0, 16,
-                                         _hip.F32, n, None, 0, 1.0, 0, 0, 0, None)
-    return rc == 0

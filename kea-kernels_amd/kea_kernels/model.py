@@ -76,8 +76,12 @@ def check_device(device) -> torch.device:
 def _binary_nemo(export: Path, manifest: dict, device, mode: str):
     """1-bit layers at the mode's part count (x1, x2, x3)."""
     from kea_kernels.binary import provider
+    from kea_kernels.binary.layer import Int8MmaLayer
     from kea_kernels.binary.layer_parts import LAYERS
-    model, _space = provider.load_binary_model(export, manifest, LAYERS[int(mode[1])], device)
+    parts = int(mode[1])
+    # three parts run on the full operator (its project() path), fewer on the P-part variants (kk/model.py:121-122)
+    layer_cls = Int8MmaLayer if parts == 3 else LAYERS[parts]
+    model, _space = provider.load_binary_model(export, manifest, layer_cls, device)
     return model
 
 
@@ -96,7 +100,7 @@ def load(path, device="cuda", mode: str | None = None, *, verify: bool = True) -
     device; RuntimeError when nemo_toolkit is missing."""
     info = formats.describe(path)
     modes = formats.BINARY_MODES if info.kind == "binary" else formats.TERNARY_MODES
-    mode = mode or info.default_mode
+    mode = info.default_mode if mode is None else mode
     if mode not in modes:
         raise ValueError(f"{info.name} supports modes {modes}, got {mode!r}")
     manifest = formats.check_export(info.export, info.kind, verify_hashes=verify)

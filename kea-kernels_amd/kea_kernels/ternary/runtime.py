@@ -2,7 +2,7 @@
 
 PackedLinear keeps the reference's resident form, `packed_t` = the export bytes padded to whole 32-bit words and
 transposed to int32 [ceil(K/16), N] (code k of row n at bits 2 * (k % 16) of packed_t[k // 16, n];
-kk/ternary/runtime.py:182-184), and adds `native`, the same codes in the gfx950 wavefront layout the int8 GEMM reads
+kk/ternary/runtime.py:33-35), and adds `native`, the same codes in the gfx950 wavefront layout the int8 GEMM reads
 (include/kea_lowbit.h). Both stay 2 bits per weight on the GPU.
 
 forward runs the int8 path: x is split into `parts` residual int8 parts (3 unless the mode says otherwise) and

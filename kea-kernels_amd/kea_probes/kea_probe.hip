@@ -1,14 +1,24 @@
-// Measurement helpers (include/kea_probe.h): a dense int8 matrix-core loop that measures the sustained MFMA rate, and
-// the launch floors of a GEMM-shaped grid (an empty kernel, and kernels that only move a GEMM tile's bytes).
+// Measurement helpers of the benchmark library libkea_probe.so (include/kea_probe.h), built beside the product library
+// libkea_hip.so but not part of it: a dense int8 matrix-core loop that measures the sustained MFMA rate, the launch
+// floors of a GEMM-shaped grid (an empty kernel, and kernels that only move a GEMM tile's bytes), the cost of a
+// cross-workgroup exchange and a bounded spin that keeps host submission out of a timed region.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 #include <string>
 
+#include "../../include/kea_lowbit.h"  // status codes (KEA_E*)
 #include "../../include/kea_probe.h"
-#include "kea_internal.h"
 
 namespace {
+
+// The calling thread's last failure message (kea_probe_last_error), kept apart from the product library's.
+thread_local std::string g_probe_error;
+
+int fail(int code, const std::string &message) {
+    g_probe_error = message;
+    return code;
+}
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -149,6 +159,8 @@ __global__ void __launch_bounds__(64) spin_kernel(unsigned long long ticks) {
 
 extern "C" {
 
+const char *kea_probe_last_error(void) { return g_probe_error.c_str(); }
+
 int64_t kea_probe_mfma_i8_ops(int64_t blocks, int64_t iters) {
     if (!probe_args_ok(blocks, iters)) return 0;
     return blocks * 4 * iters * kProbeChains * kOpsPerMfma;
@@ -156,14 +168,14 @@ int64_t kea_probe_mfma_i8_ops(int64_t blocks, int64_t iters) {
 
 int kea_probe_mfma_i8_operands(int64_t blocks, int64_t iters, const int32_t *operands, int32_t *out, void *stream) {
     if (!probe_args_ok(blocks, iters))
-        return kea::fail(KEA_EINVAL, "kea_probe_mfma_i8: blocks must be in [1, 65536] and iters in [1, 2^20]");
-    if (!out) return kea::fail(KEA_EINVAL, "kea_probe_mfma_i8: out is null");
-    if ((uintptr_t)out & 3) return kea::fail(KEA_EALIGN, "kea_probe_mfma_i8: out must be 4-byte aligned");
-    if ((uintptr_t)operands & 15) return kea::fail(KEA_EALIGN, "kea_probe_mfma_i8: operands must be 16-byte aligned");
+        return fail(KEA_EINVAL, "kea_probe_mfma_i8: blocks must be in [1, 65536] and iters in [1, 2^20]");
+    if (!out) return fail(KEA_EINVAL, "kea_probe_mfma_i8: out is null");
+    if ((uintptr_t)out & 3) return fail(KEA_EALIGN, "kea_probe_mfma_i8: out must be 4-byte aligned");
+    if ((uintptr_t)operands & 15) return fail(KEA_EALIGN, "kea_probe_mfma_i8: operands must be 16-byte aligned");
     hipLaunchKernelGGL(mfma_i8_loop, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (int)iters,
                        (const v4i *)operands, out);
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_mfma_i8: ") + hipGetErrorString(e));
+    if (e != hipSuccess) return fail((int)e, std::string("kea_probe_mfma_i8: ") + hipGetErrorString(e));
     return 0;
 }
 
@@ -172,31 +184,31 @@ int kea_probe_mfma_i8(int64_t blocks, int64_t iters, int32_t *out, void *stream)
 }
 
 int kea_probe_spin(int64_t ns, void *stream) {
-    if (ns < 0 || ns > 100000000LL) return kea::fail(KEA_EINVAL, "kea_probe_spin: ns must be in [0, 1e8]");
+    if (ns < 0 || ns > 100000000LL) return fail(KEA_EINVAL, "kea_probe_spin: ns must be in [0, 1e8]");
     int dev = 0, khz = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
-    if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_spin: ") + hipGetErrorString(e));
-    if (khz <= 0) return kea::fail(KEA_ENODEV, "kea_probe_spin: the device reports no wall-clock rate");
+    if (e != hipSuccess) return fail((int)e, std::string("kea_probe_spin: ") + hipGetErrorString(e));
+    if (khz <= 0) return fail(KEA_ENODEV, "kea_probe_spin: the device reports no wall-clock rate");
     const unsigned long long ticks = (unsigned long long)(ns * (long long)khz / 1000000LL);
     hipLaunchKernelGGL(spin_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, ticks);
     e = hipGetLastError();
-    if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_spin: ") + hipGetErrorString(e));
+    if (e != hipSuccess) return fail((int)e, std::string("kea_probe_spin: ") + hipGetErrorString(e));
     return 0;
 }
 
 int kea_probe_exchange(int kind, int64_t workgroups, int64_t words, int64_t group, void *slots, uint32_t *counters,
                        uint32_t *result, void *stream) {
     if (kind < KEA_EXCHANGE_WRITE || kind > KEA_EXCHANGE_FENCED)
-        return kea::fail(KEA_EINVAL, "kea_probe_exchange: kind must be 0 (write), 1 (count) or 2 (fenced)");
+        return fail(KEA_EINVAL, "kea_probe_exchange: kind must be 0 (write), 1 (count) or 2 (fenced)");
     if (workgroups < 1 || workgroups > 65536 || words < 1 || words > 65536 || group < 1 || group > workgroups)
-        return kea::fail(KEA_EINVAL, "kea_probe_exchange: workgroups and words must be in [1, 65536], group in "
+        return fail(KEA_EINVAL, "kea_probe_exchange: workgroups and words must be in [1, 65536], group in "
                                      "[1, workgroups]");
-    if (!slots || ((uintptr_t)slots & 15)) return kea::fail(KEA_EALIGN, "kea_probe_exchange: slots must be 16-byte aligned");
+    if (!slots || ((uintptr_t)slots & 15)) return fail(KEA_EALIGN, "kea_probe_exchange: slots must be 16-byte aligned");
     if (kind != KEA_EXCHANGE_WRITE && (!counters || ((uintptr_t)counters & 3)))
-        return kea::fail(KEA_EINVAL, "kea_probe_exchange: counting kinds need 4-byte aligned counters");
+        return fail(KEA_EINVAL, "kea_probe_exchange: counting kinds need 4-byte aligned counters");
     if (kind == KEA_EXCHANGE_FENCED && (!result || ((uintptr_t)result & 3)))
-        return kea::fail(KEA_EINVAL, "kea_probe_exchange: the fenced kind needs a 4-byte aligned result");
+        return fail(KEA_EINVAL, "kea_probe_exchange: the fenced kind needs a 4-byte aligned result");
     hipStream_t st = (hipStream_t)stream;
     void (*fn)(uint4 *, int, int, uint32_t *, uint32_t *) =
         kind == KEA_EXCHANGE_WRITE ? exchange_kernel<KEA_EXCHANGE_WRITE>
@@ -205,7 +217,7 @@ int kea_probe_exchange(int kind, int64_t workgroups, int64_t words, int64_t grou
     hipLaunchKernelGGL(fn, dim3((unsigned)workgroups), dim3(256), 0, st, (uint4 *)slots, (int)words, (int)group,
                        counters, result);
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_exchange: ") + hipGetErrorString(e));
+    if (e != hipSuccess) return fail((int)e, std::string("kea_probe_exchange: ") + hipGetErrorString(e));
     return 0;
 }
 
@@ -216,21 +228,21 @@ int kea_probe_floor(int kind, int64_t m, int64_t n, int64_t k, int bm, int bn, c
 
 int kea_probe_floor_waves(int kind, int64_t m, int64_t n, int64_t k, int bm, int bn, int waves, const int8_t *a,
                           const uint32_t *w, uint16_t *y, int64_t ldy, void *stream) {
-    if (waves < 1 || waves > 16) return kea::fail(KEA_EINVAL, "kea_probe_floor: waves must be in [1, 16]");
+    if (waves < 1 || waves > 16) return fail(KEA_EINVAL, "kea_probe_floor: waves must be in [1, 16]");
     if (kind < KEA_PROBE_EMPTY || kind > (KEA_PROBE_LOADS | KEA_PROBE_STORES))
-        return kea::fail(KEA_EINVAL, "kea_probe_floor: kind must be 0 (empty), 1 (loads), 2 (stores) or 3 (both)");
+        return fail(KEA_EINVAL, "kea_probe_floor: kind must be 0 (empty), 1 (loads), 2 (stores) or 3 (both)");
     if (bm < 16 || bm > 256 || bm % 16 || bn < 16 || bn > 256 || bn % 16)
-        return kea::fail(KEA_EINVAL, "kea_probe_floor: bm and bn must be multiples of 16 in [16, 256]");
+        return fail(KEA_EINVAL, "kea_probe_floor: bm and bn must be multiples of 16 in [16, 256]");
     if (m < bm || n < bn || k < 128 || m % bm || n % bn || k % 128 || m > (1 << 20) || n > (1 << 20) || k > (1 << 16))
-        return kea::fail(KEA_EINVAL, "kea_probe_floor: m, n must be multiples of bm, bn (<= 2^20) and k a multiple of "
+        return fail(KEA_EINVAL, "kea_probe_floor: m, n must be multiples of bm, bn (<= 2^20) and k a multiple of "
                                      "128 (<= 65536)");
     const long long a_units = (long long)bm * k / 16, w_units = (long long)bn * k / 128;
     const long long lds = (kind & KEA_PROBE_LOADS) ? (a_units + w_units) * 16 : 0;
-    if (lds > 160 * 1024) return kea::fail(KEA_EINVAL, "kea_probe_floor: bm * k + bn * k / 8 exceeds 160 KiB of LDS");
+    if (lds > 160 * 1024) return fail(KEA_EINVAL, "kea_probe_floor: bm * k + bn * k / 8 exceeds 160 KiB of LDS");
     if ((kind & KEA_PROBE_LOADS) && (!a || !w || ((uintptr_t)a & 15) || ((uintptr_t)w & 15)))
-        return kea::fail(KEA_EINVAL, "kea_probe_floor: loads need 16-byte aligned a [m, k] and w (native words)");
+        return fail(KEA_EINVAL, "kea_probe_floor: loads need 16-byte aligned a [m, k] and w (native words)");
     if ((kind & KEA_PROBE_STORES) && (!y || ((uintptr_t)y & 7) || ldy < n || ldy % 4))
-        return kea::fail(KEA_EINVAL, "kea_probe_floor: stores need an 8-byte aligned fp16 y [m, ldy >= n], ldy % 4 == 0");
+        return fail(KEA_EINVAL, "kea_probe_floor: stores need an 8-byte aligned fp16 y [m, ldy >= n], ldy % 4 == 0");
     FloorArgs f = {a, (const uint8_t *)w, y, (long long)ldy, (int)k, bm, bn, (int)a_units, (int)w_units};
     const dim3 grid((unsigned)(n / bn), (unsigned)(m / bm));
     hipStream_t st = (hipStream_t)stream;
@@ -240,11 +252,11 @@ int kea_probe_floor_waves(int kind, int64_t m, int64_t n, int64_t k, int bm, int
                                                      : floor_kernel<KEA_PROBE_LOADS | KEA_PROBE_STORES>;
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_floor: ") + hipGetErrorString(e));
+        if (e != hipSuccess) return fail((int)e, std::string("kea_probe_floor: ") + hipGetErrorString(e));
     }
     hipLaunchKernelGGL(fn, grid, dim3((unsigned)waves * 64), (size_t)lds, st, f);
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return kea::fail((int)e, std::string("kea_probe_floor: ") + hipGetErrorString(e));
+    if (e != hipSuccess) return fail((int)e, std::string("kea_probe_floor: ") + hipGetErrorString(e));
     return 0;
 }
 

@@ -1,6 +1,6 @@
 """CPU contract tests of the host API: export formats and checks, the provider seam (Table, row handles, fused QKV,
 BinaryProjection, PartCount), the ternary packed_t form and the native relayout. Restates the reference's CPU tests
-(tests/test_formats.py:14-130, tests/test_kernels_cpu.py:12-17, :58-75) against this build's modules."""
+(tests/test_formats.py:14-130, tests/test_kernels_cpu.py:12-17, :53-71) against this build's modules."""
 from __future__ import annotations
 
 import json
@@ -104,6 +104,46 @@ def test_check_export_refuses_a_modified_file(tmp_path):
     (d / "tokenizer" / "vocab.txt").write_text("b\n")
     with pytest.raises(ValueError, match="SHA-256"):
         formats.check_export(d, "binary")
+    formats.check_export(d, "binary", verify_hashes=False)
+
+
+def test_check_export_refuses_a_truncated_or_malformed_tensor_file(tmp_path):
+    """The safetensors structure is checked without the SHA-256 too: a truncated data buffer, one with trailing
+    bytes, overlapping or mis-sized data_offsets and a header that is not a JSON object are all ValueErrors."""
+    import struct
+    d = write_fake_export(tmp_path / "t", "binary")
+    path = d / formats.FILE
+    intact = path.read_bytes()
+    (length,) = struct.unpack("<Q", intact[:8])
+    header = json.loads(intact[8:8 + length])
+    data = intact[8 + length:]
+
+    def write(hdr, payload):
+        text = json.dumps(hdr).encode()
+        path.write_bytes(struct.pack("<Q", len(text)) + text + payload)
+
+    for payload, match in ((data[:-1], "truncated or corrupt"), (data + b"\0", "truncated or corrupt")):
+        path.write_bytes(intact[:8 + length] + payload)
+        with pytest.raises(ValueError, match=match):
+            formats.check_export(d, "binary", verify_hashes=False)
+    name = next(k for k in header if k != "__metadata__")
+    bad = json.loads(json.dumps(header))
+    bad[name]["data_offsets"][1] += 1  # one byte more than its shape holds
+    write(bad, data)
+    with pytest.raises(ValueError, match="do not hold"):
+        formats.check_export(d, "binary", verify_hashes=False)
+    ranges = sorted((v["data_offsets"][0], k) for k, v in header.items() if k != "__metadata__")
+    bad = json.loads(json.dumps(header))
+    second = ranges[1][1]
+    size = bad[second]["data_offsets"][1] - bad[second]["data_offsets"][0]
+    bad[second]["data_offsets"] = [0, size]  # overlaps the first tensor
+    write(bad, data)
+    with pytest.raises(ValueError, match="starts at byte"):
+        formats.check_export(d, "binary", verify_hashes=False)
+    write([1, 2, 3], b"")
+    with pytest.raises(ValueError, match="not a JSON object"):
+        formats.check_export(d, "binary", verify_hashes=False)
+    path.write_bytes(intact)
     formats.check_export(d, "binary", verify_hashes=False)
 
 

@@ -13,15 +13,25 @@ import pytest
 from kea_kernels import _hip
 from oracle import oracle as O
 
-HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
+INCLUDE = Path(__file__).resolve().parents[1] / "include"
+# the product library's headers; include/kea_probe.h declares the benchmark's separate probe library
+HEADERS = sorted(h for h in INCLUDE.glob("*.h") if h.name != "kea_probe.h")
+PROBE_HEADER = INCLUDE / "kea_probe.h"
 
 
-def declared_functions() -> list[str]:
+def declared_functions(headers=HEADERS) -> list[str]:
     names = set()
-    for header in HEADERS:
+    for header in headers:
         text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
         names.update(re.findall(r"\b(kea_\w+)\s*\(", text))
     return sorted(names)
+
+
+def _exported(path: Path) -> set[str]:
+    """Dynamic symbols a shared library defines (nm -D --defined-only)."""
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True, text=True, check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if line.strip()}
 
 
 def test_library_exports_every_declared_function():
@@ -34,6 +44,19 @@ def test_library_exports_every_declared_function():
         assert name in _hip.SIGNATURES, f"{name} has no ctypes signature"
     assert L.kea_version() >= 100
     assert L.kea_config_count() >= 1 and L.kea_config_name(1)
+    # the product library carries no measurement probes: they live in the benchmark's libkea_probe.so
+    assert not {s for s in _exported(_hip.LIB_PATH) if s.startswith("kea_probe")}
+
+
+def test_probe_library_exports_every_declared_function():
+    import kea_probes
+    names = declared_functions([PROBE_HEADER])
+    assert "kea_probe_spin" in names and "kea_probe_last_error" in names
+    L = kea_probes.lib()
+    for name in names:
+        assert hasattr(L, name), name
+        assert name in kea_probes.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(names) == {s for s in _exported(kea_probes.LIB_PATH) if s.startswith("kea_")}
 
 
 def _words(wbits, codes, n, k):
@@ -196,40 +219,3 @@ def test_plan_refuses_what_the_direct_call_refuses():
     assert not h and b"aligned" in L.kea_last_error()
     assert L.kea_lowbit_gemm_plan_launch(None, None) == -1
     L.kea_lowbit_gemm_plan_free(None)
-
-
-def test_rows_gemm_refuses_bad_arguments_before_any_launch():
-    """kea_lowbit_gemm_rows checks its mode, sizes, alignment and buffer overlaps on the host; m = 0 with valid
-    arguments returns 0. No device is touched (fake addresses)."""
-    L = _hip.lib()
-    P = ctypes.c_void_p
-
-    def call(rows, *, parts=1, n=1024, k=1024, y=0x200000, m=32, flags=0, config=0, wbits=1):
-        return L.kea_lowbit_gemm_rows(wbits, None if rows is None else ctypes.byref(rows), parts, P(0x1000), n, k,
-                                      P(0x2000), 0, None, 0, P(y), 0, n, None, 0, 1.0, m, flags, config, None)
-
-    def rows(mode=_hip.ROWS_PLAIN, x=0x100000, ldx=1024, **kw):
-        r = _hip.Rows(mode=mode, x=x, ldx=ldx)
-        for key, value in kw.items():
-            setattr(r, key, value)
-        return r
-
-    assert call(None) == -1 and b"rows is required" in L.kea_last_error()
-    assert call(rows(mode=7)) == -1 and b"unknown rows mode" in L.kea_last_error()
-    assert call(rows(), k=512) == -1 and b"k must be 1024" in L.kea_last_error()
-    assert call(rows(_hip.ROWS_NORM), k=4096) == -1 and b"k must be 1024" in L.kea_last_error()
-    assert call(rows(), config=3) == -1 and b"wave-split tile id" in L.kea_last_error()
-    assert call(rows(), config=14) == -1 and b"no row-quantizing kernel" in L.kea_last_error()  # 32-row tile
-    assert call(rows(), k=4096, parts=3) == -1 and b"no row-quantizing kernel" in L.kea_last_error()
-    assert call(rows(), y=0x100000 + 4096) == -1 and b"must not overlap the source rows" in L.kea_last_error()
-    assert call(rows(x=0x100008)) == -2 and b"aligned" in L.kea_last_error()
-    assert call(rows(ldx=1000)) == -1 and b"ldx" in L.kea_last_error()
-    assert call(rows(_hip.ROWS_NORM)) == -1 and b"norm0_w" in L.kea_last_error()
-    norm2 = dict(norm0_w=0x300000, norm0_b=0x301000, norm1_w=0x302000, norm1_b=0x303000, ld_out=1024)
-    assert call(rows(_hip.ROWS_NORM2, x_out=0x100000 + 64, **norm2)) == -1
-    assert b"x_out must not overlap" in L.kea_last_error()
-    assert call(rows(_hip.ROWS_MERGE, heads=4)) == -1 and b"heads * 128" in L.kea_last_error()
-    assert call(rows(_hip.ROWS_MERGE, heads=8, ws_bytes=1024)) == -4 and b"workspace too small" in L.kea_last_error()
-    assert call(rows(), flags=4, n=1023) == -1 and b"GLU" in L.kea_last_error()
-    assert call(rows(), m=0) == 0
-    assert call(rows(_hip.ROWS_NORM2, x_out=0x800000, **norm2), m=0, parts=3) == 0

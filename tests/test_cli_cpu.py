@@ -76,6 +76,9 @@ def test_api_surface_and_clip_handling(tmp_path):
     assert kea_kernels.load is model.load and kea_kernels.Transcript is model.Transcript
     with pytest.raises(ValueError, match="supports modes"):
         kea_kernels.load(write_fake_export(tmp_path / "t", "ternary"), mode="x1")
+    # only None means "the model's own mode" (kk/model.py:92): an empty mode is a bad mode, not the default
+    with pytest.raises(ValueError, match="supports modes"):
+        kea_kernels.load(write_fake_export(tmp_path / "b", "binary"), mode="")
     with pytest.raises(ValueError, match="AMD MI355X GPUs only"):
         model.check_device("cpu")
     short = model.as_clip(np.ones(100, dtype=np.float64))

@@ -269,25 +269,6 @@ def test_fused_encoder_matches_unfused():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("parts", [1, 3])
-@pytest.mark.parametrize("batch,samples", [(1, 160000), (2, 160000), (3, 48000)])
-@torch.inference_mode()
-def test_row_quantizing_layers_equal_separate_quantizers(parts, batch, samples):
-    """The encoder whose projections quantize their own rows (10 launches a layer; W_out merges the key-split
-    attention halves itself at batch 1-2, batch 3 runs unsplit attention) is bitwise the encoder with the quantizers
-    as separate row kernels; at three parts W2 (K = 4096) falls back to the separate quantizer."""
-    cfg = E.EncoderConfig(layers=3)
-    w = E.synthetic_weights(cfg, seed=31)
-    audio = torch.randn(batch, samples, generator=torch.Generator().manual_seed(32 + batch)).cuda()
-    rows = E.FastConformerEncoder(w, cfg, "cuda", parts=parts, rows=True)
-    assert batch * E.encoded_length(E.frames_for(cfg, samples)) <= rows.ROWS_MAX_M
-    got = rows(audio)
-    want = E.FastConformerEncoder(w, cfg, "cuda", parts=parts, rows=False)(audio)
-    torch.cuda.synchronize()
-    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
-
-
-@pytest.mark.gpu
 @torch.inference_mode()
 def test_graph_cache_bounds_shapes_and_returns_owned_outputs():
     """At most max_graphs graphs (one per shape and stream), bitwise the eager forward on every replay; a shape past

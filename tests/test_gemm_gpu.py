@@ -430,6 +430,31 @@ def test_quantizer_fp16_input_and_scales():
     assert np.array_equal(qs.cpu().float().numpy(), rqs)
 
 
+@pytest.mark.parametrize("parts", [1, 2, 3])
+@pytest.mark.parametrize("qs_dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("k,x_dtype", [(256, np.float32), (1024, np.float32), (1024, np.float16), (300, np.float32)])
+@torch.inference_mode()
+def test_quantizer_rounds_exact_ties_half_to_even(parts, qs_dtype, k, x_dtype):
+    """Rows whose first-part quotients are exact half-integers (tests/tie_rows.py): the GPU quantizer rounds them half
+    to even (0.5 -> 0, 1.5 -> 2, -2.5 -> -2; expected codes from integer arithmetic), on the one-wave (K <= 256) and
+    four-wave row paths, f32 and f16 inputs and scales; every part bitwise the oracle's."""
+    from tie_rows import NAMED, tie_rows
+    x, want = tie_rows(23, k, seed=k + parts, dtype=x_dtype)
+    xt = torch.from_numpy(x)
+    xd = xt.to(DEV)
+    q, qs, ldq = lowbit.quantize(xd, (0, k, 1, 23), 23, k, parts, qs_dtype=qs_dtype)
+    torch.cuda.synchronize()
+    got = q.cpu().numpy()
+    assert np.array_equal(got[0, :, :k], want)
+    s0 = qs.cpu().float().numpy()[0]
+    for h, c in NAMED.items():
+        cols = np.nonzero(x[0].astype(np.float64) == h * float(s0[0]))[0]
+        assert cols.size and (got[0, 0, cols] == c).all(), h
+    rq, rqs = O.quantize(x, parts, ldq=ldq, qs_f16=qs_dtype == torch.float16)
+    assert np.array_equal(got, rq)
+    assert np.array_equal(qs.cpu().float().numpy(), rqs)
+
+
 @torch.inference_mode()
 def test_graph_replays_match_eager():
     """Captured launches replayed several times, with eager work between replays, equal the eager result."""

@@ -268,3 +268,19 @@ def test_quantize_fp16_scales_clamp():
     assert np.abs(q).max() <= 127
     ref = np.clip(np.rint(x / qs[0][:, None]), -127, 127)
     assert np.array_equal(q[0].astype(np.float32), ref)
+
+
+@pytest.mark.parametrize("parts", [1, 2, 3])
+@pytest.mark.parametrize("qs_f16", [False, True])
+def test_quantize_rounds_exact_ties_half_to_even(parts, qs_f16):
+    """The oracle's quantizer on rows whose quotients are exact half-integers: 0.5 -> 0, 1.5 -> 2, -2.5 -> -2, ...
+    (expected codes from integer arithmetic, tests/tie_rows.py); a round-half-away rule fails here."""
+    from tie_rows import NAMED, tie_rows
+    x, want = tie_rows(9, 300, seed=parts + 10 * qs_f16)
+    q, qs = O.quantize(x, parts, qs_f16=qs_f16)
+    assert np.array_equal(q[0], want)
+    # the scale is the power of two the row was built on: amax / 127 exactly
+    assert np.array_equal(qs[0], np.abs(x).max(axis=1) / 127)
+    for h, c in NAMED.items():
+        cols = np.nonzero(x[0] == np.float32(h * qs[0, 0]))[0]
+        assert cols.size and (q[0, 0, cols] == c).all(), h

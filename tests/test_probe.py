@@ -1,4 +1,4 @@
-"""The measured-peak probe (include/kea_probe.h): argument checks on the CPU; on the GPU its checksum against a numpy
+"""The benchmark's probe library (libkea_probe.so, include/kea_probe.h): argument checks on the CPU; on the GPU its checksum against a numpy
 emulation of v_mfma_i32_16x16x64_i8, which also pins the operand layout the GEMM relies on (source A lane l: row
 l % 16, k = 16 * (l // 16) + byte; source B lane l: column l % 16, same k; result lane l: rows 4 * (l // 16) + r of
 column l % 16)."""
@@ -10,24 +10,24 @@ import numpy as np
 import pytest
 import torch
 
-from kea_kernels import _hip
+import kea_probes
 
 
 def test_probe_arguments():
-    L = _hip.lib()
+    L = kea_probes.lib()
     assert L.kea_probe_mfma_i8_ops(2048, 2000) == 2048 * 4 * 2000 * 8 * 16 * 16 * 64 * 2
     assert L.kea_probe_mfma_i8_ops(0, 10) == 0 and L.kea_probe_mfma_i8_ops(1, 0) == 0
     assert L.kea_probe_mfma_i8(0, 10, None, None) == -1
-    assert b"blocks" in L.kea_last_error()
+    assert b"blocks" in L.kea_probe_last_error()
     assert L.kea_probe_mfma_i8(1, 1, None, None) == -1
 
 
 def test_floor_and_spin_probe_arguments():
     """The launch-floor and spin probes refuse bad arguments before any launch (no GPU is touched)."""
-    L = _hip.lib()
+    L = kea_probes.lib()
     vp = ctypes.c_void_p
     assert L.kea_probe_floor(4, 128, 4096, 1024, 32, 32, None, None, None, 4096, None) == -1
-    assert b"kind" in L.kea_last_error()
+    assert b"kind" in L.kea_probe_last_error()
     assert L.kea_probe_floor(0, 128, 4096, 1024, 24, 32, None, None, None, 4096, None) == -1   # bm % 16
     assert L.kea_probe_floor(0, 100, 4096, 1024, 32, 32, None, None, None, 4096, None) == -1   # m % bm
     assert L.kea_probe_floor(0, 128, 4096, 1000, 32, 32, None, None, None, 4096, None) == -1   # k % 128
@@ -35,22 +35,22 @@ def test_floor_and_spin_probe_arguments():
     assert L.kea_probe_floor(2, 128, 4096, 1024, 32, 32, None, None, None, 4096, None) == -1   # stores need y
     assert L.kea_probe_floor(2, 128, 4096, 1024, 32, 32, None, None, vp(16), 4000, None) == -1  # ldy < n
     assert L.kea_probe_floor(1, 256, 256, 65536, 256, 256, vp(16), vp(16), None, 256, None) == -1  # LDS
-    assert b"LDS" in L.kea_last_error()
+    assert b"LDS" in L.kea_probe_last_error()
     assert L.kea_probe_spin(-1, None) == -1 and L.kea_probe_spin(100000001, None) == -1
     assert L.kea_probe_floor_waves(0, 128, 4096, 1024, 32, 32, 0, None, None, None, 4096, None) == -1  # waves
     assert L.kea_probe_floor_waves(0, 128, 4096, 1024, 32, 32, 17, None, None, None, 4096, None) == -1
-    assert b"waves" in L.kea_last_error()
+    assert b"waves" in L.kea_probe_last_error()
 
 
 def test_operand_and_exchange_probe_arguments():
     """The operand-fed MFMA loop and the exchange probe refuse bad arguments before any launch."""
-    L = _hip.lib()
+    L = kea_probes.lib()
     vp = ctypes.c_void_p
     assert L.kea_probe_mfma_i8_operands(1, 1, vp(8), vp(16), None) == -2       # operands not 16-byte aligned
-    assert b"operands" in L.kea_last_error()
+    assert b"operands" in L.kea_probe_last_error()
     assert L.kea_probe_mfma_i8_operands(0, 1, None, vp(16), None) == -1        # blocks
     assert L.kea_probe_exchange(3, 64, 64, 4, vp(16), vp(16), vp(16), None) == -1  # kind
-    assert b"kind" in L.kea_last_error()
+    assert b"kind" in L.kea_probe_last_error()
     assert L.kea_probe_exchange(0, 0, 64, 1, vp(16), None, None, None) == -1      # workgroups
     assert L.kea_probe_exchange(0, 64, 64, 65, vp(16), None, None, None) == -1    # group > workgroups
     assert L.kea_probe_exchange(0, 64, 64, 4, vp(8), None, None, None) == -2      # slots alignment
@@ -91,13 +91,13 @@ def expected_checksums(iters: int, words=None) -> np.ndarray:
 
 @pytest.mark.gpu
 def test_probe_checksum_matches_the_mfma_emulation():
-    L = _hip.lib()
+    L = kea_probes.lib()
     dev = torch.device("cuda", 0)
     blocks, iters = 3, 5
     out = torch.full((blocks * 256,), -1, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev)
     rc = L.kea_probe_mfma_i8(blocks, iters, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream.cuda_stream))
-    assert rc == 0, L.kea_last_error()
+    assert rc == 0, L.kea_probe_last_error()
     torch.cuda.synchronize()
     want = np.tile(expected_checksums(iters), blocks * 4)
     assert np.array_equal(out.cpu().numpy(), want)
@@ -105,7 +105,7 @@ def test_probe_checksum_matches_the_mfma_emulation():
 
 @pytest.mark.gpu
 def test_operand_fed_probe_checksum_on_random_operands():
-    L = _hip.lib()
+    L = kea_probes.lib()
     dev = torch.device("cuda", 0)
     g = np.random.default_rng(7)
     words = g.integers(-2 ** 31, 2 ** 31, size=(128, 4), dtype=np.int64).astype(np.int32)
@@ -115,7 +115,7 @@ def test_operand_fed_probe_checksum_on_random_operands():
     stream = torch.cuda.current_stream(dev)
     rc = L.kea_probe_mfma_i8_operands(blocks, iters, ctypes.c_void_p(ops.data_ptr()), ctypes.c_void_p(out.data_ptr()),
                                       ctypes.c_void_p(stream.cuda_stream))
-    assert rc == 0, L.kea_last_error()
+    assert rc == 0, L.kea_probe_last_error()
     torch.cuda.synchronize()
     want = np.tile(expected_checksums(iters, (words[:64], words[64:])), blocks * 4)
     assert np.array_equal(out.cpu().numpy(), want)
@@ -126,7 +126,7 @@ def test_operand_fed_probe_checksum_on_random_operands():
 def test_exchange_probe_fenced_sum_and_counters(workgroups, words, group):
     """The fenced exchange's last arrivers read every member's slot: after two launches the sum is twice
     0 + 1 + ... + (workgroups - 1), and every group counter is back at zero."""
-    L = _hip.lib()
+    L = kea_probes.lib()
     dev = torch.device("cuda", 0)
     slots = torch.zeros(workgroups * words * 4, dtype=torch.int32, device=dev)
     counters = torch.zeros(-(-workgroups // group), dtype=torch.int32, device=dev)
@@ -136,7 +136,7 @@ def test_exchange_probe_fenced_sum_and_counters(workgroups, words, group):
     for kind in (1, 2, 2):
         rc = L.kea_probe_exchange(kind, workgroups, words, group, vp(slots.data_ptr()), vp(counters.data_ptr()),
                                   vp(result.data_ptr()), vp(stream.cuda_stream))
-        assert rc == 0, L.kea_last_error()
+        assert rc == 0, L.kea_probe_last_error()
     torch.cuda.synchronize()
     assert int(result.item()) & 0xFFFFFFFF == (workgroups * (workgroups - 1)) & 0xFFFFFFFF
     assert not counters.any()
