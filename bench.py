@@ -22,9 +22,12 @@ metric's second part, ms per 10-s clip of the 24-layer synthetic encoder (BASELI
 the batch-1 error against the FP32 dense twin, and `cpu_baseline` = the oracle's C port of the reference's b1_fallback
 arithmetic (unpack -> exact int32 dot -> FP32 epilogue -> fp16) on this host's cores and on one core, beside a PyTorch
 CPU restatement of the reference's own oracle formula; that leg also checks the GPU output bitwise against the oracle
-(`parity`). Other modes: --suite (configs 2-4 and the reference's tuned shapes), --case (one GEMM shape), --encoder
-(config 5 with accuracy against the FP32 dense twin), --copy-calibration (a plain copy for the PMC traffic
-calibration), --sweep (every tile of the library at the chooser's shapes).
+(`parity`), and `suite` = BASELINE.json configs 2-4 at full size (config 2 per-channel and group-128, config 3's six
+encoder linears at M = 1000, config 4's single-token shapes at both weight widths, hot and cold), each with us per
+launch, TOPS, GB/s and the fraction of the binding published peak. Other modes: --suite (configs 2-4 and the
+reference's tuned shapes, one line each), --case (one GEMM shape), --encoder (config 5 with accuracy against the FP32
+dense twin), --copy-calibration (a plain copy for the PMC traffic calibration), --sweep (every tile of the library at
+the chooser's shapes), --trace-summary (a rocprofv3 kernel trace of this benchmark read the way it times).
 """
 from __future__ import annotations
 
@@ -516,22 +519,46 @@ def _suite_case(wbits, parts, m, n, k, *, scale_dtype, out_dtype, seed, reps=200
             "roofline_frac": round(t_roof / (us * 1e-6), 4)}
 
 
+# BASELINE.json configs 2-4 as named cases: (name, weight bits, M, N, K, ws_group, cold); fp16 scales and output
+CONFIG3_SHAPES = [("qkv", 3072, 1024), ("attn_out", 1024, 1024), ("ffn_up", 4096, 1024), ("ffn_down", 1024, 4096),
+                  ("pw1", 2048, 1024), ("pw2", 1024, 1024)]
+BASELINE_CASES = ([("config2", 2, 128, 1024, 4096, 0, False), ("config2_group128", 2, 128, 1024, 4096, 128, False)]
+                  + [(f"config3_{name}", 1, 1000, n, k, 0, False) for name, n, k in CONFIG3_SHAPES]
+                  + [(f"config4_w{w}_{tag}_m{m}", w, m, n, k, 0, cold)
+                     for cold in (False, True) for w in (1, 2) for m in (1, 4, 16)
+                     for tag, n, k in [("pred", 2560, 640), ("joint", 1030, 640)]]
+                  + [(f"config4_w{w}_down_m16", w, 16, 1024, 4096, 0, cold) for cold in (False, True) for w in (1, 2)])
+
+
+def _case_name(name: str, cold: bool) -> str:
+    return name + ("_cold" if cold else "")
+
+
+def baseline_suite(reps: int = 200) -> dict:
+    """BASELINE.json configs 2-4 at their full sizes, library-chosen configuration, inputs resident in HBM, HIP-graph
+    replay: {case: {us, tops, gbs, bound, frac}} (frac against the binding published peak: 5.0 POP/s int8 or
+    8 TB/s HBM). `_cold` cases read every launch's weights and activations from their own copy (>= 768 MiB cycled)."""
+    import torch
+    out = {}
+    for i, (name, w, m, n, k, group, cold) in enumerate(BASELINE_CASES):
+        row = _suite_case(w, 1, m, n, k, scale_dtype=torch.float16, out_dtype=torch.float16, seed=100 + i,
+                          ws_group=group, cold=cold, reps=reps)
+        out[_case_name(name, cold)] = {"us": row["us"], "tops": row["tops"], "gbs": row["gbs"],
+                                       "bound": row["bound"], "frac": row["roofline_frac"]}
+    return out
+
+
 def suite() -> None:
     """One JSON line per case: configs 2-4 of BASELINE.json and the reference's tuned (N, K, M) shapes at three
     activation parts with FP32 scales and output (the arithmetic its in-source timings use)."""
     import torch
     f16, f32 = torch.float16, torch.float32
-    cases = [("config2", 2, 1, 128, 1024, 4096, f16, f16), ("config2_group128", 2, 1, 128, 1024, 4096, f16, f16)]
-    cases += [("config3", 1, 1, 1000, n, k, f16, f16)
-              for n, k in [(3072, 1024), (1024, 1024), (4096, 1024), (1024, 4096), (2048, 1024)]]
-    cases += [("config4", w, 1, m, n, k, f16, f16) for w in (1, 2) for m in (1, 4, 16)
-              for n, k in [(2560, 640), (1030, 640)]]
-    cases += [("config4", w, 1, 16, 1024, 4096, f16, f16) for w in (1, 2)]
-    cases += [(name + "_cold", *rest) for name, *rest in cases if name == "config4"]
-    cases += [("refshape_x3", w, 3, m, n, k, f32, f32) for w in (1, 2) for n, k, m in REF_SHAPES]
+    for i, (name, w, m, n, k, group, cold) in enumerate(BASELINE_CASES):
+        row = _suite_case(w, 1, m, n, k, scale_dtype=f16, out_dtype=f16, seed=100 + i, ws_group=group, cold=cold)
+        print(json.dumps({"case": _case_name(name, cold), **row}), flush=True)
+    cases = [("refshape_x3", w, 3, m, n, k, f32, f32) for w in (1, 2) for n, k, m in REF_SHAPES]
     for i, (name, w, p, m, n, k, sd, od) in enumerate(cases):
-        row = _suite_case(w, p, m, n, k, scale_dtype=sd, out_dtype=od, seed=i,
-                          ws_group=128 if name.endswith("group128") else 0, cold=name.endswith("_cold"))
+        row = _suite_case(w, p, m, n, k, scale_dtype=sd, out_dtype=od, seed=i)
         print(json.dumps({"case": name, **row}), flush=True)
 
 
@@ -627,6 +654,41 @@ def encoder_bench(batch: int, parts: int, reps: int = 20, seed: int = 5, check_d
             "quantized_linear_ops_per_clip": lin_ops // batch, "weight_bytes": enc.weight_bytes()}
 
 
+def trace_summary(csv_path: str) -> dict:
+    """--trace-summary: a rocprofv3 kernel trace (`<name>_kernel_trace.csv`) of this benchmark read the way the
+    benchmark times: every run of back-to-back dispatches of one kernel that directly follows a bounded spin kernel
+    (the queued regions of the headline figure and of the graph replays) gives (last end - first start) / dispatches,
+    beside the mean and median of the traced per-dispatch durations of the same dispatches. Nanosecond timestamps."""
+    import csv
+    import statistics
+    with open(csv_path, newline="") as handle:
+        rows = sorted(csv.DictReader(handle), key=lambda r: int(r["Start_Timestamp"]))
+    regions = []
+    i = 0
+    while i < len(rows):
+        if "spin_kernel(" in rows[i]["Kernel_Name"]:
+            j = i + 1
+            if j < len(rows):
+                name = rows[j]["Kernel_Name"]
+                k = j
+                while k < len(rows) and rows[k]["Kernel_Name"] == name:
+                    k += 1
+                run = rows[j:k]
+                durations = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in run]
+                span = int(run[-1]["End_Timestamp"]) - int(run[0]["Start_Timestamp"])
+                gaps = [int(b["Start_Timestamp"]) - int(a["End_Timestamp"]) for a, b in zip(run, run[1:])]
+                label = name.replace("void ", "", 1).replace("(anonymous namespace)::", "")
+                regions.append({"kernel": label[:label.find("(")] if "(" in label else label, "dispatches": len(run),
+                                "span_us_per_dispatch": round(span / len(run) / 1e3, 4),
+                                "mean_duration_us": round(statistics.fmean(durations) / 1e3, 4),
+                                "median_duration_us": round(statistics.median(durations) / 1e3, 4),
+                                "median_gap_us": round(statistics.median(gaps) / 1e3, 4) if gaps else None})
+                i = k
+                continue
+        i += 1
+    return {"trace": str(csv_path), "regions": regions}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="low-bit GEMM benchmark (BASELINE.json config 1)")
     ap.add_argument("--gpus", type=int, default=1)
@@ -649,10 +711,11 @@ def main(argv=None) -> int:
                     help="--encoder: skip the FP32 dense comparison (profiles then hold only the quantized encoder)")
     ap.add_argument("--suite", action="store_true",
                     help="only time BASELINE.json configs 2-4 and the reference's tuned shapes (one JSON line each)")
-    ap.add_argument("--case", default=None, metavar="BITS,P,M,N,K[,TILE]",
-                    help="only time one GEMM shape (fp16 scales and output; the library-chosen configuration, or "
-                         "tile id TILE unsplit) for --steps launches; used for the rocprofv3 counter passes of the "
-                         "larger configs")
+    ap.add_argument("--case", default=None, metavar="BITS,P,M,N,K[,TILE][;...]",
+                    help="only time GEMM shapes (fp16 scales and output; the library-chosen configuration, or "
+                         "tile id TILE unsplit) for --steps launches each; used for the rocprofv3 counter passes of "
+                         "the larger configs")
+    ap.add_argument("--ws-group", type=int, default=0, help="--case: per-group weight scales of this group size")
     ap.add_argument("--sweep", default=None, metavar="PARTS",
                     help="only time every tile configuration at the chooser's shapes for these part counts "
                          "(e.g. 1,2,3; one JSON line per shape)")
@@ -661,7 +724,15 @@ def main(argv=None) -> int:
                          "cross-workgroup exchange inside one launch, and config 3's launch floors")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache config-1 figure")
     ap.add_argument("--no-floors", action="store_true", help="skip the launch-floor probes")
+    ap.add_argument("--no-suite", action="store_true",
+                    help="skip the `suite` object (BASELINE.json configs 2-4, library-chosen configurations)")
+    ap.add_argument("--trace-summary", default=None, metavar="CSV",
+                    help="only summarise a rocprofv3 kernel trace of this benchmark: per-dispatch time of every "
+                         "queued region ((last end - first start) / dispatches) beside the traced mean duration")
     args = ap.parse_args(argv)
+    if args.trace_summary:
+        print(json.dumps(trace_summary(args.trace_summary)), flush=True)
+        return 0
     if args.suite:
         suite()
         return 0
@@ -672,14 +743,19 @@ def main(argv=None) -> int:
         sweep(tuple(int(v) for v in args.sweep.split(",")))
         return 0
     if args.case:
-        fields = [int(v) for v in args.case.split(",")]
-        w, p, m, n, k = fields[:5]
         import torch
         from kea_kernels.binary.kernels import GemmConfig
-        config = GemmConfig(fields[5], 1) if len(fields) > 5 else None
-        row = _suite_case(w, p, m, n, k, scale_dtype=torch.float16, out_dtype=torch.float16, seed=0,
-                          reps=max(100, args.steps // 100 * 100), config=config)
-        print(json.dumps({"case": "gemm", "tile": fields[5] if config else 0, **row}), flush=True)
+        for spec in args.case.split(";"):
+            fields = [int(v) for v in spec.split(",")]
+            w, p, m, n, k = fields[:5]
+            tile = fields[5] if len(fields) > 5 else 0
+            try:
+                row = _suite_case(w, p, m, n, k, scale_dtype=torch.float16, out_dtype=torch.float16, seed=0,
+                                  reps=max(100, args.steps // 100 * 100), ws_group=args.ws_group,
+                                  config=GemmConfig(tile, 1) if tile else None)
+            except ValueError as e:  # a tile that does not take this shape
+                row = {"error": str(e)}
+            print(json.dumps({"case": "gemm", "tile": tile, **row}), flush=True)
         return 0
     if args.encoder:
         for case in args.encoder_cases.split(","):
@@ -756,6 +832,9 @@ def main(argv=None) -> int:
         floors = launch_floors(d, stream, name, waves=_config_waves(name))
         floors["gemm_us"] = round(ms_per_step * 1e3, 3)
         line["floors"] = floors
+    if not args.no_suite:
+        # BASELINE.json configs 2-4 at full size (the per-shape table the reference keeps in kk/binary/configs.py)
+        line["suite"] = baseline_suite()
     if not args.no_peaks:
         peaks = measured_peaks()
         measured = peaks["mfma_i8_tops_random"] if bound == "mfma" else peaks["copy_gbs"]

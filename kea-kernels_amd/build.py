@@ -28,7 +28,8 @@ PROBE_DIR = HERE / "kea_probes"
 PROBE_LIB = PROBE_DIR / "lib" / "libkea_probe.so"
 PROBE_SOURCES = ["kea_probe.hip"]
 SOURCES = ["kea_gemm_ring_w1.hip", "kea_gemm_ring_w2.hip", "kea_gemm_wsplit_p1.hip", "kea_gemm_wsplit_p2.hip",
-           "kea_gemm_wsplit_p3.hip", "kea_gemm.hip", "kea_gemm_wsplit.hip", "kea_quantize.hip", "kea_encoder.hip",
+           "kea_gemm_wsplit_p3.hip", "kea_gemm_wsplit_g1.hip", "kea_gemm_wsplit_g2.hip", "kea_gemm_wsplit_g3.hip",
+           "kea_gemm.hip", "kea_gemm_wsplit.hip", "kea_quantize.hip", "kea_encoder.hip",
            "kea_layout.cpp"]
 ARCH = "gfx950"
 # Per-source flags. The probe's loop keeps eight MFMA accumulators live across iterations; in the accumulator
@@ -39,6 +40,7 @@ SOURCE_FLAGS = {"kea_probe.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 # the dispatch preloads into SGPRs, so the first loads issue without a kernel-argument round trip.
 for _p in (1, 2, 3):
     SOURCE_FLAGS[f"kea_gemm_wsplit_p{_p}.hip"] = ["-mllvm", "-amdgpu-kernarg-preload-count=10"]
+    SOURCE_FLAGS[f"kea_gemm_wsplit_g{_p}.hip"] = ["-mllvm", "-amdgpu-kernarg-preload-count=10"]
 
 
 def hipcc() -> str:

@@ -174,6 +174,21 @@ int choose_tile(int wbits, int parts, long long m, long long n, long long k) {
     return best ? best : ring_tile(parts, m, n);
 }
 
+// The tile for per-group weight scales where the per-channel choice is a wave-split tile (small M; at M = 1000 the
+// ring's group tile wins: 20.3 against 24.9 us at N = 1024, K = 4096): the first wave-split tile of a measured
+// preference order that takes groups at this K (kea::wsplit_group_steps), else the LDS-ring group tile. The order puts
+// first the tiles whose every thread folds one output of the tile (the group fold is one FP32 chain per output):
+// config 2 with group-128 scales took 5.2-5.5 us on 16x32 k/8, 6.5-7.0 on 16x16 k/4 and k/8, 6.3 on 16x32 k/4 and
+// 7.2-8.9 on the 64-column tiles, against 11.1 us on the ring's best group tile.
+int group_tile(int wbits, int parts, long long k, int gq) {
+    static const char *const order[] = {"16x32 k/8", "16x16 k/4", "16x16 k/8", "16x32 k/4", "16x64 k/8", "16x64 k/4"};
+    for (const char *name : order)
+        for (int i = 0; i < kNumWsplitTiles; ++i)
+            if (std::string(kWsplitTiles[i].name) == name && kea::wsplit_group_steps(wbits, parts, k, kWsplitTiles[i], gq))
+                return kNumTiles + 1 + i;
+    return parts >= 2 ? 1 : 4;
+}
+
 // Split factor for split_k == 0: split K only for long K ranges (>= 2048) whose tiling leaves at most 64 workgroups,
 // by powers of two up to 8 slices and 256 workgroups (ternary, one part, K >= 4096: up to 128 workgroups, 512 after
 // the split); the split's second launch costs more than it saves otherwise.
@@ -318,11 +333,18 @@ int gemm_prepare(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, i
     if (ws_group != 0) {
         if (ws_group != 64 && ws_group != 128 && ws_group != 256)
             return kea::fail(KEA_EINVAL, "ws_group must be 0 (per-channel scales), 64, 128 or 256");
-        if (config != 0 && config != 1 && config != 4)
-            return kea::fail(KEA_EINVAL, "per-group weight scales run tile configs 1 and 4 only");
+        if (config != 0 && config != 1 && config != 4 && config <= kNumTiles)
+            return kea::fail(KEA_EINVAL, "per-group weight scales run tile configs 1 and 4 or a wave-split tile");
         if (split_k > 1) return kea::fail(KEA_EINVAL, "per-group weight scales run unsplit (split_k 0 or 1)");
         gq = (int)(ws_group / 64);
-        if (!config) config = parts >= 2 ? 1 : 4;
+        if (config > kNumTiles && config <= kNumTiles + kNumWsplitTiles &&
+            !kea::wsplit_group_steps(wbits, parts, k, kWsplitTiles[config - kNumTiles - 1], gq))
+            return kea::fail(KEA_EINVAL, std::string("per-group weight scales on wave-split tile ") +
+                                             kWsplitTiles[config - kNumTiles - 1].name +
+                                             " need 16-row blocks, at most 64 columns and one workgroup covering K "
+                                             "exactly (K = waves x 64 x 2..16, whole groups per wave)");
+        if (!config) config = choose_tile(wbits, parts, m, n, k) > kNumTiles ? group_tile(wbits, parts, k, gq)
+                                                                             : parts >= 2 ? 1 : 4;
         split_k = 1;
     }
     int rc = resolve(wbits, parts, m, n, k, split_k, config, &tile, &s, &qps);
@@ -389,10 +411,21 @@ int gemm_prepare(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, i
     }
 
     if (tile > kNumTiles) {
-        if (gq) return kea::fail(KEA_EINVAL, "per-group weight scales run the LDS-ring tiles");
         const WsplitTile &wt = kWsplitTiles[tile - kNumTiles - 1];
         if (!kea::fits_dispatch(cdivl(n, wt.nt * 16), wt.nw * 64))
             return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N or M");
+        if (gq) {
+            const int gs = kea::wsplit_group_steps(wbits, parts, k, wt, gq);
+            p.groups = (int)cdivl(k, ws_group);
+            p.steps_per_slice = wt.nw * gs;
+            const hipError_t e = gs ? kea::wsplit_group_prepare(p, wbits, parts, tile - kNumTiles - 1, gq, gs, &ls->wl)
+                                    : hipErrorInvalidDeviceFunction;
+            if (e != hipSuccess)
+                return kea::fail((int)e, std::string("no per-group wave-split kernel: ") + hipGetErrorString(e));
+            ls->wsplit = true;
+            ls->splits = 1;
+            return KEA_OK;
+        }
         p.steps_per_slice = qps;
         const hipError_t e = kea::wsplit_prepare(p, wbits, parts, tile - kNumTiles - 1, qps / wt.nw, s, s > 1, &ls->wl);
         if (e != hipSuccess) return kea::fail((int)e, std::string("no wave-split kernel: ") + hipGetErrorString(e));

@@ -68,6 +68,46 @@ WsplitFn wsplit_pick_p1(int wbits, int tile, int s, bool sliced, bool ragged);
 WsplitFn wsplit_pick_p2(int wbits, int tile, int s, bool sliced, bool ragged);
 WsplitFn wsplit_pick_p3(int wbits, int tile, int s, bool sliced, bool ragged);
 
+// Per-group weight scales on a wave-split tile (kea_gemm_wsplit_group_inst.h): instances for 16-row tiles of at most
+// four n-tiles whose workgroup covers K exactly, gq k-steps of 64 per group. Defined per activation part count.
+WsplitFn wsplit_group_pick_p1(int wbits, int tile, int gq, int s);
+WsplitFn wsplit_group_pick_p2(int wbits, int tile, int gq, int s);
+WsplitFn wsplit_group_pick_p3(int wbits, int tile, int gq, int s);
+
+// Outputs each thread of a per-group launch folds (1, 2 or 4 consecutive columns of one row of the 16 x 16nt tile).
+constexpr int wsplit_group_opt(int nt, int nw) {
+    return 256 * nt >= nw * 64 * 4 ? 4 : 256 * nt >= nw * 64 * 2 ? 2 : 1;
+}
+
+// Whether a per-group launch holds each thread's alpha values in registers (threads folding one output, at most 64
+// groups), loaded straight from [N][G]; otherwise the tile's alpha block is staged in LDS. (Register-held alpha for two
+// outputs a thread measured slower than LDS staging: 9.6 against 6.3 us at config 2 on the 16x32 k/4 tile.)
+constexpr bool wsplit_group_alpha_regs(int nt, int nw, int groups) {
+    return wsplit_group_opt(nt, nw) == 1 && groups <= 64;
+}
+
+// LDS bytes of a per-group launch: each of the tile's nw * s / gq groups has its int32 sums (parts x nt blocks of 64
+// lanes x 4) and, unless alpha is held in registers, its staged f32 alpha row (16 * nt + 4 floats).
+inline int wsplit_group_lds_bytes(int parts, const WsplitTile &t, int s, int gq) {
+    const int groups = t.nw * (s / gq);
+    return groups * (parts * t.nt * 1024 + (wsplit_group_alpha_regs(t.nt, t.nw, groups) ? 0 : (t.nt * 16 + 4) * 4));
+}
+
+// k-steps per wave of a per-group launch of tile t at this K (one workgroup covering K exactly with whole groups per
+// wave and whole weight quads per wave), or 0 when the tile cannot take per-group scales at this K.
+inline int wsplit_group_steps(int wbits, int parts, long long k, const WsplitTile &t, int gq) {
+    if (t.rm != 1 || t.nt > 4 || k % 64 != 0) return 0;
+    const long long ksteps = k / 64;
+    if (ksteps % t.nw != 0) return 0;
+    const long long s = ksteps / t.nw;
+    if (s != 2 && s != 4 && s != 8 && s != 16) return 0;
+    if (s % gq != 0 || (wbits == 1 && s % 2 != 0)) return 0;
+    const long long words = wbits == 1 ? s / 2 : s, J = wbits == 1 ? (k + 127) / 128 : ksteps;
+    if (words > 1 && J % 4 != 0) return 0;
+    if (!wsplit_fits(wbits, parts, t, (int)s) || wsplit_group_lds_bytes(parts, t, (int)s, gq) > 160 * 1024) return 0;
+    return (int)s;
+}
+
 // A resolved wave-split launch: kernel instance, grid, workgroup size, dynamic LDS and the dtype bits of its scales.
 struct WsplitLaunch {
     WsplitFn fn;
@@ -81,6 +121,10 @@ struct WsplitLaunch {
 // more than 64 KiB. SLICED: the kernel writes int32 slices. Returns a hipError_t.
 hipError_t wsplit_prepare(const Params &p, int wbits, int parts, int tile, int s, int splits, bool sliced,
                           WsplitLaunch *out);
+
+// Resolves a per-group launch of tile `tile` (s = wsplit_group_steps(...) != 0, p.groups set): grid
+// (ceil(N / BN), ceil(M / 16)), the instance and its LDS. Returns a hipError_t.
+hipError_t wsplit_group_prepare(const Params &p, int wbits, int parts, int tile, int gq, int s, WsplitLaunch *out);
 
 // Enqueues a resolved wave-split launch on `stream`; returns the launch's hipError_t.
 inline hipError_t wsplit_enqueue(const WsplitLaunch &l, const Params &p, hipStream_t stream) {

@@ -529,6 +529,36 @@ def test_config2_ternary_group128_fp16():
     assert torch.equal(y1.view(torch.int16), y.view(torch.int16))
 
 
+@pytest.mark.parametrize("wbits,p,m,n,k", [(2, 1, 128, 1024, 4096), (1, 1, 70, 300, 1024), (2, 2, 37, 200, 2048),
+                                           (1, 3, 16, 64, 1024), (2, 1, 1, 72, 4096)])
+@pytest.mark.parametrize("ws_group", [64, 128, 256])
+@torch.inference_mode()
+def test_group_scales_on_every_wave_split_tile(wbits, p, m, n, k, ws_group):
+    """Per-group scales on the wave-split tiles (each wave's int32 group sums through LDS, the fold in group order by
+    one wave per block): every tile that takes groups at this K, bitwise the oracle's per-group rule, with bias, f16
+    scales and f16 output; acc_out is the full-K sum."""
+    case = Case(wbits, p, m, n, k, seed=k + n + ws_group + p, bias=True)
+    groups = -(-k // ws_group)
+    g = torch.Generator().manual_seed(ws_group + m)
+    alpha_g = (torch.rand(n, groups, generator=g) * 0.09 + 0.01).to(case.qs.dtype)
+    ref_y, ref_acc = _group_ref(case, ws_group, alpha_g, order=p % 2)
+    ran = 0
+    for tile in range(1, kernels.tile_count() + 1):
+        if " k/" not in kernels.config_name(tile):
+            continue
+        try:
+            y, acc = _group_run(case, ws_group, alpha_g, out_dtype=torch.float16, order=p % 2,
+                                config=kernels.GemmConfig(tile=tile, split=1))
+        except ValueError as e:
+            # tiles that cannot take groups at this K, or whose registers cannot hold this many parts
+            assert "per-group weight scales on wave-split tile" in str(e) or "does not fit" in str(e)
+            continue
+        assert np.array_equal(acc, ref_acc), kernels.config_name(tile)
+        assert np.array_equal(_gpu_bits(y, torch.float16), O.to_f16_bits(ref_y)), kernels.config_name(tile)
+        ran += 1
+    assert ran >= 1
+
+
 @pytest.mark.parametrize("k", [17, 300, 4096 + 64])
 @torch.inference_mode()
 def test_group_scales_ragged_k_and_silu(k):
@@ -578,6 +608,39 @@ def test_residual_epilogue_bitwise(wbits, p, m, n, k, split, in_place):
     want = (res.numpy() + value * np.float32(factor)).astype(np.float32)
     got = y.cpu().numpy()
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("wbits,p,m,n,k,split", [(1, 1, 37, 300, 1024, 0), (2, 2, 37, 300, 640, 0),
+                                                 (1, 1, 37, 300, 4096, 2), (1, 3, 19, 72, 1100, 0)])
+@pytest.mark.parametrize("in_place", [False, True])
+@torch.inference_mode()
+def test_residual_epilogue_bitwise_on_every_wave_split_tile(wbits, p, m, n, k, split, in_place):
+    """The wave-split kernel loads its residual values with the epilogue's scales, before the MFMAs, from clamped rows
+    and columns (partial M and N blocks, an unused clamped block when a wave finishes more blocks than exist): on
+    every wave-split tile, unsplit and split, in place and not, y = residual + value * factor bitwise."""
+    case = Case(wbits, p, m, n, k, seed=m + n + p + k, bias=True, scale_dtype=torch.float32)
+    g = torch.Generator().manual_seed(m * 5 + k)
+    res = torch.randn(m, n, generator=g)
+    factor = 0.5
+    want = (res.numpy() + case.oracle_y(case.oracle_acc()) * np.float32(factor)).astype(np.float32)
+    ran = 0
+    for tile in range(1, kernels.tile_count() + 1):
+        if " k/" not in kernels.config_name(tile):
+            continue
+        dres = res.to(DEV)
+        y = dres if in_place else torch.full((m, n), float("nan"), device=DEV)
+        try:
+            lowbit.gemm(case.wbits, case.dq, case.dqs, case.words, n, k, case.dalpha, case.dbias, y, None,
+                        config=kernels.GemmConfig(tile=tile, split=split), residual=dres, residual_factor=factor)
+        except ValueError as e:
+            if "does not fit" in str(e) or "unsplit K range" in str(e):
+                continue  # registers that cannot hold this many parts, or a ragged K range too long for one workgroup
+            raise
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), kernels.config_name(tile)
+        ran += 1
+    assert ran >= 5
 
 
 @torch.inference_mode()
