@@ -151,9 +151,12 @@ def gpu_bench(steps: int, warmup: int):
     graph_ms = replay_timed(stream, [graph]) / steps
     del graph
 
-    # eager launch rate (host path included, synchronized at the end): through the plan and through lowbit.gemm
+    # eager launch rate (host path included, synchronized at the end): through the plan and through lowbit.gemm;
+    # warm-up calls first (the first call of a layout resolves it, the first launch of a kernel loads its code)
     def eager_us(fn, count=200):
         with torch.cuda.stream(stream):
+            for _ in range(20):
+                fn()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             for _ in range(count):
@@ -163,9 +166,18 @@ def gpu_bench(steps: int, warmup: int):
 
     checked = eager_us(lambda: lowbit.gemm(1, d["q"], d["qs"], d["words"], N, K, d["alpha"], None, d["y"], None))
     planned = eager_us(step)
+    # the drop-in operator a caller uses: Int8MmaLayer.linear at one part on config 1's weights (quantizer + GEMM,
+    # two launches, output and int8 parts allocated per call), beside the cost of one empty kernel launch
+    from kea_kernels.binary import layer_parts
+    lay = layer_parts.LAYERS[1].prepare(host["codes"], host["alpha"].float(), None, K, device)
+    xh = torch.randn(M, K, generator=torch.Generator().manual_seed(7)).to(torch.float16).to(device)
+    with torch.cuda.stream(stream):
+        layer_us = eager_us(lambda: lay.linear(xh, out_dtype=torch.float16))
+        empty_us = eager_us(lambda: kea_probes.lib().kea_probe_spin(0, handle))
     cfg = configs.choose(M, N, K, parts=1, wbits=1)
     return {"ms_per_step": ms_per_step, "graph_ms_per_step": graph_ms, "host_us_per_launch": host_us,
-            "eager_us": planned, "eager_checked_us": checked, "cfg": cfg, "host": host, "d": d, "stream": stream}
+            "eager_us": planned, "eager_checked_us": checked, "eager_layer_us": layer_us, "eager_empty_us": empty_us,
+            "cfg": cfg, "host": host, "d": d, "stream": stream}
 
 
 def cold_bench(d, stream, launches: int = 1300) -> float:
@@ -820,6 +832,8 @@ def main(argv=None) -> int:
                    "graph_note": "the same K launches replayed as one HIP graph; a replay adds a fixed cost"},
         "eager_launch_us": round(r["eager_us"], 3),
         "eager_launch_us_checked": round(r["eager_checked_us"], 3),
+        "eager_layer_us": round(r["eager_layer_us"], 3),
+        "eager_empty_launch_us": round(r["eager_empty_us"], 3),
     }
     if not args.no_cold:
         cold_us = cold_bench(d, stream)

@@ -216,6 +216,18 @@ kea_gemm_plan *kea_lowbit_gemm_plan(int wbits,
 int kea_lowbit_gemm_plan_launch(const kea_gemm_plan *plan, void *stream);
 void kea_lowbit_gemm_plan_free(kea_gemm_plan *plan);
 
+/* The plan's GEMM on other activation and output buffers of the same layout: q (16-byte aligned), qs, y, acc_out and
+ * residual replace the pointers the plan was made with (each present exactly where the plan has one; their shapes,
+ * strides and dtypes are the plan's), the weights and scales stay the plan's. workspace: kea_lowbit_gemm_plan_workspace
+ * bytes (0: none needed). The plan is not modified, so one plan may be launched from several threads. This is the
+ * per-call path of the operators' cached launches (an operator resolves a plan once per call layout, then binds each
+ * call's buffers), which replaces the reference's per-call validation and launch (kk/binary/layer.py:182-209,
+ * kk/ternary/fused_kernels.py:139-160). */
+int kea_lowbit_gemm_plan_launch_with(const kea_gemm_plan *plan, const int8_t *q_dev, const void *qs_dev, void *y_dev,
+                                     int32_t *acc_out_dev, const float *residual_dev, void *workspace_dev,
+                                     int64_t workspace_bytes, void *stream);
+int64_t kea_lowbit_gemm_plan_workspace(const kea_gemm_plan *plan);
+
 /* kea_lowbit_gemm without the workspace arguments, for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). It has no counterpart in the reference. The
  * split-K slices live in a library-owned device array of KEA_NOALLOC_SCRATCH_BYTES per GPU (a file-scope __device__

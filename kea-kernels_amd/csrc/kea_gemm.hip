@@ -532,6 +532,42 @@ int kea_lowbit_gemm_plan_launch(const kea_gemm_plan *plan, void *stream) {
     return gemm_launch(plan->spec, (hipStream_t)stream);
 }
 
+int kea_lowbit_gemm_plan_launch_with(const kea_gemm_plan *plan, const int8_t *q, const void *qs, void *y,
+                                     int32_t *acc_out, const float *residual, void *workspace,
+                                     int64_t workspace_bytes, void *stream) {
+    if (!plan) return kea::fail(KEA_EINVAL, "plan is NULL");
+    if (plan->spec.empty) return KEA_OK;
+    LaunchSpec ls = plan->spec;  // a copy: the plan stays read-only, so concurrent launches of it are safe
+    Params &p = ls.p;
+    if (!q || ((uintptr_t)q & 15)) return kea::fail(KEA_EALIGN, "q must be a 16-byte aligned device pointer");
+    if (!qs) return kea::fail(KEA_EINVAL, "qs is required");
+    if ((y != nullptr) != (p.y != nullptr) || (acc_out != nullptr) != (p.acc != nullptr) ||
+        (residual != nullptr) != (p.res != nullptr))
+        return kea::fail(KEA_EINVAL, "y, acc_out and residual must be given exactly where the plan has them");
+    p.q = q;
+    p.qs = qs;
+    p.y = y;
+    p.acc = acc_out;
+    p.res = residual;
+    // the vector-store flags follow the new buffers' alignment (the row strides are the plan's)
+    const int esz = p.y_dtype == KEA_F32 ? 4 : 2, yv = (p.flags & KEA_FLAG_GLU) ? 2 : 4;
+    p.y_vec = y && (p.ldy % yv == 0) && ((uintptr_t)y % (yv * esz) == 0);
+    p.acc_vec = acc_out && (p.acc_ld % 4 == 0) && ((uintptr_t)acc_out % 16 == 0);
+    if (ls.splits > 1) {
+        const int64_t need = (int64_t)ls.splits * ls.parts * p.M * p.N * 4;
+        if (!workspace || workspace_bytes < need)
+            return kea::fail(KEA_ESPACE, "split-K workspace too small: need " + std::to_string(need) + " bytes");
+        if ((uintptr_t)workspace & 15) return kea::fail(KEA_EALIGN, "workspace must be 16-byte aligned");
+        p.slices = (int32_t *)workspace;
+    }
+    return gemm_launch(ls, (hipStream_t)stream);
+}
+
+int64_t kea_lowbit_gemm_plan_workspace(const kea_gemm_plan *plan) {
+    if (!plan || plan->spec.empty || plan->spec.splits <= 1) return 0;
+    return (int64_t)plan->spec.splits * plan->spec.parts * plan->spec.p.M * plan->spec.p.N * 4;
+}
+
 void kea_lowbit_gemm_plan_free(kea_gemm_plan *plan) { delete plan; }
 
 int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts, const void *qs,

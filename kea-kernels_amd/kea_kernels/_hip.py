@@ -39,6 +39,8 @@ SIGNATURES = {
                                     _vp, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _i64, _vp,
                                     _i64, _f32]),
     "kea_lowbit_gemm_plan_launch": (_i32, [_vp, _vp]),
+    "kea_lowbit_gemm_plan_launch_with": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
+    "kea_lowbit_gemm_plan_workspace": (_i64, [_vp]),
     "kea_lowbit_gemm_plan_free": (None, [_vp]),
     "kea_lowbit_gemm_noalloc": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _vp, _i32,
                                        _i64, _vp, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _i32, _i32, _i32, _vp]),
@@ -122,11 +124,17 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise ValueError(f"unsupported dtype {dtype}") from None
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
     """torch's current stream on `device`; ValueError for a device that is not a GPU (the kernels would read host
-    pointers as device addresses)."""
+    pointers as device addresses). Read through torch's raw-stream accessor where it has one (a fraction of a
+    microsecond; torch.cuda.current_stream(device) builds a Stream object and costs about 2 us per call)."""
     if device.type != "cuda":
         raise ValueError(f"the kernels run on the GPU: tensors on {device} cannot be launched on")
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 

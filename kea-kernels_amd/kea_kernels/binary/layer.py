@@ -6,6 +6,8 @@ dtype of `y`, fp16 per-token scales via the dtype of `qs`, raw int32 accumulator
 call, both on the current stream and both graph-capturable (no allocation inside the library, no host sync):
   1. kea_quantize: x (any strides) -> q int8 [P, M, ldq] + qs [P, M] (LayerNorm / input SiLU fused for `project`);
   2. kea_lowbit_gemm: the 1-bit x int8 GEMM with the fused epilogue.
+The layer resolves each call layout once (lowbit.Launches: a GEMM plan per layout, the buffers bound per call), so a
+repeated call pays the two launches and two allocations, not the argument checks.
 There is no slow fallback layout: every shape runs the MFMA kernel (the native layout pads N to 16 and K to 128).
 """
 from __future__ import annotations
@@ -53,6 +55,17 @@ class Int8MmaLayer:
     def fast(self) -> bool:
         return True
 
+    @property
+    def launches(self) -> lowbit.Launches:
+        """The layer's launches resolved once per call layout (lowbit.Launches), rebuilt if the weights change."""
+        cache = self.__dict__.get("_launches")
+        if (cache is None or cache.words is not self.words or cache.wscale is not self.scale
+                or cache.bias is not self.bias):
+            cache = lowbit.Launches(self.WBITS, self.words, self.out_features, self.in_features, self.scale,
+                                    self.bias)
+            self.__dict__["_launches"] = cache
+        return cache
+
     def weight_bytes(self) -> int:
         return api.resident_bytes(self.words, self.scale, self.bias)
 
@@ -99,8 +112,9 @@ class Int8MmaLayer:
         return y.transpose(1, 2)
 
     def _run(self, x: Tensor, rows: tuple, m: int, y: Tensor) -> None:
-        q, qs, ldq = quantize(x, rows, m, self.in_features, parts=self.PARTS)
-        self.dot(q, qs, ldq, m, y)
+        if not self.launches.project(x, rows, m, self.PARTS, y):
+            q, qs, ldq = quantize(x, rows, m, self.in_features, parts=self.PARTS)
+            self.dot(q, qs, ldq, m, y)
 
     def dot(self, q: Tensor, qs: Tensor, ldq: int, m: int, y: Tensor | None, *, silu: bool = False, config=None,
             order: int = 0, acc_out: Tensor | None = None) -> None:
@@ -132,9 +146,11 @@ def _project(layer: Int8MmaLayer, x: Tensor, conv: bool, parts: int, activation:
     m, n = b * t, layer.out_features
     y = torch.empty(b, t, n, device=layer.device, dtype=torch.float32)
     if m:
-        q, qs, ldq = lowbit.quantize(xx, (xx.stride(0), xx.stride(1), xx.stride(2), t), m, k, parts, norm=norm,
-                                     input_activation=input_activation)
-        layer.dot(q, qs, ldq, m, y.view(m, n), silu=activation == "silu")
+        rows = (xx.stride(0), xx.stride(1), xx.stride(2), t)
+        if not layer.launches.project(xx, rows, m, parts, y.view(m, n), silu=activation == "silu", norm=norm,
+                                      input_activation=input_activation):
+            q, qs, ldq = lowbit.quantize(xx, rows, m, k, parts, norm=norm, input_activation=input_activation)
+            layer.dot(q, qs, ldq, m, y.view(m, n), silu=activation == "silu")
     if conv:
         return y.transpose(1, 2)
     return y if x.dim() == 3 else y.view(*x.shape[:-1], n)
@@ -164,5 +180,4 @@ def dot(layer: Int8MmaLayer, q: Tensor, qs: Tensor, ldq: int, m: int, y: Tensor 
         raise ValueError("fast path needs 16-byte aligned rows of q")
     if order not in (0, 1):
         raise ValueError("order must be 0 or 1")
-    lowbit.gemm(layer.WBITS, q, qs, layer.words, n, k, layer.scale, layer.bias, y, acc_out, m=m, silu=silu,
-                order=order, config=config)
+    layer.launches.dot(q, qs, m, y, acc_out, silu=silu, order=order, config=config)

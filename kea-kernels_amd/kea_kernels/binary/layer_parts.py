@@ -51,8 +51,9 @@ class Int8MmaPartsLayer(Int8MmaLayer):
 
     def _run(self, x: Tensor, rows: tuple, m: int, y: Tensor) -> None:
         """linear / conv: the first PARTS residual parts (bitwise the PARTS-part quantizer)."""
-        q, qs, ldq = quantize(x, rows, m, self.in_features, parts=self.PARTS)
-        self.dot(q, qs, ldq, m, y, parts=self.PARTS)
+        if not self.launches.project(x, rows, m, self.PARTS, y):
+            q, qs, ldq = quantize(x, rows, m, self.in_features, parts=self.PARTS)
+            self.dot(q, qs, ldq, m, y, parts=self.PARTS)
 
 
 def _aligned(q: Tensor, k: int) -> tuple[Tensor, int]:
@@ -75,8 +76,7 @@ def dot_parts(layer: Int8MmaLayer, q: Tensor, qs: Tensor, ldq: int, m: int, y: T
         raise ValueError("fast path needs 16-byte aligned rows of q")
     if order not in (0, 1):
         raise ValueError("order must be 0 or 1")
-    lowbit.gemm(layer.WBITS, q, qs, layer.words, n, k, layer.scale, layer.bias, y, acc_out, m=m, silu=silu,
-                order=order, config=config)
+    layer.launches.dot(q, qs, m, y, acc_out, silu=silu, order=order, config=config)
 
 
 def variant(parts: int):

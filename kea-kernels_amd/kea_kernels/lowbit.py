@@ -305,3 +305,140 @@ def quantize(x: Tensor, rows: tuple, m: int, k: int, parts: int, *, norm=None, i
                                  qs.data_ptr(), _hip.dtype_code(qs_dtype), _hip.stream_handle(x.device))
     _hip.check(rc, "kea_quantize")
     return q, qs, ldq
+
+
+class _Entry:
+    """One resolved call layout of a Launches cache: the GEMM plan, its workspace bytes and the quantizer's fixed
+    arguments."""
+    __slots__ = ("plan", "free", "need", "ldq", "qs_off", "nbytes", "qargs")
+
+    def __del__(self):
+        plan, self.plan = getattr(self, "plan", None), None
+        if plan:
+            self.free(plan)
+
+
+class Launches:
+    """The launches of one weight matrix (an operator's layer), resolved once per call layout.
+
+    An operator call is the residual quantizer of its input plus the low-bit GEMM. gemm() and quantize() check every
+    argument and resolve the tile, split and kernel on each call, about 11 us of host time each. Here the first call
+    of a layout (input dtype, shape and strides, part count, output dtype and row stride, epilogue flags, LayerNorm)
+    does those checks once and keeps a GEMM plan (kea_lowbit_gemm_plan); later calls of that layout allocate the int8
+    parts and the output, enqueue kea_quantize and bind the plan to the new buffers (kea_lowbit_gemm_plan_launch_with,
+    which re-checks the buffer alignments it depends on). The reference validates and launches on every call
+    (kk/binary/layer.py:182-209, kk/ternary/fused_kernels.py:139-160); the results are the same bits either way.
+    Layouts are kept up to `max_entries` (the oldest is dropped first)."""
+
+    def __init__(self, wbits: int, words: Tensor, n: int, k: int, wscale: Tensor, bias: Tensor | None, *,
+                 max_entries: int = 64):
+        self.wbits, self.words, self.n, self.k, self.wscale, self.bias = wbits, words, n, k, wscale, bias
+        self.max_entries = max_entries
+        self._entries: dict = {}
+
+    def __len__(self) -> int:
+        return len(self._entries)
+
+    @staticmethod
+    def _norm_key(norm, device):
+        """(weight pointer, bias pointer, eps) of a LayerNorm whose parameters the kernel can read in place (f32,
+        contiguous, on the device), None without one, False where they would need a copy (the uncached path)."""
+        if norm is None:
+            return None
+        w, b = getattr(norm, "weight", None), getattr(norm, "bias", None)
+        for t in (w, b):
+            if t is None or t.dtype != torch.float32 or t.device != device or not t.is_contiguous():
+                return False
+        return (w.data_ptr(), b.data_ptr(), float(norm.eps))
+
+    def project(self, x: Tensor, rows: tuple, m: int, parts: int, y: Tensor, *, silu: bool = False,
+                order: int = 0, norm=None, input_activation: str = "", config=None) -> bool:
+        """y[:m] (row-major [>= m, N] view) = the GEMM of the parts-part quantization of x's rows (x's own rows:
+        `rows` = (XB, XT, XK, T) derived from x's shape and strides by the caller, so every row lies inside x).
+        Returns False, having done nothing, where the call needs the uncached path (a LayerNorm whose parameters
+        are not f32 device-contiguous)."""
+        nkey = self._norm_key(norm, x.device)
+        if nkey is False:
+            return False
+        tile = 0 if config is None or not hasattr(config, "tile") else (int(config.tile), int(config.split))
+        key = (x.dtype, x.device, tuple(x.shape), x.stride(), rows, m, parts, y.dtype, y.stride(0), tuple(y.shape),
+               bool(silu), order, nkey, input_activation, tile)
+        e = self._entries.get(key)
+        if e is None:
+            e = self._resolve(key, x, rows, m, parts, y, silu, order, norm, input_activation, config)
+        buf = torch.empty(e.nbytes, dtype=torch.uint8, device=x.device)
+        q, qs = buf.data_ptr(), buf.data_ptr() + e.qs_off
+        stream = _hip.stream_handle(x.device)
+        L = _hip.lib()
+        rc = L.kea_quantize(x.data_ptr(), *e.qargs, q, e.ldq, qs, _hip.F32, stream)
+        if rc:
+            _hip.check(rc, "kea_quantize")
+        ws = torch.empty(e.need, dtype=torch.uint8, device=x.device) if e.need else None
+        rc = L.kea_lowbit_gemm_plan_launch_with(e.plan, q, qs, y.data_ptr(), None, None,
+                                                ws.data_ptr() if ws is not None else None, e.need, stream)
+        if rc:
+            _hip.check(rc, "kea_lowbit_gemm_plan_launch_with")
+        return True
+
+    def _resolve(self, key, x, rows, m, parts, y, silu, order, norm, input_activation, config) -> _Entry:
+        """The first call of a layout: the full checks of quantize() and gemm() on real buffers, then the plan."""
+        if m < 1:
+            raise ValueError("a cached launch needs at least one row")
+        q, qs, ldq = quantize(x, rows, m, self.k, parts, norm=norm, input_activation=input_activation)
+        args, _, workspace = _gemm_args(self.wbits, q, qs, self.words, self.n, self.k, self.wscale, self.bias, y,
+                                        None, m, silu, order, config, 0, None, False)
+        L = _hip.lib()
+        e = _Entry()
+        e.free = L.kea_lowbit_gemm_plan_free
+        e.plan = L.kea_lowbit_gemm_plan(*args, None, 0, 1.0)
+        if not e.plan:
+            _hip.check(-1, "kea_lowbit_gemm_plan")
+        e.need = int(L.kea_lowbit_gemm_plan_workspace(e.plan))
+        e.ldq = ldq
+        e.qs_off = parts * m * ldq                       # a multiple of 16: the scales start 16-byte aligned
+        e.nbytes = e.qs_off + 4 * parts * m
+        nw, nb, eps = (None, None, 0.0) if norm is None else (norm.weight.data_ptr(), norm.bias.data_ptr(),
+                                                              float(norm.eps))
+        xb, xt, xk, t = rows
+        e.qargs = (_hip.dtype_code(x.dtype), xb, xt, xk, max(t, 1), m, self.k, parts, nw, nb, eps,
+                   int(input_activation == "silu"))
+        if len(self._entries) >= self.max_entries:
+            self._entries.pop(next(iter(self._entries)))
+        self._entries[key] = e
+        return e
+
+    def dot(self, q: Tensor, qs: Tensor, m: int, y: Tensor | None, acc_out: Tensor | None = None, *,
+            silu: bool = False, order: int = 0, config=None) -> None:
+        """gemm() of caller-made parts q int8 [P, >= m, ldq] / qs [P, >= m] with this matrix, resolved once per
+        layout of (q, qs, y, acc_out, flags)."""
+        tile = 0 if config is None or not hasattr(config, "tile") else (int(config.tile), int(config.split))
+        key = ("dot", q.dtype, q.device, tuple(q.shape), q.stride(), qs.dtype, tuple(qs.shape), qs.stride(), m,
+               None if y is None else (y.dtype, tuple(y.shape), y.stride()),
+               None if acc_out is None else (acc_out.dtype, tuple(acc_out.shape), acc_out.stride()),
+               bool(silu), order, tile)
+        e = self._entries.get(key)
+        if e is None or m < 1:
+            if m < 1:  # nothing to launch (the library's m = 0 path)
+                gemm(self.wbits, q, qs, self.words, self.n, self.k, self.wscale, self.bias, y, acc_out, m=m, silu=silu,
+                     order=order, config=config)
+                return
+            args, _, _ = _gemm_args(self.wbits, q, qs, self.words, self.n, self.k, self.wscale, self.bias, y, acc_out,
+                                    m, silu, order, config, 0, None, False)
+            L = _hip.lib()
+            e = _Entry()
+            e.free = L.kea_lowbit_gemm_plan_free
+            e.plan = L.kea_lowbit_gemm_plan(*args, None, 0, 1.0)
+            if not e.plan:
+                _hip.check(-1, "kea_lowbit_gemm_plan")
+            e.need = int(L.kea_lowbit_gemm_plan_workspace(e.plan))
+            if len(self._entries) >= self.max_entries:
+                self._entries.pop(next(iter(self._entries)))
+            self._entries[key] = e
+        if torch.is_grad_enabled() and (q.requires_grad or qs.requires_grad):
+            raise RuntimeError("the low-bit GEMM is inference only: an input requires grad")
+        ws = torch.empty(e.need, dtype=torch.uint8, device=q.device) if e.need else None
+        rc = _hip.lib().kea_lowbit_gemm_plan_launch_with(
+            e.plan, q.data_ptr(), qs.data_ptr(), _hip.ptr(y), _hip.ptr(acc_out), None,
+            ws.data_ptr() if ws is not None else None, e.need, _hip.stream_handle(q.device))
+        if rc:
+            _hip.check(rc, "kea_lowbit_gemm_plan_launch_with")

@@ -46,7 +46,22 @@ def int8_matmul(x, mod, conv=False, components=1, activation="", norm=None, conf
     m, n = b * t, mod.out_features
     y = torch.empty((b, t, n), dtype=torch.float32, device=x.device)
     if m:
-        q, qs, _ = _quantize(xx, components, norm, input_activation)
-        lowbit.gemm(2, q, qs, native_words(mod), n, k, mod.scale, mod.bias, y.view(m, n), None,
-                    silu=activation == "silu", config=config)
+        launches = _launches(mod)
+        rows = (xx.stride(0), xx.stride(1), xx.stride(2), t)
+        if not launches.project(xx, rows, m, components, y.view(m, n), silu=activation == "silu", norm=norm,
+                                input_activation=input_activation, config=config):
+            q, qs, _ = _quantize(xx, components, norm, input_activation)
+            lowbit.gemm(2, q, qs, native_words(mod), n, k, mod.scale, mod.bias, y.view(m, n), None,
+                        silu=activation == "silu", config=config)
     return y.transpose(1, 2) if conv else y.reshape(*x.shape[:-1], n)
+
+
+def _launches(mod) -> lowbit.Launches:
+    """The module's launches resolved once per call layout (lowbit.Launches), kept on the module and rebuilt if its
+    codes, scale or bias change."""
+    words = native_words(mod)
+    cache = mod.__dict__.get("_kea_launches")
+    if cache is None or cache.words is not words or cache.wscale is not mod.scale or cache.bias is not mod.bias:
+        cache = lowbit.Launches(2, words, mod.out_features, mod.in_features, mod.scale, mod.bias)
+        mod.__dict__["_kea_launches"] = cache
+    return cache

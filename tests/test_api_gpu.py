@@ -237,3 +237,100 @@ def test_quantize_zero_rows_and_lowbit_zero_m():
     x = torch.empty(0, 64, device="cuda")
     q, qs, ldq = lowbit.quantize(x, (0, 64, 1, 1), 0, 64, 3)
     assert q.shape == (3, 0, 64) and qs.shape == (3, 0)
+
+
+# --- launches resolved once per call layout (lowbit.Launches) ----------------------------------------------------------
+
+def _uncached(layer, x, rows, m, parts, y, *, silu=False, norm=None, input_activation=""):
+    """The checked, uncached path: quantize() then gemm() on the layer's weights."""
+    q, qs, _ = lowbit.quantize(x, rows, m, layer.in_features, parts, norm=norm, input_activation=input_activation)
+    lowbit.gemm(layer.WBITS, q, qs, layer.words, layer.out_features, layer.in_features, layer.scale, layer.bias, y,
+                None, m=m, silu=silu)
+
+
+@pytest.mark.parametrize("parts", [1, 3])
+@torch.inference_mode()
+def test_cached_launches_are_bitwise_the_checked_path(parts):
+    """linear (2-D, 3-D, strided, f16 input), conv and project (LayerNorm, input SiLU, SiLU epilogue) through the
+    layer's cached launches: every call, including repeated calls of one layout on new buffers, gives the checked
+    path's bits; a layout is resolved once."""
+    n, k = 300, 1024
+    codes, scale, _ = _weights(n, k, seed=parts + 40)
+    bias = torch.randn(n, generator=torch.Generator().manual_seed(41))
+    layer = layer_parts.LAYERS[parts].prepare(codes, scale, bias, k, "cuda")
+    g = torch.Generator().manual_seed(parts)
+    for step in range(3):  # the same layouts again, on new inputs
+        xs = [torch.randn(37, k, generator=g).cuda(),
+              torch.randn(2, 19, k, generator=g).cuda(),
+              torch.randn(70, 2 * k, generator=g).cuda()[:, ::2],
+              torch.randn(16, k, generator=g).cuda().half()]
+        for x in xs:
+            got = layer.linear(x)
+            x3 = x.reshape(-1, x.shape[-2], x.shape[-1]) if x.dim() == 3 else x
+            m = got.numel() // n
+            rows = (x3.stride(0), x3.stride(1), x3.stride(2), x3.shape[1]) if x.dim() == 3 else \
+                (0, x.stride(0), x.stride(1), m)
+            want = torch.empty(m, n, device="cuda")
+            _uncached(layer, x3, rows, m, parts, want)
+            torch.cuda.synchronize()
+            assert torch.equal(got.reshape(m, n).view(torch.int32), want.view(torch.int32)), (step, tuple(x.shape))
+        xc = torch.randn(3, k, 25, generator=g).cuda()
+        got = layer.conv(xc)
+        want = torch.empty(3 * 25, n, device="cuda")
+        _uncached(layer, xc, (xc.stride(0), xc.stride(2), xc.stride(1), 25), 75, parts, want)
+        assert torch.equal(got.transpose(1, 2).reshape(75, n).view(torch.int32), want.view(torch.int32))
+        norm = torch.nn.LayerNorm(k).cuda()
+        with torch.no_grad():
+            norm.weight.copy_(torch.rand(k, generator=g) + 0.5)
+            norm.bias.copy_(torch.randn(k, generator=g) * 0.1)
+        xp = torch.randn(2, 33, k, generator=g).cuda()
+        got = layer.project(xp, components=parts, activation="silu", norm=norm, input_activation="silu")
+        want = torch.empty(66, n, device="cuda")
+        _uncached(layer, xp, (xp.stride(0), xp.stride(1), xp.stride(2), 33), 66, parts, want, silu=True, norm=norm,
+                  input_activation="silu")
+        torch.cuda.synchronize()
+        assert torch.equal(got.reshape(66, n).view(torch.int32), want.view(torch.int32))
+    assert 1 <= len(layer.launches) <= 8  # one entry per layout, not per call
+
+
+@torch.inference_mode()
+def test_cached_dot_split_k_workspace_and_acc_out():
+    """dot through the cached plan: a split-K configuration (its workspace allocated per call) and raw
+    accumulators, bitwise the checked gemm() on the same parts; a layer whose weights are replaced gets new plans."""
+    n, k, m = 256, 4096, 64
+    codes, scale, _ = _weights(n, k, seed=77)
+    layer = layer_parts.LAYERS[2].prepare(codes, scale, None, k, "cuda")
+    x = torch.randn(m, k, device="cuda")
+    q, qs, ldq = L.quantize(x, (0, x.stride(0), x.stride(1), m), m, k, parts=2)
+    cfg = GemmConfig(tile=1, split=4)
+    for _ in range(2):
+        y = torch.empty(m, n, device="cuda")
+        acc = torch.empty(2, m, n, dtype=torch.int32, device="cuda")
+        layer.dot(q, qs, ldq, m, y, config=cfg, acc_out=acc)
+        y_ref = torch.empty_like(y)
+        acc_ref = torch.empty_like(acc)
+        lowbit.gemm(1, q, qs, layer.words, n, k, layer.scale, None, y_ref, acc_ref, m=m, config=cfg)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), y_ref.view(torch.int32)) and torch.equal(acc, acc_ref)
+    assert np.array_equal(acc.cpu().numpy(), O.b1_gemm(q.cpu().numpy(), codes.numpy(), k))
+    old = layer.launches
+    layer.scale = layer.scale * 2
+    assert layer.launches is not old
+
+
+@torch.inference_mode()
+def test_ternary_int8_matmul_cached_equals_checked_path():
+    n, k = 200, 640
+    g = torch.Generator().manual_seed(5)
+    vals = torch.randint(-1, 2, (n, k), generator=g, dtype=torch.int8)
+    packed = formats.pack_ternary(vals)
+    mod = runtime.PackedLinear(packed, torch.rand(n, generator=g) * 0.05 + 0.01, k, torch.randn(n, generator=g),
+                               mode="fp16").cuda()
+    for _ in range(2):
+        x = torch.randn(3, 21, k, generator=g).cuda()
+        got = fused_kernels.int8_matmul(x, mod, components=2, activation="silu")
+        q, qs, _ = lowbit.quantize(x, (x.stride(0), x.stride(1), x.stride(2), 21), 63, k, 2)
+        want = torch.empty(63, n, device="cuda")
+        lowbit.gemm(2, q, qs, runtime.native_words(mod), n, k, mod.scale, mod.bias, want, None, silu=True)
+        torch.cuda.synchronize()
+        assert torch.equal(got.reshape(63, n).view(torch.int32), want.view(torch.int32))

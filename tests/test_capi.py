@@ -219,3 +219,45 @@ def test_plan_refuses_what_the_direct_call_refuses():
     assert not h and b"aligned" in L.kea_last_error()
     assert L.kea_lowbit_gemm_plan_launch(None, None) == -1
     L.kea_lowbit_gemm_plan_free(None)
+
+
+def test_plan_launch_with_refuses_mismatched_buffers_before_any_launch():
+    """kea_lowbit_gemm_plan_launch_with binds new buffers to a plan: NULL plan, an unaligned or missing q, a missing
+    qs, buffers present where the plan has none (or absent where it has one) and a short split-K workspace are all
+    refused on the host; no device is touched (fake addresses)."""
+    L = _hip.lib()
+    P = ctypes.c_void_p
+
+    def plan(acc=None, split=1):
+        return L.kea_lowbit_gemm_plan(1, P(0x1000), 64 * 1024, 1024, 1, P(0x2000), 0, 64, P(0x3000), 256, 1024,
+                                      P(0x4000), 0, 0, None, 0, P(0x10000), 0, 256, acc, 256 if acc else 0, 64, 0,
+                                      split, 0, P(0x100000) if split > 1 else None, 1 << 20 if split > 1 else 0,
+                                      None, 0, 1.0)
+
+    h = plan()
+    assert h, L.kea_last_error()
+    try:
+        assert L.kea_lowbit_gemm_plan_workspace(h) == 0
+        call = L.kea_lowbit_gemm_plan_launch_with
+        assert call(None, P(0x1000), P(0x2000), P(0x10000), None, None, None, 0, None) == -1
+        assert call(h, P(0x1008), P(0x2000), P(0x10000), None, None, None, 0, None) == -2
+        assert call(h, None, P(0x2000), P(0x10000), None, None, None, 0, None) == -2
+        assert call(h, P(0x1000), None, P(0x10000), None, None, None, 0, None) == -1
+        assert call(h, P(0x1000), P(0x2000), None, None, None, None, 0, None) == -1
+        assert b"exactly where the plan has them" in L.kea_last_error()
+        assert call(h, P(0x1000), P(0x2000), P(0x10000), P(0x20000), None, None, 0, None) == -1
+        assert call(h, P(0x1000), P(0x2000), P(0x10000), None, P(0x30000), None, 0, None) == -1
+    finally:
+        L.kea_lowbit_gemm_plan_free(h)
+    hs = plan(split=4)  # a split K needs a workspace per launch: slices [S][P][M][N] int32
+    assert hs, L.kea_last_error()
+    if hs:
+        try:
+            need = L.kea_lowbit_gemm_plan_workspace(hs)
+            assert need > 0 and need % (1 * 64 * 256 * 4) == 0
+            assert L.kea_lowbit_gemm_plan_launch_with(hs, P(0x1000), P(0x2000), P(0x10000), None, None, None, 0,
+                                                      None) == -4
+            assert L.kea_lowbit_gemm_plan_launch_with(hs, P(0x1000), P(0x2000), P(0x10000), None, None, P(0x100008),
+                                                      need, None) == -2
+        finally:
+            L.kea_lowbit_gemm_plan_free(hs)
