@@ -731,6 +731,8 @@ def main(argv=None) -> int:
     ap.add_argument("--sweep", default=None, metavar="PARTS",
                     help="only time every tile configuration at the chooser's shapes for these part counts "
                          "(e.g. 1,2,3; one JSON line per shape)")
+    ap.add_argument("--sweep-wbits", default="1,2", metavar="BITS",
+                    help="--sweep: the weight widths to sweep (e.g. 1 or 1,2)")
     ap.add_argument("--probes", action="store_true",
                     help="only run the bounding probes: int8 MFMA rate by occupancy and operand data, the cost of a "
                          "cross-workgroup exchange inside one launch, and config 3's launch floors")
@@ -752,7 +754,7 @@ def main(argv=None) -> int:
         probes()
         return 0
     if args.sweep:
-        sweep(tuple(int(v) for v in args.sweep.split(",")))
+        sweep(tuple(int(v) for v in args.sweep.split(",")), tuple(int(v) for v in args.sweep_wbits.split(",")))
         return 0
     if args.case:
         import torch

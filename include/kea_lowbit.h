@@ -74,6 +74,15 @@ extern "C" {
  *   l of tile t is at index  t*J*64 + (j/4)*256 + l*wq + j%4,  wq = min(4, J - 4*(j/4)).
  * --------------------------------------------------------------------------------------------------------- */
 
+/* The 1-bit native layout has a second part after the words above, the bit-plane layout, which the wave-split GEMM
+ * reads (the LDS-ring GEMM reads the words): rows in groups of 128 (8 n-tiles, zero padded past N), k in steps of
+ * 64; for group g, k-step s and lane l, a 16-byte unit of 4 words at word index
+ *   P0 + ((g * ceil(K/64) + s) * 64 + l) * 4 + d,   P0 = ceil(N/16) * ceil(K/128) * 64 (the word part's size),
+ * whose bit 8*i + p of word d is the INVERTED sign of w[n = 128g + 16p + l%16][k = 64s + 16(l/16) + 4d + i]. Masking
+ * the unit with 0x01010101 << p gives the MFMA operand of n-tile p of the group with int8 values 0 / 2^p (p = 7:
+ * -128): one AND per 4 weights instead of an AND and a byte permute. The kernel divides the exact sum by 2^p and
+ * recovers sum q * w = sum q - 2 * sum q * bit from a row sum of q (an MFMA on an all-ones operand). */
+
 /* Number of uint32 words of the native layout for an N x K weight matrix (0 on bad sizes). */
 int64_t kea_b1_native_words(int64_t n, int64_t k);
 int64_t kea_t2_native_words(int64_t n, int64_t k);

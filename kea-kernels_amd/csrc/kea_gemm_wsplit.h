@@ -50,13 +50,46 @@ inline int wsplit_steps(int wbits, long long steps, int nw) {
 // temporaries.
 constexpr int wsplit_reg_budget(int nw) { return nw == 4 ? 320 : 160; }
 
-// LDS bytes of the partial-sum exchange: nw waves x parts x rm x nt blocks of 64 lanes x 4 int32.
-inline int wsplit_lds_bytes(int parts, const WsplitTile &t) { return t.nw * parts * t.rm * t.nt * 1024; }
+// Whether an instance reads 1-bit weights from the bit-plane part of the native layout (one v_and_b32 per 4 weights,
+// plus one MFMA per k-step for the activation row sums) rather than from the word part (a mask and a byte permute per 4
+// weights). Measured over the tile sweep's shapes on MI355X: bit-planes are 4-17% faster with one activation part on
+// tiles of 4 or 8 n-tiles and 7-10% faster with two parts on 16 x 128 tiles; on narrower tiles and at three parts the
+// extra row-sum MFMA costs more than the cheaper expansion saves (up to 10% slower on 16 x 16 tiles).
+constexpr bool wsplit_planes(int wbits, int parts, int rm, int nt) {
+    return wbits == 1 && (parts == 1 ? nt >= 4 : parts == 2 && rm == 1 && nt == 8);
+}
+
+// 16x16 blocks a wave accumulates per part and row block: the tile's nt, plus (bit-plane weights) the block of
+// activation row sums that recovers the signed products from the masked ones.
+constexpr int wsplit_blocks(bool planes, int nt) { return planes ? nt + 1 : nt; }
+
+// Registers of one wave (operands + accumulators, 32-bit): activation fragments, weights (bit-planes: one 16-byte unit
+// per k-step; words: one per n-tile and native word, which holds two k-steps at 1 bit and one at 2 bits) and the
+// accumulator blocks.
+constexpr int wsplit_regs_of(bool planes, int wbits, int parts, int rm, int nt, int s) {
+    return parts * rm * s * 4 + (planes ? 4 * s : nt * (wbits == 1 ? s / 2 : s)) +
+           parts * rm * wsplit_blocks(planes, nt) * 4;
+}
+constexpr int wsplit_regs(int wbits, int parts, int rm, int nt, int s) {
+    return wsplit_regs_of(wsplit_planes(wbits, parts, rm, nt), wbits, parts, rm, nt, s);
+}
+
+// LDS bytes of the partial-sum exchange: nw waves x parts x rm x the accumulator blocks of 64 lanes x 4 int32.
+constexpr int wsplit_lds(int wbits, int parts, int rm, int nt, int nw) {
+    return nw * parts * rm * wsplit_blocks(wsplit_planes(wbits, parts, rm, nt), nt) * 1024;
+}
+inline int wsplit_lds_bytes(int wbits, int parts, const WsplitTile &t) {
+    return wsplit_lds(wbits, parts, t.rm, t.nt, t.nw);
+}
 
 inline bool wsplit_fits(int wbits, int parts, const WsplitTile &t, int s) {
-    const int words = wbits == 1 ? s / 2 : s;
-    const int regs = parts * t.rm * s * 4 + t.nt * words + parts * t.rm * t.nt * 4;
-    return regs <= wsplit_reg_budget(t.nw) && wsplit_lds_bytes(parts, t) <= 160 * 1024;
+    return wsplit_regs(wbits, parts, t.rm, t.nt, s) <= wsplit_reg_budget(t.nw) &&
+           wsplit_lds_bytes(wbits, parts, t) <= 160 * 1024;
+}
+
+// The per-group kernel reads the word part of the 1-bit layout and keeps one accumulator block per n-tile.
+inline bool wsplit_group_regs_fit(int wbits, int parts, const WsplitTile &t, int s) {
+    return wsplit_regs_of(false, wbits, parts, t.rm, t.nt, s) <= wsplit_reg_budget(t.nw);
 }
 
 using WsplitFn = void (*)(const int8_t *, const uint32_t *, const void *, const void *, int, int, int, int, int,
@@ -104,16 +137,19 @@ inline int wsplit_group_steps(int wbits, int parts, long long k, const WsplitTil
     if (s % gq != 0 || (wbits == 1 && s % 2 != 0)) return 0;
     const long long words = wbits == 1 ? s / 2 : s, J = wbits == 1 ? (k + 127) / 128 : ksteps;
     if (words > 1 && J % 4 != 0) return 0;
-    if (!wsplit_fits(wbits, parts, t, (int)s) || wsplit_group_lds_bytes(parts, t, (int)s, gq) > 160 * 1024) return 0;
+    if (!wsplit_group_regs_fit(wbits, parts, t, (int)s) || wsplit_group_lds_bytes(parts, t, (int)s, gq) > 160 * 1024)
+        return 0;
     return (int)s;
 }
 
-// A resolved wave-split launch: kernel instance, grid, workgroup size, dynamic LDS and the dtype bits of its scales.
+// A resolved wave-split launch: kernel instance, grid, workgroup size, dynamic LDS, the dtype bits of its scales and
+// the word offset of the weight layout part it reads (the bit-plane part where wsplit_planes says so).
 struct WsplitLaunch {
     WsplitFn fn;
     dim3 grid, block;
     int lds;
     int meta;
+    long long w_off;
 };
 
 // Resolves the launch of the wave-split kernel over grid (ceil(N / BN), ceil(M / BM), splits) with `s` k-steps per
@@ -128,8 +164,8 @@ hipError_t wsplit_group_prepare(const Params &p, int wbits, int parts, int tile,
 
 // Enqueues a resolved wave-split launch on `stream`; returns the launch's hipError_t.
 inline hipError_t wsplit_enqueue(const WsplitLaunch &l, const Params &p, hipStream_t stream) {
-    hipLaunchKernelGGL(l.fn, l.grid, l.block, l.lds, stream, p.q, p.w, p.qs, p.ws, p.M, p.N, p.K, (int)p.ldq, l.meta,
-                       (int)p.part_stride, p);
+    hipLaunchKernelGGL(l.fn, l.grid, l.block, l.lds, stream, p.q, p.w + l.w_off, p.qs, p.ws, p.M, p.N, p.K,
+                       (int)p.ldq, l.meta, (int)p.part_stride, p);
     return hipGetLastError();
 }
 

@@ -8,14 +8,16 @@ namespace kea {
 hipError_t wsplit_prepare(const Params &p, int wbits, int parts, int tile, int s, int splits, bool sliced,
                           WsplitLaunch *out) {
     const WsplitTile &t = kWsplitTiles[tile];
-    // unmasked vector loads need whole k-step ranges in every workgroup and complete weight quads (or one word)
+    // unmasked vector loads need whole k-step ranges in every workgroup and complete weight quads (or one word);
+    // bit-plane units are whole per k-step
+    const bool planes = wsplit_planes(wbits, parts, t.rm, t.nt);
     const int ksteps = (p.K + 63) / 64, words = wbits == 1 ? s / 2 : s;
-    const bool ragged = (p.K % 64) != 0 || ksteps % (t.nw * s) != 0 || (words > 1 && p.J % 4 != 0);
+    const bool ragged = (p.K % 64) != 0 || ksteps % (t.nw * s) != 0 || (!planes && words > 1 && p.J % 4 != 0);
     const WsplitFn fn = parts == 1 ? wsplit_pick_p1(wbits, tile, s, sliced, ragged)
                       : parts == 2 ? wsplit_pick_p2(wbits, tile, s, sliced, ragged)
                                    : wsplit_pick_p3(wbits, tile, s, sliced, ragged);
     if (!fn) return hipErrorInvalidDeviceFunction;
-    const int lds = wsplit_lds_bytes(parts, t);
+    const int lds = wsplit_lds_bytes(wbits, parts, t);
     if (lds > 65536) {
         const hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) return e;
@@ -27,6 +29,7 @@ hipError_t wsplit_prepare(const Params &p, int wbits, int parts, int tile, int s
     out->lds = lds;
     out->meta = (p.qs_dtype == KEA_F16 ? 1 : 0) | (p.ws_dtype == KEA_F16 ? 2 : 0) |
                 (p.bias && p.bias_dtype == KEA_F16 ? 4 : 0);
+    out->w_off = planes ? b1_plane_offset(p.N, p.K) : 0;  // the bit-plane part of the 1-bit layout, or its words
     return hipSuccess;
 }
 
@@ -50,6 +53,7 @@ hipError_t wsplit_group_prepare(const Params &p, int wbits, int parts, int tile,
     const bool avec = ((uintptr_t)p.ws % 16 == 0) && ((long long)p.groups * esz) % 16 == 0;
     out->meta = (p.qs_dtype == KEA_F16 ? 1 : 0) | (p.ws_dtype == KEA_F16 ? 2 : 0) |
                 (p.bias && p.bias_dtype == KEA_F16 ? 4 : 0) | (avec ? 8 : 0);
+    out->w_off = 0;  // the word layout
     return hipSuccess;
 }
 

@@ -55,6 +55,75 @@ __device__ __forceinline__ void wsplit_load_w(const uint32_t *w, int n0, int NTI
     }
 }
 
+// 1-bit weights, bit-plane layout: the wave's S 16-byte units (one per k-step from the wave's first k-step s0) of the
+// 128-row group holding the tile (n0 / 128; every tile lies inside one group: BN divides 128). RAGGED: k-steps past
+// the matrix load its last unit (their activations are zero).
+template <int S, bool RAGGED>
+__device__ __forceinline__ void wsplit_load_planes(const uint32_t *w, int n0, int ksteps, int s0, int lane,
+                                                   uint4 (&wu)[S]) {
+    // wave-uniform base of the group's units, plus a 32-bit per-lane byte offset (SGPR-base loads)
+    const char *gb = (const char *)(w + (long long)(n0 >> 7) * ksteps * 256);
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+        const int st = RAGGED ? min(s0 + t, ksteps - 1) : s0 + t;
+        wu[t] = *(const uint4 *)(gb + ((uint32_t)st * 64u + (uint32_t)lane) * 16u);
+    }
+}
+
+// 1-bit bit-plane MFMAs over the wave's S k-steps: n-tile jn of the tile is plane p0 + jn of the group, whose operand
+// is the unit masked with 0x01010101 << plane (int8 values 0 / 2^plane, plane 7: -128; one AND per 4 weights),
+// accumulated in acc[c][i][jn]; acc[c][i][NT] accumulates the activation row sums (an all-ones operand). The exact
+// signed sums follow after the reduction (wsplit_planes_fix).
+template <int P, int RM, int NT, int S>
+__device__ __forceinline__ void wsplit_mfma_planes(const uint4 (&wu)[S], const v4i (&af)[P][RM][S], int p0,
+                                                   v4i (&acc)[P][RM][NT + 1]) {
+#pragma unroll
+    for (int c = 0; c < P; ++c)
+#pragma unroll
+        for (int i = 0; i < RM; ++i)
+#pragma unroll
+            for (int jn = 0; jn <= NT; ++jn) acc[c][i][jn] = (v4i){0, 0, 0, 0};
+    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+#pragma unroll
+        for (int jn = 0; jn < NT; ++jn) {
+            const uint32_t mask = 0x01010101u << (p0 + jn);  // wave-uniform
+            v4i bf;
+            bf[0] = (int)(wu[t].x & mask); bf[1] = (int)(wu[t].y & mask);
+            bf[2] = (int)(wu[t].z & mask); bf[3] = (int)(wu[t].w & mask);
+#pragma unroll
+            for (int c = 0; c < P; ++c)
+#pragma unroll
+                for (int i = 0; i < RM; ++i)
+                    acc[c][i][jn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af[c][i][t], acc[c][i][jn], 0, 0, 0);
+        }
+#pragma unroll
+        for (int c = 0; c < P; ++c)
+#pragma unroll
+            for (int i = 0; i < RM; ++i)
+                acc[c][i][NT] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ones, af[c][i][t], acc[c][i][NT], 0, 0, 0);
+    }
+}
+
+// The exact signed sums of a bit-plane block from its masked sum a (= 2^plane * sum q * bit; plane 7: -128 * ...)
+// and the row sum o of the same activations: sum q * w = o - 2 * sum q * bit (bit 1 = weight -1). Exact: a is a
+// multiple of 2^plane, and the shifts divide it exactly.
+template <int P>
+__device__ __forceinline__ void wsplit_planes_fix(int plane, const int (&o)[P][4], int (&a)[P][4]) {
+    if (plane == 7) {  // wave-uniform: the plane's int8 value is -128, so the masked sum is -128 * sum q * bit
+#pragma unroll
+        for (int c = 0; c < P; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) a[c][r] = o[c][0] + 2 * (a[c][r] >> 7);
+    } else {
+#pragma unroll
+        for (int c = 0; c < P; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) a[c][r] = o[c][0] - 2 * (a[c][r] >> plane);
+    }
+}
+
 // Straight-line MFMAs over the wave's S k-steps: each weight word is expanded once (1 bit: v_and + v_perm per 4
 // weights, two k-steps per word; 2 bits: one k-step per word) and feeds the RM row blocks x P parts of
 // v_mfma_i32_16x16x64_i8 with the weights as the A operand.

@@ -8,13 +8,19 @@
 // One workgroup owns a BM x BN output tile (BM = 16 * RM rows, BN = 16 * NT columns) and a range of NW * S k-steps of
 // 64; wave w of its NW waves takes the S consecutive k-steps [w * S, (w + 1) * S) of that range. Each wave:
 //   * issues every load it needs at once, before any wait: its activation fragments (one 16-byte load per lane per
-//     k-step, the MFMA operand layout of 16 rows x 64 k), its weight words (one 32-bit word per lane per native word:
-//     2 k-steps at 1 bit, 1 at 2 bits; four consecutive words of a lane come with one 128-bit load) and the epilogue's
-//     scales (raw 32-bit words whose conversion waits until the epilogue);
-//   * expands each weight word once (v_and_b32 + v_perm_b32 per 4 weights) and feeds it to the RM row blocks x P parts
-//     of v_mfma_i32_16x16x64_i8, with the weights as the A operand (a lane ends with 4 consecutive columns of a row);
+//     k-step, the MFMA operand layout of 16 rows x 64 k), its weights and the epilogue's scales (raw 32-bit words
+//     whose conversion waits until the epilogue). Weights are native words (one 32-bit word per lane per n-tile and
+//     word: 2 k-steps at 1 bit, 1 at 2 bits; four consecutive words with one 128-bit load) or, for the 1-bit
+//     instances that kea::wsplit_planes selects, the bit-plane part of the layout (one 16-byte unit per lane per
+//     k-step holds the k-step's weights of all 8 n-tiles of a 128-row group);
+//   * feeds the RM row blocks x P parts of v_mfma_i32_16x16x64_i8, with the weights as the A operand (a lane ends
+//     with 4 consecutive columns of a row). Words are expanded once (1 bit: v_and_b32 + v_perm_b32 per 4 weights;
+//     2 bits: two v_perm_b32 per 8); bit-planes: n-tile j's operand is the unit masked with 0x01010101 << plane (one
+//     v_and_b32 per 4 weights; int8 values 0 / 2^plane), plus one MFMA per k-step on an all-ones operand for the
+//     activation row sums;
 //   * writes its int32 partial tile to LDS. After one barrier the tile's 16x16 blocks are shared out over the waves,
-//     each block summed over the NW partials in wave order (integer addition: exact) and finished by the epilogue.
+//     each block summed over the NW partials in wave order (integer addition: exact) and finished by the epilogue
+//     (bit-planes: the signed sums first, row sum - 2 * masked sum / 2^plane, exact).
 // Activations at k >= the end of the K range are zeroed at load, so the (valid, never garbage) weight words there
 // contribute nothing; rows past M are clamped to row M - 1 and columns past N to the last n-tile, and neither is
 // stored. SLICED: blockIdx.z is a K slice of steps_per_slice k-steps whose exact int32 sums go to the slices
@@ -48,14 +54,17 @@ template <int WBITS, int P, int RM, int NT, int NW, int S, bool SLICED, bool RAG
 __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const uint32_t *w, const void *qs,
                                                          const void *ws, int M, int N, int K, int ldq, int meta,
                                                          int part_stride, Params p) {
-    static_assert(WBITS == 2 || S % 2 == 0, "1-bit waves take whole words (two k-steps each)");
-    constexpr int KSW = WBITS == 1 ? 2 : 1;       // k-steps per native word
+    constexpr bool PL = wsplit_planes(WBITS, P, RM, NT);  // 1-bit weights from the bit-plane part
+    static_assert(!PL || 128 % (NT * 16) == 0, "bit-plane tiles lie inside one 128-row group");
+    static_assert(WBITS == 2 || PL || S % 2 == 0, "1-bit waves take whole words (two k-steps each)");
+    constexpr int KSW = WBITS == 1 && !PL ? 2 : 1; // k-steps per native word
     constexpr int WPW = S / KSW;                  // words per lane per n-tile for one wave
     constexpr int BM = RM * 16, BN = NT * 16;
     constexpr int NB = RM * NT;                   // 16x16 blocks of the tile
+    constexpr int NBK = wsplit_blocks(PL, NT);    // accumulator blocks per part and row block (bit-planes: + row sums)
     constexpr int UB = (NB + NW - 1) / NW;        // blocks one wave finishes
-    constexpr int PART = P * RM * NT * 256;       // int32 of one wave's partial tile in LDS
-    extern __shared__ __attribute__((aligned(16))) int32_t red[];  // [NW][P][RM][NT][64 lanes][4]
+    constexpr int PART = P * RM * NBK * 256;      // int32 of one wave's partial tile in LDS
+    extern __shared__ __attribute__((aligned(16))) int32_t red[];  // [NW][P][RM][NBK][64 lanes][4]
 
     const void *const bias = p.bias;
     const long long qs_stride = p.qs_stride;
@@ -73,8 +82,11 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
 
     // ---- loads: weights, activations, epilogue scales, all issued before the first wait ----
     const uint32_t lane16 = (uint32_t)lane * 16u;  // < 1024
-    uint32_t wv[NT][WPW];
-    wsplit_load_w<NT, WPW, RAGGED>(w, n0, NTILES, J, s0 / KSW, lane16, wv);
+    // bit-planes: the units of the tile's group (w points at the layout's bit-plane part); otherwise words
+    uint4 wu[PL ? S : 1];
+    uint32_t wv[PL ? 1 : NT][PL ? 1 : WPW];
+    if constexpr (PL) wsplit_load_planes<S, RAGGED>(w, n0, ksteps, s0, lane, wu);
+    else wsplit_load_w<NT, WPW, RAGGED>(w, n0, NTILES, J, s0 / KSW, lane16, wv);
     v4i af[P][RM][S];
     {
         const int kl = (lane >> 4) * 16;          // this lane's 16 bytes of each k-step
@@ -145,11 +157,12 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
                      "s"(p.flags), "s"(p.y_dtype), "s"(p.y_vec), "s"(p.acc));
 
     // ---- MFMAs: straight-line code over the wave's S k-steps ----
-    v4i acc[P][RM][NT];
-    wsplit_mfma<WBITS, P, RM, NT, S, WPW>(wv, af, acc);
+    v4i acc[P][RM][NBK];
+    if constexpr (PL) wsplit_mfma_planes<P, RM, NT, S>(wu, af, (n0 >> 4) & 7, acc);
+    else wsplit_mfma<WBITS, P, RM, NT, S, WPW>(wv, af, acc);
 
     // ---- exact reduction over the waves through LDS ----
-    wsplit_share<P, RM, NT>(red + wave * PART, lane, acc);
+    wsplit_share<P, RM, NBK>(red + wave * PART, lane, acc);
     __syncthreads();
 
     // ---- epilogue: block b = wave + NW * u of the tile ----
@@ -160,7 +173,12 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
         if (b >= NB) break;  // wave-uniform
         const int i = b / NT, jn = b - (b / NT) * NT;
         int a[P][4];
-        wsplit_block_sum<P, RM, NT, NW>(red, i, jn, lane, a);
+        wsplit_block_sum<P, RM, NBK, NW>(red, i, jn, lane, a);
+        if constexpr (PL) {  // the signed sums from the masked sums and the activation row sums
+            int o[P][4];
+            wsplit_block_sum<P, RM, NBK, NW>(red, i, NT, lane, o);
+            wsplit_planes_fix<P>(((n0 >> 4) + jn) & 7, o, a);
+        }
         const int mt = m0 + i * 16, m = mt + (lane & 15);
         const int nt = n0 + jn * 16, nb = nt + (lane >> 4) * 4;
         if (m >= M || nb >= N) continue;
@@ -191,9 +209,8 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
 // Instances exist only for register budgets that fit (kea::wsplit_fits, checked by the host before any launch).
 template <int WBITS, int P, int RM, int NT, int NW, int S, bool SLICED, bool RAGGED>
 WsplitFn pick_fit() {
-    constexpr int words = WBITS == 1 ? S / 2 : S;
-    constexpr int regs = P * RM * S * 4 + NT * words + P * RM * NT * 4;
-    if constexpr (regs <= wsplit_reg_budget(NW) && NW * P * RM * NT * 1024 <= 160 * 1024)
+    if constexpr (wsplit_regs(WBITS, P, RM, NT, S) <= wsplit_reg_budget(NW) &&
+                  wsplit_lds(WBITS, P, RM, NT, NW) <= 160 * 1024)
         return wsplit_kernel<WBITS, P, RM, NT, NW, S, SLICED, RAGGED>;
     else
         return nullptr;

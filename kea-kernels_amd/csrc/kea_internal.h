@@ -10,6 +10,12 @@ namespace kea {
 // Records `message` as the calling thread's last error and returns `code` (a KEA_E* value or a hipError_t).
 int fail(int code, const std::string &message);
 
+// The 1-bit native layout is two parts (include/kea_lowbit.h): the word layout of 16-row n-tiles (read by the
+// LDS-ring and per-group kernels), then the bit-plane layout of 128-row groups (read by the wave-split kernel).
+// Word offset of the bit-plane part, and its size in words: 16 bytes per lane per group per k-step of 64.
+inline long long b1_plane_offset(long long n, long long k) { return (n + 15) / 16 * ((k + 127) / 128) * 64; }
+inline long long b1_plane_words(long long n, long long k) { return (n + 127) / 128 * ((k + 63) / 64) * 64 * 4; }
+
 // A dispatch packet holds each grid dimension as a 32-bit count of work-items: `blocks` workgroups of `threads`
 // work-items along one dimension must stay within it, or the launch would be truncated and leave work undone.
 inline bool fits_dispatch(long long blocks, long long threads) {

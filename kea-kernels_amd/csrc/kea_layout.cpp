@@ -4,7 +4,8 @@
 // layouts are this library's own (declared in include/kea_lowbit.h). Their role matches the reference's one-time
 // `relayout` (kk/binary/kernels.py:730-742) and the ternary `packed_t` transposition (kk/ternary/runtime.py:33-35):
 // rearrange the codes once so that the GEMM reads each wavefront's weights with one coalesced 128-bit load per lane
-// and expands them to int8 MFMA operands with a mask and a byte permute.
+// and expands them to int8 MFMA operands with a mask and a byte permute (the word part) or with a mask alone (the
+// bit-plane part of the 1-bit layout, which the wave-split kernel reads).
 #include <cstdint>
 #include <cstring>
 #include <string>
@@ -30,7 +31,7 @@ extern "C" {
 
 int64_t kea_b1_native_words(int64_t n, int64_t k) {
     if (!sizes_ok(n, k)) return 0;
-    return cdiv(n, 16) * cdiv(k, 128) * 64;
+    return kea::b1_plane_offset(n, k) + kea::b1_plane_words(n, k);
 }
 
 int64_t kea_t2_native_words(int64_t n, int64_t k) {
@@ -64,6 +65,26 @@ int kea_b1_relayout_host(const uint8_t *codes, int64_t n, int64_t k, uint32_t *w
                             if (kk < k && !((src[kk >> 3] >> (kk & 7)) & 1)) word |= 1u << (8 * i + 4 * h + d);
                         }
                 words[word_index(t, j, l, J)] = word;
+            }
+    // the bit-plane part: unit (group g, k-step s, lane l) = 4 words; bit p of byte 4d + i of the unit is the
+    // inverted sign of w[128g + 16p + l%16][64s + 16(l/16) + 4d + i] (rows and k past the matrix: 0)
+    uint32_t *planes = words + kea::b1_plane_offset(n, k);
+    const int64_t NG = cdiv(n, 128), KS = cdiv(k, 64);
+    std::memset(planes, 0, sizeof(uint32_t) * kea::b1_plane_words(n, k));
+    for (int64_t g = 0; g < NG; ++g)
+        for (int64_t s = 0; s < KS; ++s)
+            for (int l = 0; l < 64; ++l) {
+                uint32_t *unit = planes + ((g * KS + s) * 64 + l) * 4;
+                for (int p = 0; p < 8; ++p) {
+                    const int64_t row = 128 * g + 16 * p + (l % 16);
+                    if (row >= n) continue;
+                    const uint8_t *src = codes + row * row_bytes;
+                    for (int d = 0; d < 4; ++d)
+                        for (int i = 0; i < 4; ++i) {
+                            const int64_t kk = 64 * s + 16 * (l / 16) + 4 * d + i;
+                            if (kk < k && !((src[kk >> 3] >> (kk & 7)) & 1)) unit[d] |= 1u << (8 * i + p);
+                        }
+                }
             }
     return KEA_OK;
 }

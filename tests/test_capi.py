@@ -74,7 +74,7 @@ def _index(t, j, lane, J):
     return t * J * 64 + jq * 256 + lane * wq + (j - 4 * jq)
 
 
-@pytest.mark.parametrize("n,k", [(1, 1), (16, 128), (20, 300), (33, 640), (5, 1100)])
+@pytest.mark.parametrize("n,k", [(1, 1), (16, 128), (20, 300), (33, 640), (5, 1100), (130, 200)])
 def test_b1_native_layout_places_every_code(n, k):
     rng = np.random.default_rng(n * 7 + k)
     signs = np.where(rng.random((n, k)) < 0.5, -1, 1).astype(np.int8)
@@ -82,7 +82,9 @@ def test_b1_native_layout_places_every_code(n, k):
     rc, words = _words(1, codes, n, k)
     assert rc == 0
     J = -(-k // 128)
-    assert words.size == -(-n // 16) * J * 64
+    P0 = -(-n // 16) * J * 64                      # the word part, then the bit-plane part
+    KS = -(-k // 64)
+    assert words.size == P0 + -(-n // 128) * KS * 64 * 4
     # the header's formula: word j of lane l of tile t, bit 8i + 4h + d = inverted sign of w[16t + l%16][128j + ...]
     for row in range(n):
         t, c = divmod(row, 16)
@@ -93,6 +95,20 @@ def test_b1_native_layout_places_every_code(n, k):
             d, i = divmod(r, 4)
             bit = (words[_index(t, j, c + 16 * g, J)] >> (8 * i + 4 * h + d)) & 1
             assert bit == (signs[row, kk] == -1)
+    # the bit-plane part: unit (group, k-step, lane) word d, bit 8i + p = inverted sign of
+    # w[128 group + 16p + lane%16][64 kstep + 16(lane/16) + 4d + i]; rows and k past the matrix are 0
+    planes = words[P0:].reshape(-(-n // 128), KS, 64, 4)
+    expect = np.zeros_like(planes)
+    for row in range(n):
+        grp, r = divmod(row, 128)
+        pl, c = divmod(r, 16)
+        for kk in range(k):
+            s_, r2 = divmod(kk, 64)
+            g2, r2 = divmod(r2, 16)
+            d, i = divmod(r2, 4)
+            if signs[row, kk] == -1:
+                expect[grp, s_, c + 16 * g2, d] |= np.uint32(1 << (8 * i + pl))
+    assert np.array_equal(planes, expect)
     back = np.zeros_like(codes)
     assert _hip.lib().kea_b1_unlayout_host(words.ctypes.data_as(ctypes.c_void_p), n, k,
                                            back.ctypes.data_as(ctypes.c_void_p)) == 0

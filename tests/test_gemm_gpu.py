@@ -293,7 +293,7 @@ def _at_odd_offset(t: torch.Tensor) -> torch.Tensor:
 def test_f16_scales_at_odd_element_offsets_on_wave_split_tiles(tile, parts):
     """The wave-split kernel loads f16 per-token scales, weight scales and bias as the aligned 32-bit word holding
     each element and picks the half by address: vectors that start 2 bytes into a word give the oracle's bits."""
-    case = Case(1, parts, 37, 96, 2048, seed=tile + parts, bias=True)
+    case = Case(1, parts, 37, 96, 1024, seed=tile + parts, bias=True)
     qs, alpha, bias = _at_odd_offset(case.dqs), _at_odd_offset(case.dalpha), _at_odd_offset(case.dbias)
     y = torch.full((case.m, case.n), float("nan"), device=DEV, dtype=torch.float16)
     lowbit.gemm(1, case.dq, qs, case.words, case.n, case.k, alpha, bias, y, None,
