@@ -74,9 +74,13 @@ constexpr int wsplit_regs(int wbits, int parts, int rm, int nt, int s) {
     return wsplit_regs_of(wsplit_planes(wbits, parts, rm, nt), wbits, parts, rm, nt, s);
 }
 
-// LDS bytes of the partial-sum exchange: nw waves x parts x rm x the accumulator blocks of 64 lanes x 4 int32.
+// int32 of one wave's slice of the partial-sum exchange: parts x rm x nt blocks of 64 lanes x 4, plus (bit-planes) the
+// row sums, one int32 per lane for each part and row block.
+constexpr int wsplit_part(bool planes, int parts, int rm, int nt) { return parts * rm * (nt * 256 + (planes ? 64 : 0)); }
+
+// LDS bytes of the partial-sum exchange: nw wave slices.
 constexpr int wsplit_lds(int wbits, int parts, int rm, int nt, int nw) {
-    return nw * parts * rm * wsplit_blocks(wsplit_planes(wbits, parts, rm, nt), nt) * 1024;
+    return nw * wsplit_part(wsplit_planes(wbits, parts, rm, nt), parts, rm, nt) * 4;
 }
 inline int wsplit_lds_bytes(int wbits, int parts, const WsplitTile &t) {
     return wsplit_lds(wbits, parts, t.rm, t.nt, t.nw);

@@ -106,21 +106,21 @@ __device__ __forceinline__ void wsplit_mfma_planes(const uint4 (&wu)[S], const v
     }
 }
 
-// The exact signed sums of a bit-plane block from its masked sum a (= 2^plane * sum q * bit; plane 7: -128 * ...)
+// The exact signed sums of a bit-plane block from its masked sums a (= 2^plane * sum q * bit; plane 7: -128 * ...)
 // and the row sum o of the same activations: sum q * w = o - 2 * sum q * bit (bit 1 = weight -1). Exact: a is a
 // multiple of 2^plane, and the shifts divide it exactly.
 template <int P>
-__device__ __forceinline__ void wsplit_planes_fix(int plane, const int (&o)[P][4], int (&a)[P][4]) {
+__device__ __forceinline__ void wsplit_planes_fix(int plane, const int (&o)[P], int (&a)[P][4]) {
     if (plane == 7) {  // wave-uniform: the plane's int8 value is -128, so the masked sum is -128 * sum q * bit
 #pragma unroll
         for (int c = 0; c < P; ++c)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) a[c][r] = o[c][0] + 2 * (a[c][r] >> 7);
+            for (int r = 0; r < 4; ++r) a[c][r] = o[c] + 2 * (a[c][r] >> 7);
     } else {
 #pragma unroll
         for (int c = 0; c < P; ++c)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) a[c][r] = o[c][0] - 2 * (a[c][r] >> plane);
+            for (int r = 0; r < 4; ++r) a[c][r] = o[c] - 2 * (a[c][r] >> plane);
     }
 }
 
@@ -163,21 +163,25 @@ __device__ __forceinline__ void wsplit_mfma(const uint32_t (&wv)[NT][WPW], const
     }
 }
 
-// Writes the wave's partial tile to its LDS slice ([P][RM][NT][64 lanes][4] int32); a barrier must follow.
-template <int P, int RM, int NT>
-__device__ __forceinline__ void wsplit_share(int32_t *mine, int lane, const v4i (&acc)[P][RM][NT]) {
+// Writes the wave's partial tile to its LDS slice: the NT blocks [P][RM][NT][64 lanes][4] int32, then (bit-planes,
+// ROWS) the row-sum block compacted to one int32 per lane, [P][RM][64] (its 4 components are equal: every row of the
+// all-ones operand is the same); a barrier must follow.
+template <int P, int RM, int NT, bool ROWS, int NA>
+__device__ __forceinline__ void wsplit_share(int32_t *mine, int lane, const v4i (&acc)[P][RM][NA]) {
 #pragma unroll
     for (int c = 0; c < P; ++c)
 #pragma unroll
-        for (int i = 0; i < RM; ++i)
+        for (int i = 0; i < RM; ++i) {
 #pragma unroll
             for (int jn = 0; jn < NT; ++jn) *(v4i *)(mine + ((c * RM + i) * NT + jn) * 256 + lane * 4) = acc[c][i][jn];
+            if constexpr (ROWS) mine[P * RM * NT * 256 + (c * RM + i) * 64 + lane] = acc[c][i][NT][0];
+        }
 }
 
-// The exact sum over the NW wave partials of block (i, jn) for this lane's 4 outputs, in wave order.
-template <int P, int RM, int NT, int NW>
+// The exact sum over the NW wave partials (slices PART int32 apart) of block (i, jn) for this lane's 4 outputs, in
+// wave order.
+template <int P, int RM, int NT, int NW, int PART>
 __device__ __forceinline__ void wsplit_block_sum(const int32_t *red, int i, int jn, int lane, int (&a)[P][4]) {
-    constexpr int PART = P * RM * NT * 256;
 #pragma unroll
     for (int c = 0; c < P; ++c) {
         const int32_t *src = red + ((c * RM + i) * NT + jn) * 256 + lane * 4;
@@ -186,6 +190,19 @@ __device__ __forceinline__ void wsplit_block_sum(const int32_t *red, int i, int 
         for (int v = 1; v < NW; ++v) sum += *(const v4i *)(src + v * PART);
 #pragma unroll
         for (int r = 0; r < 4; ++r) a[c][r] = sum[r];
+    }
+}
+
+// The exact sum over the NW wave partials of the compacted row sums of row block i (bit-planes), in wave order.
+template <int P, int RM, int NT, int NW, int PART>
+__device__ __forceinline__ void wsplit_rows_sum(const int32_t *red, int i, int lane, int (&o)[P]) {
+#pragma unroll
+    for (int c = 0; c < P; ++c) {
+        const int32_t *src = red + P * RM * NT * 256 + (c * RM + i) * 64 + lane;
+        int sum = src[0];
+#pragma unroll
+        for (int v = 1; v < NW; ++v) sum += src[v * PART];
+        o[c] = sum;
     }
 }
 

@@ -63,8 +63,8 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
     constexpr int NB = RM * NT;                   // 16x16 blocks of the tile
     constexpr int NBK = wsplit_blocks(PL, NT);    // accumulator blocks per part and row block (bit-planes: + row sums)
     constexpr int UB = (NB + NW - 1) / NW;        // blocks one wave finishes
-    constexpr int PART = P * RM * NBK * 256;      // int32 of one wave's partial tile in LDS
-    extern __shared__ __attribute__((aligned(16))) int32_t red[];  // [NW][P][RM][NBK][64 lanes][4]
+    constexpr int PART = wsplit_part(PL, P, RM, NT);  // int32 of one wave's partial tile in LDS
+    extern __shared__ __attribute__((aligned(16))) int32_t red[];  // [NW][PART]: blocks, then compacted row sums
 
     const void *const bias = p.bias;
     const long long qs_stride = p.qs_stride;
@@ -139,9 +139,9 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
             if (bias) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) rb[u][r] = load_raw(bias, b16, min(nb + r, N - 1));
-            } else {
+            } else {  // the f32 bits of kNoBias (b16 is clear without a bias), so the epilogue needs no branch
 #pragma unroll
-                for (int r = 0; r < 4; ++r) rb[u][r] = 0u;
+                for (int r = 0; r < 4; ++r) rb[u][r] = 0x80000000u;
             }
             if (p.res) load_residual(p, m, nb, rr[u]);
         }
@@ -162,7 +162,7 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
     else wsplit_mfma<WBITS, P, RM, NT, S, WPW>(wv, af, acc);
 
     // ---- exact reduction over the waves through LDS ----
-    wsplit_share<P, RM, NBK>(red + wave * PART, lane, acc);
+    wsplit_share<P, RM, NT, PL>(red + wave * PART, lane, acc);
     __syncthreads();
 
     // ---- epilogue: block b = wave + NW * u of the tile ----
@@ -173,10 +173,10 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
         if (b >= NB) break;  // wave-uniform
         const int i = b / NT, jn = b - (b / NT) * NT;
         int a[P][4];
-        wsplit_block_sum<P, RM, NBK, NW>(red, i, jn, lane, a);
+        wsplit_block_sum<P, RM, NT, NW, PART>(red, i, jn, lane, a);
         if constexpr (PL) {  // the signed sums from the masked sums and the activation row sums
-            int o[P][4];
-            wsplit_block_sum<P, RM, NBK, NW>(red, i, NT, lane, o);
+            int o[P];
+            wsplit_rows_sum<P, RM, NT, NW, PART>(red, i, lane, o);
             wsplit_planes_fix<P>(((n0 >> 4) + jn) & 7, o, a);
         }
         const int mt = m0 + i * 16, m = mt + (lane & 15);
@@ -195,7 +195,7 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
             for (int r = 0; r < 4; ++r) {
                 const int n = min(nb + r, N - 1);
                 e.alpha[r] = raw_to_f32(ra[u][r], ws16, ws, (uint32_t)n);
-                e.bias[r] = bias ? raw_to_f32(rb[u][r], b16, bias, (uint32_t)n) : kNoBias;
+                e.bias[r] = raw_to_f32(rb[u][r], b16, bias, (uint32_t)n);
             }
             if (p.res) {
 #pragma unroll
