@@ -233,8 +233,9 @@ def launch_floors(d, stream, tile_name: str, reps: int = 10, shape=(M, N, K), wa
 def probes() -> None:
     """--probes: what bounds the GEMMs, one JSON line per measurement.
 
-    * mfma: the int8 MFMA loop (kea_probe_mfma_i8_operands) at 1, 2, 4 and 8 waves per SIMD, on the fixed operand
-      pattern and on random bytes (the GEMM's kind of data), best of 5 launches;
+    * mfma: the int8 MFMA loop at 1, 2, 4 and 8 waves per SIMD, on the fixed operand pattern and on random bytes (the
+      GEMM's kind of data), best of 5 launches, for both int8 instruction shapes: v_mfma_i32_16x16x64_i8
+      (kea_probe_mfma_i8_operands, the one the GEMMs use) and v_mfma_i32_32x32x32_i8 (kea_probe_mfma_i8_32);
     * exchange: what handing data to the last-arriving workgroup of a group costs inside one launch
       (kea_probe_exchange: writes only, + a relaxed arrival count, + an acquire-release count and the read), graphs of
       100 launches, at the group sizes an in-launch split-K (4) and a whole-grid exchange need;
@@ -270,16 +271,18 @@ def probes() -> None:
                 "random": torch.randint(-2 ** 31, 2 ** 31 - 1, (128, 4), generator=g, dtype=torch.int64)
                 .to(torch.int32).to(dev)}
     out = torch.empty(2048 * 256, dtype=torch.int32, device=dev)
-    for data, ops_t in operands.items():
-        for blocks in (256, 512, 1024, 2048):
-            iters = 2000
-            def run(blocks=blocks, ops_t=ops_t):
-                rc = L.kea_probe_mfma_i8_operands(blocks, iters, vp(ops_t.data_ptr() if ops_t is not None else 0),
-                                                  vp(out.data_ptr()), vp(stream.cuda_stream))
-                kea_probes.check(rc, "kea_probe_mfma_i8_operands")
-            t = best_of(run)
-            print(json.dumps({"probe": "mfma", "operands": data, "waves_per_simd": blocks // 256,
-                              "tops": round(L.kea_probe_mfma_i8_ops(blocks, iters) / t / 1e12, 1)}), flush=True)
+    shapes = {"16x16x64": (L.kea_probe_mfma_i8_operands, L.kea_probe_mfma_i8_ops, 2000),
+              "32x32x32": (L.kea_probe_mfma_i8_32, L.kea_probe_mfma_i8_32_ops, 1000)}
+    for shape, (fn, ops_fn, iters) in shapes.items():
+        for data, ops_t in operands.items():
+            for blocks in (256, 512, 1024, 2048):
+                def run(blocks=blocks, ops_t=ops_t, fn=fn, iters=iters):
+                    rc = fn(blocks, iters, vp(ops_t.data_ptr() if ops_t is not None else 0), vp(out.data_ptr()),
+                            vp(stream.cuda_stream))
+                    kea_probes.check(rc, "kea_probe_mfma")
+                t = best_of(run)
+                print(json.dumps({"probe": "mfma", "shape": shape, "operands": data, "waves_per_simd": blocks // 256,
+                                  "tops": round(ops_fn(blocks, iters) / t / 1e12, 1)}), flush=True)
 
     for wgs in (64, 256, 1024):
         for nbytes in (1024, 16384):

@@ -31,6 +31,12 @@ int kea_probe_mfma_i8_operands(int64_t blocks, int64_t iters, const int32_t *ope
 /* The ops one kea_probe_mfma_i8 launch performs (0 for arguments it would reject). */
 int64_t kea_probe_mfma_i8_ops(int64_t blocks, int64_t iters);
 
+/* The same loop on v_mfma_i32_32x32x32_i8 (65536 int8 ops each; the same 16 operand bytes per lane, read as 32 rows x
+ * 32 k), eight independent 16-register accumulators per wave, `operands` as for kea_probe_mfma_i8_operands (or NULL).
+ * Ops per launch: kea_probe_mfma_i8_32_ops(blocks, iters) = blocks * 4 * iters * 8 * 65536. */
+int kea_probe_mfma_i8_32(int64_t blocks, int64_t iters, const int32_t *operands, int32_t *out, void *stream);
+int64_t kea_probe_mfma_i8_32_ops(int64_t blocks, int64_t iters);
+
 /* Keeps the stream busy for `ns` nanoseconds (one wavefront spinning on the device's constant-rate wall clock, so
  * it always ends): enqueued in front of a timed region, it lets the host finish submitting the region's work before
  * the region's start event executes, so host submission latency stays out of the measurement. ns in [0, 1e8]. */

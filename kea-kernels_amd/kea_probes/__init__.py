@@ -19,6 +19,8 @@ SIGNATURES = {
     "kea_probe_mfma_i8": (_i32, [_i64, _i64, _vp, _vp]),
     "kea_probe_mfma_i8_ops": (_i64, [_i64, _i64]),
     "kea_probe_mfma_i8_operands": (_i32, [_i64, _i64, _vp, _vp, _vp]),
+    "kea_probe_mfma_i8_32": (_i32, [_i64, _i64, _vp, _vp, _vp]),
+    "kea_probe_mfma_i8_32_ops": (_i64, [_i64, _i64]),
     "kea_probe_exchange": (_i32, [_i32, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "kea_probe_floor": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _i64, _vp]),
     "kea_probe_floor_waves": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _vp]),

@@ -52,6 +52,35 @@ __global__ void __launch_bounds__(256) mfma_i8_loop(int iters, const v4i *operan
     out[(int64_t)blockIdx.x * 256 + threadIdx.x] = (int32_t)s;
 }
 
+// The same loop on v_mfma_i32_32x32x32_i8 (65536 int8 ops each, 16 accumulator registers per chain): the operands are
+// the same 16 bytes per lane, which this instruction reads as 32 rows x 32 k instead of 16 rows x 64 k.
+typedef int v16i __attribute__((ext_vector_type(16)));
+__global__ void __launch_bounds__(256) mfma_i8_loop32(int iters, const v4i *operands, int32_t *out) {
+    const int lane = threadIdx.x & 63;
+    v4i a = {0x01020304 + lane, 0x05060708 - lane, 0x090A0B0C ^ lane, 0x0D0E0F10 + 3 * lane};
+    v4i b = {0x11121314 - lane, 0x15161718 + lane, 0x191A1B1C ^ (lane << 8), 0x1D1E1F20 + 5 * lane};
+    if (operands) {
+        a = operands[lane];
+        b = operands[64 + lane];
+    }
+    v16i acc[kProbeChains];
+#pragma unroll
+    for (int c = 0; c < kProbeChains; ++c) {
+        acc[c] = (v16i){};
+        acc[c][0] = c;
+    }
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int c = 0; c < kProbeChains; ++c) acc[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[c], 0, 0, 0);
+    }
+    uint32_t s = 0;  // wrapping sum
+#pragma unroll
+    for (int c = 0; c < kProbeChains; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += (uint32_t)acc[c][r];
+    out[(int64_t)blockIdx.x * 256 + threadIdx.x] = (int32_t)s;
+}
+
 bool probe_args_ok(int64_t blocks, int64_t iters) {
     return blocks >= 1 && blocks <= 65536 && iters >= 1 && iters <= (1 << 20);
 }
@@ -181,6 +210,21 @@ int kea_probe_mfma_i8_operands(int64_t blocks, int64_t iters, const int32_t *ope
 
 int kea_probe_mfma_i8(int64_t blocks, int64_t iters, int32_t *out, void *stream) {
     return kea_probe_mfma_i8_operands(blocks, iters, nullptr, out, stream);
+}
+
+int64_t kea_probe_mfma_i8_32_ops(int64_t blocks, int64_t iters) { return 2 * kea_probe_mfma_i8_ops(blocks, iters); }
+
+int kea_probe_mfma_i8_32(int64_t blocks, int64_t iters, const int32_t *operands, int32_t *out, void *stream) {
+    if (!probe_args_ok(blocks, iters))
+        return fail(KEA_EINVAL, "kea_probe_mfma_i8_32: blocks must be in [1, 65536] and iters in [1, 2^20]");
+    if (!out) return fail(KEA_EINVAL, "kea_probe_mfma_i8_32: out is null");
+    if ((uintptr_t)out & 3) return fail(KEA_EALIGN, "kea_probe_mfma_i8_32: out must be 4-byte aligned");
+    if ((uintptr_t)operands & 15) return fail(KEA_EALIGN, "kea_probe_mfma_i8_32: operands must be 16-byte aligned");
+    hipLaunchKernelGGL(mfma_i8_loop32, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (int)iters,
+                       (const v4i *)operands, out);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail((int)e, std::string("kea_probe_mfma_i8_32: ") + hipGetErrorString(e));
+    return 0;
 }
 
 int kea_probe_spin(int64_t ns, void *stream) {
