@@ -231,24 +231,15 @@ __global__ void __launch_bounds__(NW * 64) wsplit_group_kernel(const int8_t *q, 
     }
     using IV = int __attribute__((ext_vector_type(OPT)));
     using FV = float __attribute__((ext_vector_type(OPT)));
-    // register-held alpha as f32, converted once, outside the chains
-    float af32[AREG ? GWG : 1];
-    if constexpr (AREG) {
-        // one loop per dtype, so every register index is a compile-time constant
-        if (ws16) {
-#pragma unroll
-            for (int g = 0; g < GWG; ++g)
-                af32[g] = (float)__builtin_bit_cast(_Float16, (uint16_t)(araw[0][g / 2] >> (16 * (g & 1))));
-        } else {
-#pragma unroll
-            for (int g = 0; g < GWG; ++g) af32[g] = __builtin_bit_cast(float, araw[0][g]);
-        }
-    }
-    // the fold, with the full-K sums for acc_out only when they are wanted (two copies: no dead adds in the chains).
-    // The group sums are read from LDS in chunks of CH groups (at most 64 registers), every read of a chunk issued
-    // before the first use, so the LDS latency is paid once per chunk rather than once per group.
+    // the fold, in copies specialised on acc_out (the full-K sums only when they are wanted: no dead adds in the chains)
+    // and on the dtype of register-held alpha (every register index a compile-time constant, no per-group branch).
+    // f16 alpha enters each fma as its f16 half: the conversion is exact and the compiler folds it into the fma
+    // (v_fma_mix_f32), so no separate conversion is spent on it. The group sums are read from LDS in chunks of CH groups
+    // (at most 64 registers), every read of a chunk issued before the first use, so the LDS latency is paid once per
+    // chunk rather than once per group.
     constexpr int CH = (64 / (P * OPT)) < GWG ? (64 / (P * OPT) > 0 ? 64 / (P * OPT) : 1) : GWG;
-    auto fold_groups = [&](auto with_acc) {
+    auto fold_groups = [&](auto with_acc, auto f16_tag) {
+        constexpr bool F16A = decltype(f16_tag)::value;
 #pragma unroll
         for (int g0 = 0; g0 < GWG; g0 += CH) {
             IV a[CH][P];
@@ -263,8 +254,12 @@ __global__ void __launch_bounds__(NW * 64) wsplit_group_kernel(const int8_t *q, 
                 const int g = g0 + i;
                 if (g >= GWG) break;
                 FV al;
-                if constexpr (AREG) al[0] = af32[g];
-                else al = *(const FV *)(alpha + g * APAD + ocol);
+                if constexpr (AREG && F16A)
+                    al[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(araw[0][g / 2] >> (16 * (g & 1))));
+                else if constexpr (AREG)
+                    al[0] = __builtin_bit_cast(float, araw[0][g]);
+                else
+                    al = *(const FV *)(alpha + g * APAD + ocol);
 #pragma unroll
                 for (int j = 0; j < OPT; ++j) {
                     int ar[3] = {a[i][0][j], P > 1 ? a[i][1 % P][j] : 0, P > 2 ? a[i][2 % P][j] : 0};
@@ -277,8 +272,13 @@ __global__ void __launch_bounds__(NW * 64) wsplit_group_kernel(const int8_t *q, 
             }
         }
     };
-    if (p.acc) fold_groups(std::true_type{});
-    else fold_groups(std::false_type{});
+    if (AREG && ws16) {
+        if (p.acc) fold_groups(std::true_type{}, std::true_type{});
+        else fold_groups(std::false_type{}, std::true_type{});
+    } else {
+        if (p.acc) fold_groups(std::true_type{}, std::false_type{});
+        else fold_groups(std::false_type{}, std::false_type{});
+    }
     // ---- epilogue of each output: r + bias, SiLU, residual, store; acc_out = the sum of the group sums ----
     const int m = m0 + orow;
     if (!fold || m >= M) return;
