@@ -116,18 +116,25 @@ constexpr int wsplit_group_opt(int nt, int nw) {
     return 256 * nt >= nw * 64 * 4 ? 4 : 256 * nt >= nw * 64 * 2 ? 2 : 1;
 }
 
-// Whether a per-group launch holds each thread's alpha values in registers (threads folding one output, at most 64
-// groups), loaded straight from [N][G]; otherwise the tile's alpha block is staged in LDS. (Register-held alpha for two
+// Whether a per-group launch holds each thread's alpha values in registers (threads folding one output, with room in
+// the wave's register budget for the tile's operands and accumulators, the G alpha words and a 64-register chunk of
+// group sums); otherwise the tile's alpha block is staged in LDS as f32 and read per group. (Register-held alpha for two
 // outputs a thread measured slower than LDS staging: 9.6 against 6.3 us at config 2 on the 16x32 k/4 tile.)
-constexpr bool wsplit_group_alpha_regs(int nt, int nw, int groups) {
-    return wsplit_group_opt(nt, nw) == 1 && groups <= 64;
+constexpr bool wsplit_group_alpha_regs(int parts, int nt, int nw, int s, int gq) {
+    const int groups = nw * (s / gq);
+    return wsplit_group_opt(nt, nw) == 1 && groups <= 64 &&
+           parts * s * 4 + nt * s + parts * nt * 4 + groups + 64 <= wsplit_reg_budget(nw);
 }
 
 // LDS bytes of a per-group launch: each of the tile's nw * s / gq groups has its int32 sums (parts x nt blocks of 64
-// lanes x 4) and, unless alpha is held in registers, its staged f32 alpha row (16 * nt + 4 floats).
+// lanes x 4) and its staged alpha: with alpha held in registers the tile's raw [16 * nt][G] block (f32 at most),
+// otherwise one f32 row of 16 * nt + 4 floats per group.
+constexpr int wsplit_group_lds(int parts, int nt, int nw, int s, int gq) {
+    return nw * (s / gq) * (parts * nt * 1024 + (wsplit_group_alpha_regs(parts, nt, nw, s, gq) ? nt * 16 * 4
+                                                                                                   : (nt * 16 + 4) * 4));
+}
 inline int wsplit_group_lds_bytes(int parts, const WsplitTile &t, int s, int gq) {
-    const int groups = t.nw * (s / gq);
-    return groups * (parts * t.nt * 1024 + (wsplit_group_alpha_regs(t.nt, t.nw, groups) ? 0 : (t.nt * 16 + 4) * 4));
+    return wsplit_group_lds(parts, t.nt, t.nw, s, gq);
 }
 
 // k-steps per wave of a per-group launch of tile t at this K (one workgroup covering K exactly with whole groups per

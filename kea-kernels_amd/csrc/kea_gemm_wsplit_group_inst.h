@@ -149,46 +149,41 @@ __global__ void __launch_bounds__(NW * 64) wsplit_group_kernel(const int8_t *q, 
             rr[j] = p.res ? p.res[(long long)m * p.ldr + n] : 0.f;
         }
     }
-    // alpha: with few values per thread (AREG) each thread's own columns x groups as raw words in registers (f16: two
-    // groups a word), loaded straight from [N][G] (meta bit 3: rows 16-byte aligned, whole 16-byte units: vector
-    // loads); otherwise the tile's block [GWG groups][BN columns], clamped into [N][G] (the clamped values are never
-    // stored), is staged in LDS as f32, consecutive threads taking consecutive groups of one column.
+    // alpha: with few values per thread (AREG) each thread's own column's G values as raw words in registers (f16: two
+    // groups a word). Meta bit 3 (rows 16-byte aligned, whole 16-byte units): the tile's block of alpha, BN rows of
+    // [N][G] and so one contiguous range, is loaded once with one 16-byte load per thread of the first BN * G * esz / 16
+    // (units past row N - 1 clamped to the last unit in the array: their columns are never stored), staged in LDS
+    // through the barrier, and each thread then reads its column's row from LDS (16 threads share a column: one global
+    // load of each byte instead of sixteen). Otherwise each thread loads its row element by element. Without AREG the
+    // tile's block [GWG groups][BN columns], clamped into [N][G] (the clamped values are never stored), is staged in
+    // LDS as f32, consecutive threads taking consecutive groups of one column.
     const int G = p.groups;  // == GWG (checked by the host)
-    constexpr bool AREG = wsplit_group_alpha_regs(NT, NW, GWG);
+    constexpr bool AREG = wsplit_group_alpha_regs(P, NT, NW, S, GQ);
+    static_assert(!AREG || OPT == 1, "register-held alpha serves one output a thread");
     constexpr int AW = AREG ? GWG : 1;
     uint32_t araw[OPT][AW];
     constexpr int AL = AREG ? 1 : (GWG * BN + NW * 64 - 1) / (NW * 64);
     float av[AL];
+    static_assert(!AREG || BN * GWG * 4 <= NW * 64 * 16, "one 16-byte unit of the alpha block per thread at most");
+    const bool avec = (meta >> 3) & 1;
+    const int arow = GWG * (ws16 ? 2 : 4);  // bytes of one alpha row
+    uint4 ast = make_uint4(0u, 0u, 0u, 0u);
     if constexpr (AREG) {
-        const bool avec = (meta >> 3) & 1;
-#pragma unroll
-        for (int j = 0; j < OPT; ++j) {
-            const int n = min(n0 + ocol + j, N - 1);
+        if (avec) {
+            if ((int)threadIdx.x * 16 < BN * arow)
+                ast = *(const uint4 *)((const char *)ws + (long long)n0 * arow +
+                                       min((int)threadIdx.x * 16, (N - n0) * arow - 16));
+        } else {
+            const int n = min(n0 + ocol, N - 1);
             if (ws16) {
                 const uint16_t *row = (const uint16_t *)ws + (long long)n * G;
-                if (avec) {
 #pragma unroll
-                    for (int i = 0; i < GWG / 8; ++i) {
-                        const uint4 v = ((const uint4 *)row)[i];
-                        araw[j][4 * i] = v.x; araw[j][4 * i + 1] = v.y; araw[j][4 * i + 2] = v.z; araw[j][4 * i + 3] = v.w;
-                    }
-                } else {
-#pragma unroll
-                    for (int g = 0; g < GWG; g += 2)
-                        araw[j][g / 2] = (uint32_t)row[g] | ((uint32_t)row[min(g + 1, GWG - 1)] << 16);
-                }
+                for (int g = 0; g < GWG; g += 2)
+                    araw[0][g / 2] = (uint32_t)row[g] | ((uint32_t)row[min(g + 1, GWG - 1)] << 16);
             } else {
                 const uint32_t *row = (const uint32_t *)ws + (long long)n * G;
-                if (avec) {
 #pragma unroll
-                    for (int i = 0; i < GWG / 4; ++i) {
-                        const uint4 v = ((const uint4 *)row)[i];
-                        araw[j][4 * i] = v.x; araw[j][4 * i + 1] = v.y; araw[j][4 * i + 2] = v.z; araw[j][4 * i + 3] = v.w;
-                    }
-                } else {
-#pragma unroll
-                    for (int g = 0; g < GWG; ++g) araw[j][g] = row[g];
-                }
+                for (int g = 0; g < GWG; ++g) araw[0][g] = row[g];
             }
         }
     } else {
@@ -205,6 +200,10 @@ __global__ void __launch_bounds__(NW * 64) wsplit_group_kernel(const int8_t *q, 
 
     // ---- MFMAs, one group at a time, each group's sums to its LDS slot ----
     group_mfma<WBITS, P, NT, S, WPW, GQ>(wv, af, lds + wave * GW * SLOT, lane);
+    uint8_t *astage = (uint8_t *)(lds + GWG * SLOT);  // AREG: the staged alpha block, raw [BN][G] bytes
+    if constexpr (AREG) {
+        if (avec && (int)threadIdx.x * 16 < BN * arow) *(uint4 *)(astage + threadIdx.x * 16) = ast;
+    }
     if constexpr (!AREG) {
 #pragma unroll
         for (int i = 0; i < AL; ++i) {
@@ -214,6 +213,25 @@ __global__ void __launch_bounds__(NW * 64) wsplit_group_kernel(const int8_t *q, 
         }
     }
     __syncthreads();
+    if constexpr (AREG) {
+        if (avec) {
+            // one loop per dtype, so every register index is a compile-time constant
+            const uint4 *src = (const uint4 *)(astage + ocol * arow);
+            if (ws16) {
+#pragma unroll
+                for (int i = 0; i < GWG / 8; ++i) {
+                    const uint4 v = src[i];
+                    araw[0][4 * i] = v.x; araw[0][4 * i + 1] = v.y; araw[0][4 * i + 2] = v.z; araw[0][4 * i + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < GWG / 4; ++i) {
+                    const uint4 v = src[i];
+                    araw[0][4 * i] = v.x; araw[0][4 * i + 1] = v.y; araw[0][4 * i + 2] = v.z; araw[0][4 * i + 3] = v.w;
+                }
+            }
+        }
+    }
 
     // ---- fold: every group of K in order (the host runs these instances with G == GWG: all of K is this
     // workgroup's), one FP32 chain per output ----
@@ -307,7 +325,7 @@ template <int WBITS, int P, int NT, int NW, int S, int GQ>
 WsplitFn group_fit() {
     constexpr int words = WBITS == 1 ? S / 2 : S;
     constexpr int regs = P * S * 4 + NT * words + P * NT * 4;
-    constexpr int lds = NW * (S / GQ) * (P * NT * 1024 + (wsplit_group_alpha_regs(NT, NW, NW * (S / GQ)) ? 0 : (NT * 16 + 4) * 4));
+    constexpr int lds = wsplit_group_lds(P, NT, NW, S, GQ);
     if constexpr (S % GQ == 0 && (WBITS == 2 || S % 2 == 0) && regs <= wsplit_reg_budget(NW) && lds <= 160 * 1024)
         return wsplit_group_kernel<WBITS, P, NT, NW, S, GQ>;
     else

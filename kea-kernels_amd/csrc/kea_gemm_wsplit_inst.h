@@ -139,9 +139,9 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
             if (bias) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) rb[u][r] = load_raw(bias, b16, min(nb + r, N - 1));
-            } else {  // the f32 bits of kNoBias (b16 is clear without a bias), so the epilogue needs no branch
+            } else {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) rb[u][r] = 0x80000000u;
+                for (int r = 0; r < 4; ++r) rb[u][r] = 0u;
             }
             if (p.res) load_residual(p, m, nb, rr[u]);
         }
@@ -195,7 +195,7 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
             for (int r = 0; r < 4; ++r) {
                 const int n = min(nb + r, N - 1);
                 e.alpha[r] = raw_to_f32(ra[u][r], ws16, ws, (uint32_t)n);
-                e.bias[r] = raw_to_f32(rb[u][r], b16, bias, (uint32_t)n);
+                e.bias[r] = bias ? raw_to_f32(rb[u][r], b16, bias, (uint32_t)n) : kNoBias;
             }
             if (p.res) {
 #pragma unroll
