@@ -74,9 +74,11 @@ extern "C" {
  *   l of tile t is at index  t*J*64 + (j/4)*256 + l*wq + j%4,  wq = min(4, J - 4*(j/4)).
  * --------------------------------------------------------------------------------------------------------- */
 
-/* The 1-bit native layout has a second part after the words above, the bit-plane layout, which the wave-split GEMM
- * reads (the LDS-ring GEMM reads the words): rows in groups of 128 (8 n-tiles, zero padded past N), k in steps of
- * 64; for group g, k-step s and lane l, a 16-byte unit of 4 words at word index
+/* The 1-bit native layout has a second part after the words above, the bit-plane layout, which the wide wave-split
+ * tiles read (one activation part on tiles of 4 or 8 n-tiles, two parts on 16x128 tiles; the LDS-ring GEMM, the
+ * per-group kernel and the other wave-split tiles read the words), so a 1-bit weight takes 2 bits resident: rows in
+ * groups of 128 (8 n-tiles, zero padded past N), k in steps of 64; for group g, k-step s and lane l, a 16-byte unit
+ * of 4 words at word index
  *   P0 + ((g * ceil(K/64) + s) * 64 + l) * 4 + d,   P0 = ceil(N/16) * ceil(K/128) * 64 (the word part's size),
  * whose bit 8*i + p of word d is the INVERTED sign of w[n = 128g + 16p + l%16][k = 64s + 16(l/16) + 4d + i]. Masking
  * the unit with 0x01010101 << p gives the MFMA operand of n-tile p of the group with int8 values 0 / 2^p (p = 7:
@@ -106,7 +108,9 @@ int kea_t2_unlayout_host(const uint32_t *words_host, int64_t n, int64_t k, uint8
  *                                                P = 3: fma(f(a2), s2, <P = 2 form>)
  *     r = bias ? fma(r, alpha[n], bias[n]) : r * alpha[n]
  *   per-group scales (ws_group = 64, 128 or 256; alpha is [N][ceil(K/ws_group)] row-major, group g covering
- *   k in [g*ws_group, (g+1)*ws_group); tile configs 0, 1 and 4 only, unsplit: split_k 0 or 1):
+ *   k in [g*ws_group, (g+1)*ws_group); unsplit, split_k 0 or 1; config 0, ring tile 1 or 4, or a wave-split tile of
+ *   16-row blocks and at most 64 columns whose one workgroup covers K exactly, K = waves x 64 x 2..16 with whole
+ *   groups per wave):
  *     r = 0; for g in groups: r = fma(comb_P(acc_g, s), alpha[n][g], r);  r = bias ? r + bias[n] : r
  *   SiLU (flags & KEA_FLAG_SILU): r = r / (1 + exp(-r)); then y[m*ldy + n] = RN(r) in y_dtype.
  *   f() is int32 -> fp32 round-to-nearest; every FP32 operation is IEEE round-to-nearest-even, unfused
