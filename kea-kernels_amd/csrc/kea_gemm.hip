@@ -374,6 +374,9 @@ int gemm_prepare(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, i
     if (((uintptr_t)q & 15) || (ldq & 15) || (parts > 1 && (part_stride & 15)))
         return kea::fail(KEA_EALIGN, "q needs 16-byte aligned rows: q % 16 == 0, ldq % 16 == 0, part_stride % 16 == 0");
     if ((uintptr_t)w & 15) return kea::fail(KEA_EALIGN, "weight words must be 16-byte aligned");
+    const auto misaligned = [](const void *v, int dtype) { return ((uintptr_t)v & (dtype == KEA_F32 ? 3 : 1)) != 0; };
+    if (misaligned(qs, qs_dtype) || misaligned(wscale, ws_dtype) || (bias && misaligned(bias, bias_dtype)))
+        return kea::fail(KEA_EALIGN, "qs, wscale and bias must be aligned to their element size");
     if ((int64_t)(parts - 1) * part_stride + m * ldq > (int64_t)INT32_MAX)
         return kea::fail(KEA_EINVAL, "q spans more than 2 GiB: split the call along M");
 

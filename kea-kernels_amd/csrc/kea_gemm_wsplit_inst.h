@@ -123,8 +123,10 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
     // epilogue scales of the blocks this wave finishes: raw words now, converted in the epilogue; and their residual
     // values, which would otherwise be a memory round trip after the reduction (the residual may be y itself: each
     // element is read here and written later by this same lane, so in-place updates stay exact)
-    uint32_t rs[UB][3], ra[UB][4], rb[UB][4];
+    uint32_t rs[UB][3];
+    v4u ra[UB], rb[UB];
     float rr[UB][4];
+    const ColVec wsv = col_vec(ws, ws16, N), bv = col_vec(bias, b16, N);
     if constexpr (!SLICED) {
 #pragma unroll
         for (int u = 0; u < UB; ++u) {
@@ -133,16 +135,10 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
             const int m = min(m0 + i * 16 + (lane & 15), M - 1);
 #pragma unroll
             for (int c = 0; c < 3; ++c) rs[u][c] = c < P ? load_raw(qs, qs16, (uint32_t)(c * qs_stride + m)) : 0u;
+            // a block's 4 scales (and bias values) with one range-checked 16-byte load
             const int nb = n0 + jn * 16 + (lane >> 4) * 4;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) ra[u][r] = load_raw(ws, ws16, min(nb + r, N - 1));
-            if (bias) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) rb[u][r] = load_raw(bias, b16, min(nb + r, N - 1));
-            } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) rb[u][r] = 0u;
-            }
+            ra[u] = col_load4(wsv, ws16, nb);
+            rb[u] = bias ? col_load4(bv, b16, nb) : (v4u){0u, 0u, 0u, 0u};
             if (p.res) load_residual(p, m, nb, rr[u]);
         }
     }
@@ -191,11 +187,12 @@ __global__ void __launch_bounds__(NW * 64) wsplit_kernel(const int8_t *q, const 
 #pragma unroll
             for (int c = 0; c < 3; ++c)
                 e.s[c] = c < P ? raw_to_f32(rs[u][c], qs16, qs, (uint32_t)(c * qs_stride + m)) : 0.f;
+            col_to_f32(ra[u], ws16, wsv.delta, e.alpha);
+            if (bias) {
+                col_to_f32(rb[u], b16, bv.delta, e.bias);
+            } else {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int n = min(nb + r, N - 1);
-                e.alpha[r] = raw_to_f32(ra[u][r], ws16, ws, (uint32_t)n);
-                e.bias[r] = bias ? raw_to_f32(rb[u][r], b16, bias, (uint32_t)n) : kNoBias;
+                for (int r = 0; r < 4; ++r) e.bias[r] = kNoBias;
             }
             if (p.res) {
 #pragma unroll
