@@ -544,6 +544,8 @@ int kea_lowbit_gemm_plan_launch_with(const kea_gemm_plan *plan, const int8_t *q,
     Params &p = ls.p;
     if (!q || ((uintptr_t)q & 15)) return kea::fail(KEA_EALIGN, "q must be a 16-byte aligned device pointer");
     if (!qs) return kea::fail(KEA_EINVAL, "qs is required");
+    if ((uintptr_t)qs & (p.qs_dtype == KEA_F32 ? 3 : 1))
+        return kea::fail(KEA_EALIGN, "qs must be aligned to its element size");
     if ((y != nullptr) != (p.y != nullptr) || (acc_out != nullptr) != (p.acc != nullptr) ||
         (residual != nullptr) != (p.res != nullptr))
         return kea::fail(KEA_EINVAL, "y, acc_out and residual must be given exactly where the plan has them");

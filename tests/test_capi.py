@@ -166,6 +166,10 @@ def test_gemm_argument_validation_happens_before_any_launch():
     assert call(**base, ldq=1000) == -1  # ldq < k
     assert call(**base, ldq=1032) == -2 and "aligned" in _hip.last_error()  # ldq % 16
     assert call(**dict(base, q=fake + 4)) == -2
+    # scales and bias at less than their element alignment (f32: 4 bytes, f16: 2) are refused, not read misaligned
+    for over in (dict(qs=fake + 2), dict(ws=fake + 2), dict(bias=fake + 2), dict(ws=fake + 1, ws_dtype=1)):
+        assert call(**dict(base, **over)) == -2 and "element size" in _hip.last_error()
+    assert call(**dict(base, ws=fake + 2, ws_dtype=1, split=4)) == -4  # f16 at a 2-byte offset passes this check
     assert call(**base, y_dtype=7) == -1
     assert call(**base, ldy=100) == -1
     assert call(**base, config=999) == -1
@@ -257,6 +261,7 @@ def test_plan_launch_with_refuses_mismatched_buffers_before_any_launch():
         call = L.kea_lowbit_gemm_plan_launch_with
         assert call(None, P(0x1000), P(0x2000), P(0x10000), None, None, None, 0, None) == -1
         assert call(h, P(0x1008), P(0x2000), P(0x10000), None, None, None, 0, None) == -2
+        assert call(h, P(0x1000), P(0x2002), P(0x10000), None, None, None, 0, None) == -2  # f32 qs off its alignment
         assert call(h, None, P(0x2000), P(0x10000), None, None, None, 0, None) == -2
         assert call(h, P(0x1000), None, P(0x10000), None, None, None, 0, None) == -1
         assert call(h, P(0x1000), P(0x2000), None, None, None, None, 0, None) == -1
