@@ -118,7 +118,8 @@ int kea_t2_unlayout_host(const uint32_t *words_host, int64_t n, int64_t k, uint8
  *
  *   q          int8, rows 16-byte aligned: q_dev % 16 == 0, ldq % 16 == 0, part_stride % 16 == 0, ldq >= k.
  *              Bytes at k .. ldq-1 are never read as data (they are masked to zero in-kernel).
- *   qs         per-token scales [parts][m] (stride qs_stride), dtype KEA_F32 or KEA_F16.
+ *   qs         per-token scales [parts][m] (stride qs_stride), dtype KEA_F32 or KEA_F16; qs, wscale and bias are
+ *              aligned to their element size (KEA_EALIGN otherwise).
  *   w          native words (kea_b1_relayout_host / kea_t2_relayout_host), 16-byte aligned.
  *   wscale     alpha, dtype KEA_F32 or KEA_F16.  bias: NULL or [n] of bias_dtype (KEA_F32 / KEA_F16).
  *   y          NULL (no dequantized output) or [m][ldy] of y_dtype (KEA_F32 / KEA_F16 / KEA_BF16), ldy >= n.
