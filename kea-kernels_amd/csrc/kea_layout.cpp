@@ -67,7 +67,11 @@ int kea_b1_relayout_host(const uint8_t *codes, int64_t n, int64_t k, uint32_t *w
                 words[word_index(t, j, l, J)] = word;
             }
     // the bit-plane part: unit (group g, k-step s, lane l) = 4 words; bit p of byte 4d + i of the unit is the
-    // inverted sign of w[128g + 16p + l%16][64s + 16(l/16) + 4d + i] (rows and k past the matrix: 0)
+    // inverted sign of w[128g + 16p + l%16][64s + 16(l/16) + 4d + i] (rows and k past the matrix: 0). A lane's 16 k of
+    // one row are two code bytes; their inverted bits 4d .. 4d+3 spread to bits 0, 8, 16, 24 of word d.
+    static const uint32_t spread4[16] = {0x00000000u, 0x00000001u, 0x00000100u, 0x00000101u, 0x00010000u, 0x00010001u,
+                                         0x00010100u, 0x00010101u, 0x01000000u, 0x01000001u, 0x01000100u, 0x01000101u,
+                                         0x01010000u, 0x01010001u, 0x01010100u, 0x01010101u};
     uint32_t *planes = words + kea::b1_plane_offset(n, k);
     const int64_t NG = cdiv(n, 128), KS = cdiv(k, 64);
     std::memset(planes, 0, sizeof(uint32_t) * kea::b1_plane_words(n, k));
@@ -75,15 +79,16 @@ int kea_b1_relayout_host(const uint8_t *codes, int64_t n, int64_t k, uint32_t *w
         for (int64_t s = 0; s < KS; ++s)
             for (int l = 0; l < 64; ++l) {
                 uint32_t *unit = planes + ((g * KS + s) * 64 + l) * 4;
+                const int64_t k0 = 64 * s + 16 * (l / 16);  // the lane's first k (a multiple of 16)
+                if (k0 >= k) continue;
+                const uint32_t valid = k - k0 >= 16 ? 0xFFFFu : (1u << (k - k0)) - 1u;
                 for (int p = 0; p < 8; ++p) {
                     const int64_t row = 128 * g + 16 * p + (l % 16);
                     if (row >= n) continue;
-                    const uint8_t *src = codes + row * row_bytes;
-                    for (int d = 0; d < 4; ++d)
-                        for (int i = 0; i < 4; ++i) {
-                            const int64_t kk = 64 * s + 16 * (l / 16) + 4 * d + i;
-                            if (kk < k && !((src[kk >> 3] >> (kk & 7)) & 1)) unit[d] |= 1u << (8 * i + p);
-                        }
+                    const uint8_t *src = codes + row * row_bytes + k0 / 8;
+                    const uint32_t bits = src[0] | (k0 / 8 + 1 < row_bytes ? (uint32_t)src[1] << 8 : 0u);
+                    const uint32_t inv = ~bits & valid;
+                    for (int d = 0; d < 4; ++d) unit[d] |= spread4[(inv >> (4 * d)) & 15u] << p;
                 }
             }
     return KEA_OK;
