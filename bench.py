@@ -241,7 +241,9 @@ def probes() -> None:
       100 launches, at the group sizes an in-launch split-K (4) and a whole-grid exchange need;
     * config3_floors: the launch floors of config 3's grid (M = 1024 so the 128x128 tile divides it; N = 4096,
       K = 1024) with 4, 8 and 16 waves per workgroup, next to the GEMM on that grid with tile 11 (128x128, 8 waves)
-      and tile 6 (the same compute waves and 8 producer waves, 16 in all);
+      and tile 6 (the same compute waves and 8 producer waves, 16 in all), and on the other grids a large-M kernel
+      could use (64x128, 64x256, 32x256 and 128x256 tiles at 8 or 16 waves: fewer activation re-reads against fewer
+      or more workgroups);
     * config1_floors: the launch floors of config 1's shape on grids of 16x16 to 128x128 tiles and 1 to 8 waves per
       workgroup (how the cost of moving the operands depends on the grid)."""
     import ctypes
@@ -321,9 +323,10 @@ def probes() -> None:
                                                                 config=GemmConfig(tile, 1)), 100)
         replay_timed(stream, [gemm])
         gemm_us[tile] = round(replay_timed(stream, [gemm], 10) * 1000 / 1000, 3)
-    for waves in (4, 8, 16):
+    for tile, waves in (("128x128", 4), ("128x128", 8), ("128x128", 16), ("64x128", 8), ("64x128", 16),
+                        ("64x256", 8), ("64x256", 16), ("32x256", 8), ("32x256", 16), ("128x256", 16)):
         row = {"probe": "config3_floors", "M": m, "N": n, "K": k}
-        row.update(launch_floors({"q": q, "words": words, "y": y}, stream, "128x128", shape=(m, n, k), waves=waves))
+        row.update(launch_floors({"q": q, "words": words, "y": y}, stream, tile, shape=(m, n, k), waves=waves))
         row["gemm_tile11_us"], row["gemm_tile6_us"] = gemm_us[11], gemm_us[6]
         print(json.dumps(row), flush=True)
 
