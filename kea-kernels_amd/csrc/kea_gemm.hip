@@ -415,7 +415,8 @@ int gemm_prepare(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, i
 
     if (tile > kNumTiles) {
         const WsplitTile &wt = kWsplitTiles[tile - kNumTiles - 1];
-        if (!kea::fits_dispatch(cdivl(n, wt.nt * 16), wt.nw * 64))
+        // the wave-split kernels address the per-column vectors with 32-bit byte offsets
+        if (!kea::fits_dispatch(cdivl(n, wt.nt * 16), wt.nw * 64) || n >= (int64_t(1) << 30))
             return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N or M");
         if (gq) {
             const int gs = kea::wsplit_group_steps(wbits, parts, k, wt, gq);

@@ -37,13 +37,15 @@ __device__ __forceinline__ ColVec col_vec(const void *v, bool f16, int n) {
     const uintptr_t a = (uintptr_t)v & ~(uintptr_t)3;
     const int d = (int)((uintptr_t)v & 3);
     // data format 32 in the descriptor's last word: the raw (untyped) buffer form of gfx9
-    return ColVec{__builtin_amdgcn_make_buffer_rsrc((void *)a, (short)0, (d + n * (f16 ? 2 : 4) + 3) & ~3, 0x00020000),
-                  d};
+    // 32-bit byte extent and offsets: the host runs these kernels with n < 2^30
+    const uint32_t extent = ((uint32_t)d + (uint32_t)n * (f16 ? 2u : 4u) + 3u) & ~3u;
+    return ColVec{__builtin_amdgcn_make_buffer_rsrc((void *)a, (short)0, (int)extent, 0x00020000), d};
 }
 // The 16 bytes from the 4-byte word holding element nb (nb % 4 == 0): f32 elements nb .. nb+3 are its words 0..3; f16
 // elements nb .. nb+3 start at bit 8 * delta of word 0 (delta 0 or 2: f16 vectors are 2-byte aligned).
 __device__ __forceinline__ v4u col_load4(const ColVec &c, bool f16, int nb) {
-    return __builtin_amdgcn_raw_buffer_load_b128(c.rsrc, (c.delta + nb * (f16 ? 2 : 4)) & ~3, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(c.rsrc, (int)(((uint32_t)c.delta + (uint32_t)nb * (f16 ? 2u : 4u)) & ~3u),
+                                                 0, 0);
 }
 __device__ __forceinline__ void col_to_f32(v4u w, bool f16, int delta, float (&out)[4]) {
     if (f16) {  // wave-uniform
