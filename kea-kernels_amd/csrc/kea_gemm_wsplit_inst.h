@@ -8,8 +8,9 @@
 // One workgroup owns a BM x BN output tile (BM = 16 * RM rows, BN = 16 * NT columns) and a range of NW * S k-steps of
 // 64; wave w of its NW waves takes the S consecutive k-steps [w * S, (w + 1) * S) of that range. Each wave:
 //   * issues every load it needs at once, before any wait: its activation fragments (one 16-byte load per lane per
-//     k-step, the MFMA operand layout of 16 rows x 64 k), its weights and the epilogue's scales (raw 32-bit words
-//     whose conversion waits until the epilogue). Weights are native words (one 32-bit word per lane per n-tile and
+//     k-step, the MFMA operand layout of 16 rows x 64 k), its weights and the epilogue's scales (raw words whose
+//     conversion waits until the epilogue: a lane's 4 per-channel scales, and bias values, with one range-checked
+//     16-byte buffer load each). Weights are native words (one 32-bit word per lane per n-tile and
 //     word: 2 k-steps at 1 bit, 1 at 2 bits; four consecutive words with one 128-bit load) or, for the 1-bit
 //     instances that kea::wsplit_planes selects, the bit-plane part of the layout (one 16-byte unit per lane per
 //     k-step holds the k-step's weights of all 8 n-tiles of a 128-row group);
