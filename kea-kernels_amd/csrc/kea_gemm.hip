@@ -379,6 +379,8 @@ int gemm_prepare(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, i
         return kea::fail(KEA_EALIGN, "qs, wscale and bias must be aligned to their element size");
     if ((int64_t)(parts - 1) * part_stride + m * ldq > (int64_t)INT32_MAX)
         return kea::fail(KEA_EINVAL, "q spans more than 2 GiB: split the call along M");
+    // the epilogues address the per-column vectors (scales, bias) with 32-bit byte offsets
+    if (n >= (int64_t(1) << 30)) return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N");
 
     Params &p = ls->p;
     p.q = q; p.part_stride = part_stride; p.ldq = ldq;
@@ -397,8 +399,6 @@ int gemm_prepare(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, i
     const int yv = glu ? 2 : 4;  // elements per vector store
     p.y_vec = y && (ldy % yv == 0) && ((uintptr_t)y % (yv * esz) == 0);
     p.acc_vec = acc_out && (acc_ld % 4 == 0) && ((uintptr_t)acc_out % 16 == 0);
-    p.ws_vec = ((uintptr_t)wscale % (ws_dtype == KEA_F16 ? 8 : 16)) == 0;
-    p.bias_vec = bias && ((uintptr_t)bias % (bias_dtype == KEA_F16 ? 8 : 16)) == 0;
     ls->splits = s;
     ls->parts = parts;
     if (s > 1) {
@@ -415,8 +415,7 @@ int gemm_prepare(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, i
 
     if (tile > kNumTiles) {
         const WsplitTile &wt = kWsplitTiles[tile - kNumTiles - 1];
-        // the wave-split kernels address the per-column vectors with 32-bit byte offsets
-        if (!kea::fits_dispatch(cdivl(n, wt.nt * 16), wt.nw * 64) || n >= (int64_t(1) << 30))
+        if (!kea::fits_dispatch(cdivl(n, wt.nt * 16), wt.nw * 64))
             return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N or M");
         if (gq) {
             const int gs = kea::wsplit_group_steps(wbits, parts, k, wt, gq);
@@ -683,6 +682,8 @@ int kea_lowbit_gemm_slices(int wbits, const int8_t *q, int64_t part_stride, int6
     if (((uintptr_t)w & 15) || ((uintptr_t)slices & 15)) return kea::fail(KEA_EALIGN, "w and slices must be 16-byte aligned");
     if ((int64_t)(parts - 1) * part_stride + m * ldq > (int64_t)INT32_MAX)
         return kea::fail(KEA_EINVAL, "q spans more than 2 GiB: split the call along M");
+    // the epilogues address the per-column vectors (scales, bias) with 32-bit byte offsets
+    if (n >= (int64_t(1) << 30)) return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N");
     Params p = {};
     p.q = q; p.part_stride = part_stride; p.ldq = ldq;
     p.w = w;
@@ -741,6 +742,11 @@ int kea_lowbit_slices_finish(const int32_t *slices, int split, int parts, int64_
     if (!slices || !qs || !wscale) return kea::fail(KEA_EINVAL, "slices, qs and wscale are required");
     if (!y && !acc_out) return kea::fail(KEA_EINVAL, "nothing to write: y and acc_out are both NULL");
     if ((uintptr_t)slices & 15) return kea::fail(KEA_EALIGN, "slices must be 16-byte aligned");
+    const auto misaligned = [](const void *v, int dtype) { return ((uintptr_t)v & (dtype == KEA_F32 ? 3 : 1)) != 0; };
+    if (misaligned(qs, qs_dtype) || misaligned(wscale, ws_dtype) || (bias && misaligned(bias, bias_dtype)))
+        return kea::fail(KEA_EALIGN, "qs, wscale and bias must be aligned to their element size");
+    // the epilogue addresses the per-column vectors with 32-bit byte offsets
+    if (n >= (int64_t(1) << 30)) return kea::fail(KEA_EINVAL, "too large for one launch: split the call along N");
     Params p = {};
     p.qs = qs; p.qs_stride = qs_stride; p.qs_dtype = qs_dtype;
     p.ws = wscale; p.ws_dtype = ws_dtype;
@@ -754,8 +760,6 @@ int kea_lowbit_slices_finish(const int32_t *slices, int split, int parts, int64_
     const int esz = (y_dtype == KEA_F32) ? 4 : 2;
     p.y_vec = y && (ldy % 4 == 0) && ((uintptr_t)y % (4 * esz) == 0);
     p.acc_vec = acc_out && (acc_ld % 4 == 0) && ((uintptr_t)acc_out % 16 == 0);
-    p.ws_vec = ((uintptr_t)wscale % (ws_dtype == KEA_F16 ? 8 : 16)) == 0;
-    p.bias_vec = bias && ((uintptr_t)bias % (bias_dtype == KEA_F16 ? 8 : 16)) == 0;
     const long long work = m * cdivl(n, 4);
     if (!kea::fits_dispatch(cdivl(work, 256), 256))
         return kea::fail(KEA_EINVAL, "too large for one launch: split the call along M");

@@ -40,7 +40,6 @@ struct Params {
     float res_factor;
     int groups;     // per-group scales: G = ceil(K / ws_group) groups, alpha [N][G]
     int gp_shift;   // log2 of the padded group count held in LDS (a power of two >= the groups the stages span)
-    int ws_vec, bias_vec;  // 1: per-channel scales / bias allow aligned 4-element vector loads
     int steps_per_slice;   // wave-split kernel: k-steps of 64 per workgroup (one K slice)
 };
 
@@ -165,33 +164,68 @@ __device__ __forceinline__ void load_row_scales(const Params &p, int m, EpiOpera
     for (int c = 0; c < 3; ++c) e.s[c] = c < P ? load_scalar(p.qs, p.qs_dtype, c * p.qs_stride + mm) : 0.f;
 }
 
-// Four consecutive values of a per-column vector (f32 or f16) at nb..nb+3: one vector load when they are all in range
-// and the vector is aligned, else clamped scalar loads (the clamped values are never stored).
-__device__ __forceinline__ void load_col4(const void *v, int dtype, bool vec, int nb, int N, float *out) {
-    if (vec && nb + 3 < N) {
-        if (dtype == KEA_F16) {
-            const uint2 h = *(const uint2 *)((const _Float16 *)v + nb);
-            const _Float16 *hv = (const _Float16 *)&h;
-            out[0] = (float)hv[0]; out[1] = (float)hv[1]; out[2] = (float)hv[2]; out[3] = (float)hv[3];
-        } else {
-            const float4 f = *(const float4 *)((const float *)v + nb);
-            out[0] = f.x; out[1] = f.y; out[2] = f.z; out[3] = f.w;
-        }
+// A per-column vector of f32 or f16 values (per-channel scales, bias) read through a range-checked buffer
+// descriptor: its base is the vector's start aligned down to 4 bytes (`delta` bytes before it) and its extent ends at
+// the 4-byte word holding the last element, so a load past the vector's end returns zeros instead of touching memory
+// (those values belong to columns past N, which are never stored) and no per-element clamp is needed.
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+struct ColVec {
+    __amdgpu_buffer_rsrc_t rsrc;
+    int delta;
+};
+__device__ __forceinline__ ColVec col_vec(const void *v, bool f16, int n) {
+    const uintptr_t a = (uintptr_t)v & ~(uintptr_t)3;
+    const int d = (int)((uintptr_t)v & 3);
+    // data format 32 in the descriptor's last word: the raw (untyped) buffer form of gfx9
+    // 32-bit byte extent and offsets: the host launches the GEMM kernels with n < 2^30
+    const uint32_t extent = ((uint32_t)d + (uint32_t)n * (f16 ? 2u : 4u) + 3u) & ~3u;
+    return ColVec{__builtin_amdgcn_make_buffer_rsrc((void *)a, (short)0, (int)extent, 0x00020000), d};
+}
+// The 16 bytes from the 4-byte word holding element nb (nb % 4 == 0): f32 elements nb .. nb+3 are its words 0..3; f16
+// elements nb .. nb+3 start at bit 8 * delta of word 0 (delta 0 or 2: f16 vectors are 2-byte aligned).
+__device__ __forceinline__ v4u col_load4(const ColVec &c, bool f16, int nb) {
+    return __builtin_amdgcn_raw_buffer_load_b128(c.rsrc, (int)(((uint32_t)c.delta + (uint32_t)nb * (f16 ? 2u : 4u)) & ~3u),
+                                                 0, 0);
+}
+__device__ __forceinline__ void col_to_f32(v4u w, bool f16, int delta, float (&out)[4]) {
+    if (f16) {  // wave-uniform
+        const uint32_t sh = (uint32_t)delta * 8u;
+        const uint32_t h01 = __builtin_amdgcn_alignbit(w.y, w.x, sh), h23 = __builtin_amdgcn_alignbit(w.z, w.y, sh);
+        out[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)h01);
+        out[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(h01 >> 16));
+        out[2] = (float)__builtin_bit_cast(_Float16, (uint16_t)h23);
+        out[3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(h23 >> 16));
     } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) out[r] = load_scalar(v, dtype, nb + r < N ? nb + r : N - 1);
+        // the whole vector is cast: hipcc's __builtin_bit_cast of one component access (w.y, ...) reads component 0
+        const v4f f = __builtin_bit_cast(v4f, w);
+        out[0] = f.x;
+        out[1] = f.y;
+        out[2] = f.z;
+        out[3] = f.w;
     }
+}
+
+// Four consecutive values nb..nb+3 (nb % 4 == 0) of a per-column vector of N values (f32 or f16): one range-checked
+// 16-byte load (values past N read 0; their columns are never stored).
+__device__ __forceinline__ void load_col4(const void *v, int dtype, int nb, int N, float *out) {
+    const bool f16 = dtype == KEA_F16;
+    const ColVec c = col_vec(v, f16, N);
+    float f[4];
+    col_to_f32(col_load4(c, f16, nb), f16, c.delta, f);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out[r] = f[r];
 }
 
 __device__ __forceinline__ void load_col_scales(const Params &p, int nb, EpiOperands &e, bool with_alpha = true) {
     if (with_alpha) {
-        load_col4(p.ws, p.ws_dtype, p.ws_vec, nb, p.N, e.alpha);
+        load_col4(p.ws, p.ws_dtype, nb, p.N, e.alpha);
     } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) e.alpha[r] = 0.f;
     }
     if (p.bias) {
-        load_col4(p.bias, p.bias_dtype, p.bias_vec, nb, p.N, e.bias);
+        load_col4(p.bias, p.bias_dtype, nb, p.N, e.bias);
     } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) e.bias[r] = kNoBias;

@@ -23,48 +23,6 @@ __device__ __forceinline__ float raw_to_f32(uint32_t raw, bool f16, const void *
     return f16 ? h : __builtin_bit_cast(float, raw);
 }
 
-// A per-column vector of f32 or f16 values (per-channel scales, bias) read through a range-checked buffer
-// descriptor: its base is the vector's start aligned down to 4 bytes (`delta` bytes before it) and its extent ends at
-// the 4-byte word holding the last element, so a load past the vector's end returns zeros instead of touching memory
-// (those values belong to columns past N, which are never stored) and no per-element clamp is needed.
-typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-struct ColVec {
-    __amdgpu_buffer_rsrc_t rsrc;
-    int delta;
-};
-__device__ __forceinline__ ColVec col_vec(const void *v, bool f16, int n) {
-    const uintptr_t a = (uintptr_t)v & ~(uintptr_t)3;
-    const int d = (int)((uintptr_t)v & 3);
-    // data format 32 in the descriptor's last word: the raw (untyped) buffer form of gfx9
-    // 32-bit byte extent and offsets: the host runs these kernels with n < 2^30
-    const uint32_t extent = ((uint32_t)d + (uint32_t)n * (f16 ? 2u : 4u) + 3u) & ~3u;
-    return ColVec{__builtin_amdgcn_make_buffer_rsrc((void *)a, (short)0, (int)extent, 0x00020000), d};
-}
-// The 16 bytes from the 4-byte word holding element nb (nb % 4 == 0): f32 elements nb .. nb+3 are its words 0..3; f16
-// elements nb .. nb+3 start at bit 8 * delta of word 0 (delta 0 or 2: f16 vectors are 2-byte aligned).
-__device__ __forceinline__ v4u col_load4(const ColVec &c, bool f16, int nb) {
-    return __builtin_amdgcn_raw_buffer_load_b128(c.rsrc, (int)(((uint32_t)c.delta + (uint32_t)nb * (f16 ? 2u : 4u)) & ~3u),
-                                                 0, 0);
-}
-__device__ __forceinline__ void col_to_f32(v4u w, bool f16, int delta, float (&out)[4]) {
-    if (f16) {  // wave-uniform
-        const uint32_t sh = (uint32_t)delta * 8u;
-        const uint32_t h01 = __builtin_amdgcn_alignbit(w.y, w.x, sh), h23 = __builtin_amdgcn_alignbit(w.z, w.y, sh);
-        out[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)h01);
-        out[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(h01 >> 16));
-        out[2] = (float)__builtin_bit_cast(_Float16, (uint16_t)h23);
-        out[3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(h23 >> 16));
-    } else {
-        // the whole vector is cast: hipcc's __builtin_bit_cast of one component access (w.y, ...) reads component 0
-        const v4f f = __builtin_bit_cast(v4f, w);
-        out[0] = f.x;
-        out[1] = f.y;
-        out[2] = f.z;
-        out[3] = f.w;
-    }
-}
-
 // The wave's weight words: WPW native words per lane for each of the NT n-tiles from the tile at column n0, starting
 // at word j0 (J words per lane per n-tile). RAGGED = false: complete quads of words (or one word per wave), loaded
 // with 64- or 128-bit vector loads; otherwise general per-word addressing (a short last quad has lane stride < 4,
