@@ -187,6 +187,12 @@ def test_grids_past_one_dispatch_are_refused_before_any_launch():
     rc = L.kea_lowbit_gemm(1, fake, 0, 1024, 1, fake, 0, 0, fake, big, 1024, fake, 0, 0, None, 0, fake, 1, big,
                            None, 0, 128, 0, 1, 0, None, 0, None)
     assert rc == -1 and "too large for one launch" in _hip.last_error()
+    # N = 2^30: a grid that fits one dispatch, refused because the epilogues address per-column vectors with 32-bit
+    # byte offsets (ldy = N; fake pointers, nothing launched)
+    n30 = 2**30
+    rc = L.kea_lowbit_gemm(1, fake, 0, 1024, 1, fake, 0, 0, fake, n30, 1024, fake, 0, 0, None, 0, fake, 1, n30,
+                           None, 0, 128, 0, 1, 0, None, 0, None)
+    assert rc == -1 and "too large for one launch" in _hip.last_error()
     # the same N with M = 0 is an empty call, not an error
     assert L.kea_lowbit_gemm(1, fake, 0, 1024, 1, fake, 0, 0, fake, big, 1024, fake, 0, 0, None, 0, fake, 1, big,
                              None, 0, 0, 0, 1, 0, None, 0, None) == 0
