@@ -242,6 +242,26 @@ int kea_lowbit_gemm_plan_launch_with(const kea_gemm_plan *plan, const int8_t *q_
                                      int64_t workspace_bytes, void *stream);
 int64_t kea_lowbit_gemm_plan_workspace(const kea_gemm_plan *plan);
 
+/* One operator call in one C call: kea_quantize of x's rows into int8 parts, then a plan's GEMM on those parts, both
+ * enqueued on `stream`. kea_lowbit_project_plan takes a GEMM plan made on a quantizer layout (y only, no acc_out or
+ * residual; part_stride = m * ldq, qs_stride = m; the plan's parts, m, k, ldq and qs dtype are the quantizer's) and
+ * kea_quantize's row mapping and LayerNorm / SiLU arguments; it copies what it needs, so the GEMM plan may be freed
+ * afterwards, and returns NULL with kea_last_error() set on any argument kea_quantize or the launch would refuse.
+ * The norm pointers are recorded and read on every launch. kea_lowbit_project_launch takes x (the plan's dtype and
+ * row mapping), y (the plan's dtype and row stride) and a 16-byte aligned device workspace of at least
+ * kea_lowbit_project_workspace bytes, which holds the int8 parts from its first byte, then their scales and any
+ * split-K slices (calls that share a workspace must be ordered on one stream). Results are the bits of kea_quantize
+ * followed by kea_lowbit_gemm. Replaces the reference's two per-call launches of an operator call, b1_quantize and
+ * b1_dot (kk/binary/layer.py:154-165 and :182-209). */
+typedef struct kea_project_plan kea_project_plan;
+kea_project_plan *kea_lowbit_project_plan(const kea_gemm_plan *plan, int x_dtype, int64_t xb, int64_t xt,
+                                          int64_t xk, int64_t t, const float *norm_w_dev, const float *norm_b_dev,
+                                          float eps, int input_silu);
+int64_t kea_lowbit_project_workspace(const kea_project_plan *pp);
+int kea_lowbit_project_launch(const kea_project_plan *pp, const void *x_dev, void *y_dev, void *workspace_dev,
+                              int64_t workspace_bytes, void *stream);
+void kea_lowbit_project_plan_free(kea_project_plan *pp);
+
 /* kea_lowbit_gemm without the workspace arguments, for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). It has no counterpart in the reference. The
  * split-K slices live in a library-owned device array of KEA_NOALLOC_SCRATCH_BYTES per GPU (a file-scope __device__

@@ -507,6 +507,32 @@ struct kea_gemm_plan {
     LaunchSpec spec;
 };
 
+// A quantizer launch followed by a plan's GEMM on the parts it wrote: the quantizer's arguments and the byte offsets
+// of the scales and the split-K slices in the caller's workspace (the int8 parts start at its first byte).
+struct kea_project_plan {
+    LaunchSpec spec;
+    int x_dtype, silu;
+    int64_t xb, xt, xk, t;
+    const float *norm_w, *norm_b;
+    float eps;
+    int64_t qs_off, slices_off, need;
+};
+
+namespace {
+
+// Points a plan's copy at new outputs; the vector-store flags follow their alignment (the row strides are the plan's).
+void bind_outputs(Params &p, void *y, int32_t *acc_out) {
+    p.y = y;
+    p.acc = acc_out;
+    const int esz = p.y_dtype == KEA_F32 ? 4 : 2, yv = (p.flags & KEA_FLAG_GLU) ? 2 : 4;
+    p.y_vec = y && (p.ldy % yv == 0) && ((uintptr_t)y % (yv * esz) == 0);
+    p.acc_vec = acc_out && (p.acc_ld % 4 == 0) && ((uintptr_t)acc_out % 16 == 0);
+}
+
+int64_t round16(int64_t v) { return (v + 15) & ~(int64_t)15; }
+
+}  // namespace
+
 extern "C" {
 
 kea_gemm_plan *kea_lowbit_gemm_plan(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts,
@@ -551,13 +577,8 @@ int kea_lowbit_gemm_plan_launch_with(const kea_gemm_plan *plan, const int8_t *q,
         return kea::fail(KEA_EINVAL, "y, acc_out and residual must be given exactly where the plan has them");
     p.q = q;
     p.qs = qs;
-    p.y = y;
-    p.acc = acc_out;
     p.res = residual;
-    // the vector-store flags follow the new buffers' alignment (the row strides are the plan's)
-    const int esz = p.y_dtype == KEA_F32 ? 4 : 2, yv = (p.flags & KEA_FLAG_GLU) ? 2 : 4;
-    p.y_vec = y && (p.ldy % yv == 0) && ((uintptr_t)y % (yv * esz) == 0);
-    p.acc_vec = acc_out && (p.acc_ld % 4 == 0) && ((uintptr_t)acc_out % 16 == 0);
+    bind_outputs(p, y, acc_out);
     if (ls.splits > 1) {
         const int64_t need = (int64_t)ls.splits * ls.parts * p.M * p.N * 4;
         if (!workspace || workspace_bytes < need)
@@ -574,6 +595,78 @@ int64_t kea_lowbit_gemm_plan_workspace(const kea_gemm_plan *plan) {
 }
 
 void kea_lowbit_gemm_plan_free(kea_gemm_plan *plan) { delete plan; }
+
+kea_project_plan *kea_lowbit_project_plan(const kea_gemm_plan *plan, int x_dtype, int64_t xb, int64_t xt, int64_t xk,
+                                          int64_t t, const float *norm_w, const float *norm_b, float eps,
+                                          int input_silu) {
+    if (!plan) {
+        kea::fail(KEA_EINVAL, "plan is NULL");
+        return nullptr;
+    }
+    const LaunchSpec &ls = plan->spec;
+    const Params &p = ls.p;
+    if (ls.empty) {
+        kea::fail(KEA_EINVAL, "a projection plan needs at least one row");
+        return nullptr;
+    }
+    if (!p.y || p.acc || p.res) {
+        kea::fail(KEA_EINVAL, "a projection plan's GEMM writes y only (no acc_out, no residual)");
+        return nullptr;
+    }
+    if (p.part_stride != (long long)p.M * p.ldq || p.qs_stride != p.M) {
+        kea::fail(KEA_EINVAL, "a projection plan's GEMM reads the quantizer's layout: part_stride = m * ldq and "
+                              "qs_stride = m");
+        return nullptr;
+    }
+    if (kea::quantize_check(x_dtype, t, p.M, p.K, ls.parts, p.ldq, p.qs_dtype, norm_w, norm_b) != KEA_OK)
+        return nullptr;
+    kea_project_plan *pp = new (std::nothrow) kea_project_plan;
+    if (!pp) {
+        kea::fail(KEA_EINVAL, "out of host memory for a plan");
+        return nullptr;
+    }
+    pp->spec = ls;
+    pp->x_dtype = x_dtype;
+    pp->silu = input_silu;
+    pp->xb = xb;
+    pp->xt = xt;
+    pp->xk = xk;
+    pp->t = t;
+    pp->norm_w = norm_w;
+    pp->norm_b = norm_b;
+    pp->eps = eps;
+    const int64_t qbytes = (int64_t)ls.parts * p.M * p.ldq;
+    const int qs_esz = p.qs_dtype == KEA_F32 ? 4 : 2;
+    pp->qs_off = round16(qbytes);
+    pp->slices_off = round16(pp->qs_off + (int64_t)ls.parts * p.M * qs_esz);
+    pp->need = ls.splits > 1 ? pp->slices_off + (int64_t)ls.splits * ls.parts * p.M * p.N * 4 : pp->slices_off;
+    return pp;
+}
+
+int64_t kea_lowbit_project_workspace(const kea_project_plan *pp) { return pp ? pp->need : 0; }
+
+int kea_lowbit_project_launch(const kea_project_plan *pp, const void *x, void *y, void *workspace,
+                              int64_t workspace_bytes, void *stream) {
+    if (!pp) return kea::fail(KEA_EINVAL, "plan is NULL");
+    if (!x || !y) return kea::fail(KEA_EINVAL, "x and y are required");
+    if (!workspace || workspace_bytes < pp->need)
+        return kea::fail(KEA_ESPACE, "projection workspace too small: need " + std::to_string(pp->need) + " bytes");
+    if ((uintptr_t)workspace & 15) return kea::fail(KEA_EALIGN, "workspace must be 16-byte aligned");
+    LaunchSpec ls = pp->spec;  // a copy: the plan stays read-only, so concurrent launches of it are safe
+    Params &p = ls.p;
+    uint8_t *ws = (uint8_t *)workspace;
+    int rc = kea::quantize_enqueue(x, pp->x_dtype, pp->xb, pp->xt, pp->xk, pp->t, p.M, p.K, ls.parts, pp->norm_w,
+                                   pp->norm_b, pp->eps, pp->silu, (int8_t *)ws, p.ldq, ws + pp->qs_off, p.qs_dtype,
+                                   stream);
+    if (rc != KEA_OK) return rc;
+    p.q = (const int8_t *)ws;
+    p.qs = ws + pp->qs_off;
+    bind_outputs(p, y, nullptr);
+    if (ls.splits > 1) p.slices = (int32_t *)(ws + pp->slices_off);
+    return gemm_launch(ls, (hipStream_t)stream);
+}
+
+void kea_lowbit_project_plan_free(kea_project_plan *pp) { delete pp; }
 
 int kea_lowbit_gemm(int wbits, const int8_t *q, int64_t part_stride, int64_t ldq, int parts, const void *qs,
                     int qs_dtype, int64_t qs_stride, const uint32_t *w, int64_t n, int64_t k, const void *wscale,

@@ -22,4 +22,12 @@ inline bool fits_dispatch(long long blocks, long long threads) {
     return blocks >= 0 && blocks * threads <= 0xFFFFFFFFLL;
 }
 
+// kea_quantize in two steps: the checks that depend on no pointer (KEA_OK or the error kea_quantize returns), and
+// the launch for arguments that passed them with m >= 1 and x, q, qs present (kea_quantize.hip).
+int quantize_check(int x_dtype, int64_t t, int64_t m, int64_t k, int parts, int64_t ldq, int qs_dtype,
+                   const float *norm_w, const float *norm_b);
+int quantize_enqueue(const void *x, int x_dtype, int64_t xb, int64_t xt, int64_t xk, int64_t t, int64_t m, int64_t k,
+                     int parts, const float *norm_w, const float *norm_b, float eps, int input_silu, int8_t *q,
+                     int64_t ldq, void *qs, int qs_dtype, void *stream);
+
 }  // namespace kea

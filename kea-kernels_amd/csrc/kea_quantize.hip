@@ -486,18 +486,26 @@ __global__ void __launch_bounds__(256) row_epilogue_kernel(RowParams rp) {
 
 }  // namespace
 
-extern "C" int kea_quantize(const void *x, int x_dtype, int64_t xb, int64_t xt, int64_t xk, int64_t t, int64_t m,
-                            int64_t k, int parts, const float *norm_w, const float *norm_b, float eps,
-                            int input_silu, int8_t *q, int64_t ldq, void *qs, int qs_dtype, void *stream) {
-    if (parts < 1 || parts > 3) return kea::fail(KEA_EINVAL, "parts must be 1, 2 or 3");
-    if (m < 0 || k < 1 || m > INT32_MAX || k > 8192) return kea::fail(KEA_EINVAL, "bad sizes (k must be 1..8192)");
-    if (t < 1) return kea::fail(KEA_EINVAL, "t must be >= 1");
-    if (ldq < k) return kea::fail(KEA_EINVAL, "ldq < k");
-    if (x_dtype != KEA_F32 && x_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "x dtype must be f32 or f16");
-    if (qs_dtype != KEA_F32 && qs_dtype != KEA_F16) return kea::fail(KEA_EINVAL, "qs dtype must be f32 or f16");
-    if ((norm_w == nullptr) != (norm_b == nullptr)) return kea::fail(KEA_EINVAL, "norm weight and bias go together");
-    if (m == 0) return KEA_OK;
-    if (!x || !q || !qs) return kea::fail(KEA_EINVAL, "x, q and qs are required");
+namespace kea {
+
+int quantize_check(int x_dtype, int64_t t, int64_t m, int64_t k, int parts, int64_t ldq, int qs_dtype,
+                   const float *norm_w, const float *norm_b) {
+    if (parts < 1 || parts > 3) return fail(KEA_EINVAL, "parts must be 1, 2 or 3");
+    if (m < 0 || k < 1 || m > INT32_MAX || k > 8192) return fail(KEA_EINVAL, "bad sizes (k must be 1..8192)");
+    if (t < 1) return fail(KEA_EINVAL, "t must be >= 1");
+    if (ldq < k) return fail(KEA_EINVAL, "ldq < k");
+    if (x_dtype != KEA_F32 && x_dtype != KEA_F16) return fail(KEA_EINVAL, "x dtype must be f32 or f16");
+    if (qs_dtype != KEA_F32 && qs_dtype != KEA_F16) return fail(KEA_EINVAL, "qs dtype must be f32 or f16");
+    if ((norm_w == nullptr) != (norm_b == nullptr)) return fail(KEA_EINVAL, "norm weight and bias go together");
+    const int wpr = k > 256 ? 4 : 1;
+    if (!fits_dispatch((m + 4 / wpr - 1) / (4 / wpr), 256))
+        return fail(KEA_EINVAL, "too large for one launch: split the call along M");
+    return KEA_OK;
+}
+
+int quantize_enqueue(const void *x, int x_dtype, int64_t xb, int64_t xt, int64_t xk, int64_t t, int64_t m, int64_t k,
+                     int parts, const float *norm_w, const float *norm_b, float eps, int input_silu, int8_t *q,
+                     int64_t ldq, void *qs, int qs_dtype, void *stream) {
     hipStream_t st = (hipStream_t)stream;
     const int esz = x_dtype == KEA_F16 ? 2 : 4;
     const int wpr = k > 256 ? 4 : 1;               // waves per row (the oracle restates this rule)
@@ -505,7 +513,6 @@ extern "C" int kea_quantize(const void *x, int x_dtype, int64_t xb, int64_t xt, 
     const bool vec = xk == 1 && k % 4 == 0 && ldq % 4 == 0 && xb % 4 == 0 && xt % 4 == 0 &&
                      ((uintptr_t)x % (4 * esz)) == 0 && ((uintptr_t)q % 4) == 0 &&
                      (((uintptr_t)norm_w | (uintptr_t)norm_b) % 16) == 0;
-    if (!kea::fits_dispatch((m + 4 / wpr - 1) / (4 / wpr), 256)) return kea::fail(KEA_EINVAL, "too large for one launch: split the call along M");
     const dim3 grid((unsigned)((m + 4 / wpr - 1) / (4 / wpr))), block(256);
 #define KEA_Q(V, W)                                                                                                \
     do {                                                                                                           \
@@ -526,8 +533,21 @@ extern "C" int kea_quantize(const void *x, int x_dtype, int64_t xb, int64_t xt, 
     }
 #undef KEA_Q
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return kea::fail((int)e, std::string("quantize launch failed: ") + hipGetErrorString(e));
+    if (e != hipSuccess) return fail((int)e, std::string("quantize launch failed: ") + hipGetErrorString(e));
     return KEA_OK;
+}
+
+}  // namespace kea
+
+extern "C" int kea_quantize(const void *x, int x_dtype, int64_t xb, int64_t xt, int64_t xk, int64_t t, int64_t m,
+                            int64_t k, int parts, const float *norm_w, const float *norm_b, float eps,
+                            int input_silu, int8_t *q, int64_t ldq, void *qs, int qs_dtype, void *stream) {
+    const int rc = kea::quantize_check(x_dtype, t, m, k, parts, ldq, qs_dtype, norm_w, norm_b);
+    if (rc != KEA_OK) return rc;
+    if (m == 0) return KEA_OK;
+    if (!x || !q || !qs) return kea::fail(KEA_EINVAL, "x, q and qs are required");
+    return kea::quantize_enqueue(x, x_dtype, xb, xt, xk, t, m, k, parts, norm_w, norm_b, eps, input_silu, q, ldq, qs,
+                                 qs_dtype, stream);
 }
 
 extern "C" int kea_norm_quantize(const float *x, int64_t ldx, int64_t m, int64_t k, const float *norm0_w,

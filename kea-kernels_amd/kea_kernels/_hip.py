@@ -42,6 +42,10 @@ SIGNATURES = {
     "kea_lowbit_gemm_plan_launch_with": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
     "kea_lowbit_gemm_plan_workspace": (_i64, [_vp]),
     "kea_lowbit_gemm_plan_free": (None, [_vp]),
+    "kea_lowbit_project_plan": (_vp, [_vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp, _f32, _i32]),
+    "kea_lowbit_project_workspace": (_i64, [_vp]),
+    "kea_lowbit_project_launch": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp]),
+    "kea_lowbit_project_plan_free": (None, [_vp]),
     "kea_lowbit_gemm_noalloc": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _vp, _i32,
                                        _i64, _vp, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _i32, _i32, _i32, _vp]),
     "kea_lowbit_gemm_residual": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _i32, _i64, _vp, _i64, _i64, _vp, _i32,

@@ -6,8 +6,9 @@ dtype of `y`, fp16 per-token scales via the dtype of `qs`, raw int32 accumulator
 call, both on the current stream and both graph-capturable (no allocation inside the library, no host sync):
   1. kea_quantize: x (any strides) -> q int8 [P, M, ldq] + qs [P, M] (LayerNorm / input SiLU fused for `project`);
   2. kea_lowbit_gemm: the 1-bit x int8 GEMM with the fused epilogue.
-The layer resolves each call layout once (lowbit.Launches: a GEMM plan per layout, the buffers bound per call), so a
-repeated call pays the two launches and two allocations, not the argument checks.
+The layer resolves each call layout once (lowbit.Launches: a projection plan per layout, the buffers bound per call),
+so a repeated linear / conv call with the same input shape, strides, dtype and output dtype pays one C call that
+enqueues both launches and two allocations (output and workspace), not the argument checks.
 There is no slow fallback layout: every shape runs the MFMA kernel (the native layout pads N to 16 and K to 128).
 """
 from __future__ import annotations
@@ -86,35 +87,56 @@ class Int8MmaLayer:
 
     def linear(self, x: Tensor, *, out_dtype: torch.dtype = torch.float32) -> Tensor:
         """[..., K] -> [..., N] (FP32 unless out_dtype says otherwise)."""
+        launches, key = self.launches, _call_key(x, out_dtype, "linear")
+        hit = launches.recall(key)
+        if hit is not None and not (x.requires_grad and torch.is_grad_enabled()):
+            # a layout checked and resolved before: everything checked derives from the key
+            y = torch.empty(hit[1], device=self.device, dtype=out_dtype)
+            launches.launch(hit[0], x, y)
+            return y
         self._check(x, "linear")
         lead = tuple(x.shape[:-1])
         m = math.prod(lead)
-        y = torch.empty(m, self.out_features, device=self.device, dtype=out_dtype)
+        y = torch.empty(*lead, self.out_features, device=self.device, dtype=out_dtype)
         if m:
+            xr = x
             if x.dim() == 1:
                 rows = (0, 0, x.stride(0), 1)
             elif x.dim() == 2:
                 rows = (0, x.stride(0), x.stride(1), m)
             else:
-                x3 = x.reshape(-1, x.shape[-2], x.shape[-1])
-                x = x3
-                rows = (x3.stride(0), x3.stride(1), x3.stride(2), x3.shape[1])
-            self._run(x, rows, m, y)
-        return y.view(*lead, self.out_features)
+                xr = x.reshape(-1, x.shape[-2], x.shape[-1])
+                rows = (xr.stride(0), xr.stride(1), xr.stride(2), xr.shape[1])
+            e = self._run(xr, rows, m, y.view(m, self.out_features))
+            if e and key is not None and xr.data_ptr() == x.data_ptr():  # not where the reshape copied x
+                launches.remember(key, e, y.shape)
+        return y
 
     def conv(self, x: Tensor, *, out_dtype: torch.dtype = torch.float32) -> Tensor:
         """Pointwise convolution [B, K, T] -> [B, N, T] (a transposed view of a [B, T, N] result)."""
+        launches, key = self.launches, _call_key(x, out_dtype, "conv")
+        hit = launches.recall(key)
+        if hit is not None and not (x.requires_grad and torch.is_grad_enabled()):
+            y = torch.empty(hit[1], device=self.device, dtype=out_dtype)
+            launches.launch(hit[0], x, y)
+            return y.transpose(1, 2)
         self._check(x, "conv")
         b, _, t = x.shape
         y = torch.empty(b, t, self.out_features, device=self.device, dtype=out_dtype)
         if b * t:
-            self._run(x, (x.stride(0), x.stride(2), x.stride(1), t), b * t, y.view(b * t, self.out_features))
+            e = self._run(x, (x.stride(0), x.stride(2), x.stride(1), t), b * t, y.view(b * t, self.out_features))
+            if e and key is not None:
+                launches.remember(key, e, y.shape)
         return y.transpose(1, 2)
 
-    def _run(self, x: Tensor, rows: tuple, m: int, y: Tensor) -> None:
-        if not self.launches.project(x, rows, m, self.PARTS, y):
+    def _run(self, x: Tensor, rows: tuple, m: int, y: Tensor):
+        """The layer's parts of x's rows into y [m, N]; returns the cached launch entry used, or None."""
+        e = self.launches.project(x, rows, m, self.PARTS, y)
+        if not e:
             q, qs, ldq = quantize(x, rows, m, self.in_features, parts=self.PARTS)
             self.dot(q, qs, ldq, m, y)
+            return None
+        return e
 
     def dot(self, q: Tensor, qs: Tensor, ldq: int, m: int, y: Tensor | None, *, silu: bool = False, config=None,
             order: int = 0, acc_out: Tensor | None = None) -> None:
@@ -130,6 +152,15 @@ class Int8MmaLayer:
         if components != self.PARTS and type(self) is Int8MmaLayer:
             raise ValueError("Int8MmaLayer implements INT8x3 arithmetic only (components=3)")
         return _project(self, x, conv, components, activation, norm, input_activation)
+
+
+def _call_key(x, out_dtype, kind: str):
+    """A linear / conv call's layout: x's shape, strides, dtype and device and the output dtype determine every
+    argument the call checks and launches with (the rows are x's own); None for a non-tensor (the checks raise)."""
+    try:
+        return (kind, x.shape, x.stride(), x.dtype, x.device, out_dtype)
+    except (AttributeError, TypeError, RuntimeError):  # not a strided tensor
+        return None
 
 
 def _project(layer: Int8MmaLayer, x: Tensor, conv: bool, parts: int, activation: str, norm,

@@ -49,11 +49,15 @@ class Int8MmaPartsLayer(Int8MmaLayer):
             raise ValueError(f"components must be 1, 2 or 3, got {components!r}")
         return _project(self, x, conv, parts, activation, norm, input_activation)
 
-    def _run(self, x: Tensor, rows: tuple, m: int, y: Tensor) -> None:
-        """linear / conv: the first PARTS residual parts (bitwise the PARTS-part quantizer)."""
-        if not self.launches.project(x, rows, m, self.PARTS, y):
+    def _run(self, x: Tensor, rows: tuple, m: int, y: Tensor):
+        """linear / conv: the first PARTS residual parts (bitwise the PARTS-part quantizer); returns the cached
+        launch entry used, or None."""
+        e = self.launches.project(x, rows, m, self.PARTS, y)
+        if not e:
             q, qs, ldq = quantize(x, rows, m, self.in_features, parts=self.PARTS)
             self.dot(q, qs, ldq, m, y, parts=self.PARTS)
+            return None
+        return e
 
 
 def _aligned(q: Tensor, k: int) -> tuple[Tensor, int]:

@@ -308,9 +308,9 @@ def quantize(x: Tensor, rows: tuple, m: int, k: int, parts: int, *, norm=None, i
 
 
 class _Entry:
-    """One resolved call layout of a Launches cache: the GEMM plan, its workspace bytes and the quantizer's fixed
-    arguments."""
-    __slots__ = ("plan", "free", "need", "ldq", "qs_off", "nbytes", "qargs")
+    """One resolved call layout of a Launches cache: a plan (a projection plan, or a GEMM plan for dot()), the C
+    function that frees it and the device workspace bytes one launch of it needs."""
+    __slots__ = ("plan", "free", "need")
 
     def __del__(self):
         plan, self.plan = getattr(self, "plan", None), None
@@ -324,17 +324,19 @@ class Launches:
     An operator call is the residual quantizer of its input plus the low-bit GEMM. gemm() and quantize() check every
     argument and resolve the tile, split and kernel on each call, about 11 us of host time each. Here the first call
     of a layout (input dtype, shape and strides, part count, output dtype and row stride, epilogue flags, LayerNorm)
-    does those checks once and keeps a GEMM plan (kea_lowbit_gemm_plan); later calls of that layout allocate the int8
-    parts and the output, enqueue kea_quantize and bind the plan to the new buffers (kea_lowbit_gemm_plan_launch_with,
-    which re-checks the buffer alignments it depends on). The reference validates and launches on every call
-    (kk/binary/layer.py:182-209, kk/ternary/fused_kernels.py:139-160); the results are the same bits either way.
-    Layouts are kept up to `max_entries` (the oldest is dropped first)."""
+    does those checks once and keeps a projection plan (kea_lowbit_project_plan: the quantizer's arguments and a GEMM
+    plan); later calls of that layout allocate one workspace for the int8 parts, their scales and any split-K slices
+    and make one C call, kea_lowbit_project_launch, which enqueues the quantizer and the GEMM on the new x, y and
+    workspace. The reference validates and launches on every call (kk/binary/layer.py:154-165 and :182-209,
+    kk/ternary/fused_kernels.py:139-160); the results are the same bits either way. Layouts are kept up to
+    `max_entries` (the oldest is dropped first)."""
 
     def __init__(self, wbits: int, words: Tensor, n: int, k: int, wscale: Tensor, bias: Tensor | None, *,
                  max_entries: int = 64):
         self.wbits, self.words, self.n, self.k, self.wscale, self.bias = wbits, words, n, k, wscale, bias
         self.max_entries = max_entries
         self._entries: dict = {}
+        self._calls: dict = {}
 
     def __len__(self) -> int:
         return len(self._entries)
@@ -355,8 +357,8 @@ class Launches:
                 order: int = 0, norm=None, input_activation: str = "", config=None) -> bool:
         """y[:m] (row-major [>= m, N] view) = the GEMM of the parts-part quantization of x's rows (x's own rows:
         `rows` = (XB, XT, XK, T) derived from x's shape and strides by the caller, so every row lies inside x).
-        Returns False, having done nothing, where the call needs the uncached path (a LayerNorm whose parameters
-        are not f32 device-contiguous)."""
+        Returns the layout's entry (for remember()), or False, having done nothing, where the call needs the uncached
+        path (a LayerNorm whose parameters are not f32 device-contiguous)."""
         nkey = self._norm_key(norm, x.device)
         if nkey is False:
             return False
@@ -366,42 +368,59 @@ class Launches:
         e = self._entries.get(key)
         if e is None:
             e = self._resolve(key, x, rows, m, parts, y, silu, order, norm, input_activation, config)
-        buf = torch.empty(e.nbytes, dtype=torch.uint8, device=x.device)
-        q, qs = buf.data_ptr(), buf.data_ptr() + e.qs_off
-        stream = _hip.stream_handle(x.device)
-        L = _hip.lib()
-        rc = L.kea_quantize(x.data_ptr(), *e.qargs, q, e.ldq, qs, _hip.F32, stream)
+        self.launch(e, x, y)
+        return e
+
+    @staticmethod
+    def launch(e: _Entry, x: Tensor, y: Tensor) -> None:
+        """One launch of a projection entry on x and y of its layout: a workspace from torch's allocator (stream
+        ordered, so it may be reused as soon as the launches are enqueued) and kea_lowbit_project_launch."""
+        ws = torch.empty(e.need, dtype=torch.uint8, device=x.device)
+        rc = _hip.lib().kea_lowbit_project_launch(e.plan, x.data_ptr(), y.data_ptr(), ws.data_ptr(), e.need,
+                                                  _hip.stream_handle(x.device))
         if rc:
-            _hip.check(rc, "kea_quantize")
-        ws = torch.empty(e.need, dtype=torch.uint8, device=x.device) if e.need else None
-        rc = L.kea_lowbit_gemm_plan_launch_with(e.plan, q, qs, y.data_ptr(), None, None,
-                                                ws.data_ptr() if ws is not None else None, e.need, stream)
-        if rc:
-            _hip.check(rc, "kea_lowbit_gemm_plan_launch_with")
-        return True
+            _hip.check(rc, "kea_lowbit_project_launch")
+
+    def recall(self, key):
+        """What an operator kept with remember() for `key`: (entry, output shape), or None."""
+        try:
+            return self._calls.get(key)
+        except TypeError:  # an unhashable argument, which the operator's checks refuse
+            return None
+
+    def remember(self, key, e: _Entry, out_shape: tuple) -> None:
+        """Keeps a projection entry under an operator's own key: a tuple of the call's inputs (tensor shapes,
+        strides, dtypes, device) from which the operator derives every argument it checks and passes, so that a call
+        with the same key may skip to launch(). Up to `max_entries` keys (the oldest is dropped first)."""
+        if len(self._calls) >= self.max_entries:
+            self._calls.pop(next(iter(self._calls)))
+        self._calls[key] = (e, out_shape)
 
     def _resolve(self, key, x, rows, m, parts, y, silu, order, norm, input_activation, config) -> _Entry:
         """The first call of a layout: the full checks of quantize() and gemm() on real buffers, then the plan."""
         if m < 1:
             raise ValueError("a cached launch needs at least one row")
-        q, qs, ldq = quantize(x, rows, m, self.k, parts, norm=norm, input_activation=input_activation)
+        q, qs, _ = quantize(x, rows, m, self.k, parts, norm=norm, input_activation=input_activation)
         args, _, workspace = _gemm_args(self.wbits, q, qs, self.words, self.n, self.k, self.wscale, self.bias, y,
                                         None, m, silu, order, config, 0, None, False)
         L = _hip.lib()
-        e = _Entry()
-        e.free = L.kea_lowbit_gemm_plan_free
-        e.plan = L.kea_lowbit_gemm_plan(*args, None, 0, 1.0)
-        if not e.plan:
+        plan = L.kea_lowbit_gemm_plan(*args, None, 0, 1.0)
+        if not plan:
             _hip.check(-1, "kea_lowbit_gemm_plan")
-        e.need = int(L.kea_lowbit_gemm_plan_workspace(e.plan))
-        e.ldq = ldq
-        e.qs_off = parts * m * ldq                       # a multiple of 16: the scales start 16-byte aligned
-        e.nbytes = e.qs_off + 4 * parts * m
         nw, nb, eps = (None, None, 0.0) if norm is None else (norm.weight.data_ptr(), norm.bias.data_ptr(),
                                                               float(norm.eps))
         xb, xt, xk, t = rows
-        e.qargs = (_hip.dtype_code(x.dtype), xb, xt, xk, max(t, 1), m, self.k, parts, nw, nb, eps,
-                   int(input_activation == "silu"))
+        try:  # the projection plan copies the GEMM plan
+            pp = L.kea_lowbit_project_plan(plan, _hip.dtype_code(x.dtype), xb, xt, xk, max(t, 1), nw, nb, eps,
+                                           int(input_activation == "silu"))
+        finally:
+            L.kea_lowbit_gemm_plan_free(plan)
+        if not pp:
+            _hip.check(-1, "kea_lowbit_project_plan")
+        e = _Entry()
+        e.free = L.kea_lowbit_project_plan_free
+        e.plan = pp
+        e.need = int(L.kea_lowbit_project_workspace(pp))
         if len(self._entries) >= self.max_entries:
             self._entries.pop(next(iter(self._entries)))
         self._entries[key] = e

@@ -218,6 +218,11 @@ def test_layer_errors_match_the_reference_contract():
         layer.dot(q, torch.ones(3, 4, device="cuda"), 128, 4, torch.empty(4, 64, device="cuda"))
     with pytest.raises(RuntimeError, match="inference only"):
         layer.linear(torch.randn(4, 128, device="cuda", requires_grad=True))
+    layer.linear(torch.randn(4, 128, device="cuda"))  # a layout the layer now launches without its checks
+    with pytest.raises(RuntimeError, match="inference only"):
+        layer.linear(torch.randn(4, 128, device="cuda", requires_grad=True))
+    with pytest.raises(ValueError, match="input on"):
+        layer.linear(torch.randn(4, 128))
 
 
 @torch.inference_mode()
@@ -263,12 +268,14 @@ def test_cached_launches_are_bitwise_the_checked_path(parts):
         xs = [torch.randn(37, k, generator=g).cuda(),
               torch.randn(2, 19, k, generator=g).cuda(),
               torch.randn(70, 2 * k, generator=g).cuda()[:, ::2],
-              torch.randn(16, k, generator=g).cuda().half()]
+              torch.randn(16, k, generator=g).cuda().half(),
+              torch.randn(2, 3, 19, k, generator=g).cuda().transpose(0, 1)]  # its 3-D view is a copy
         for x in xs:
             got = layer.linear(x)
-            x3 = x.reshape(-1, x.shape[-2], x.shape[-1]) if x.dim() == 3 else x
+            assert got.shape == (*x.shape[:-1], n)
+            x3 = x.reshape(-1, x.shape[-2], x.shape[-1]) if x.dim() >= 3 else x
             m = got.numel() // n
-            rows = (x3.stride(0), x3.stride(1), x3.stride(2), x3.shape[1]) if x.dim() == 3 else \
+            rows = (x3.stride(0), x3.stride(1), x3.stride(2), x3.shape[1]) if x.dim() >= 3 else \
                 (0, x.stride(0), x.stride(1), m)
             want = torch.empty(m, n, device="cuda")
             _uncached(layer, x3, rows, m, parts, want)
@@ -290,7 +297,13 @@ def test_cached_launches_are_bitwise_the_checked_path(parts):
                   input_activation="silu")
         torch.cuda.synchronize()
         assert torch.equal(got.reshape(66, n).view(torch.int32), want.view(torch.int32))
-    assert 1 <= len(layer.launches) <= 8  # one entry per layout, not per call
+    # one entry per layout, not per call: 5 linear layouts, conv, and project once per LayerNorm (a new one per step)
+    assert 1 <= len(layer.launches) <= 9
+    # repeated linear / conv calls skip the checks (a kept entry per input layout), except where x's 3-D view copies
+    assert layer.launches.recall(("linear", xs[0].shape, xs[0].stride(), xs[0].dtype, xs[0].device, torch.float32))
+    assert layer.launches.recall(("conv", xc.shape, xc.stride(), xc.dtype, xc.device, torch.float32))
+    assert not layer.launches.recall(("linear", xs[4].shape, xs[4].stride(), xs[4].dtype, xs[4].device,
+                                      torch.float32))
 
 
 @torch.inference_mode()

@@ -288,3 +288,62 @@ def test_plan_launch_with_refuses_mismatched_buffers_before_any_launch():
                                                       need, None) == -2
         finally:
             L.kea_lowbit_gemm_plan_free(hs)
+
+
+def test_project_plan_refuses_what_the_two_calls_refuse_and_sizes_its_workspace():
+    """kea_lowbit_project_plan takes a GEMM plan made on the quantizer's layout (y only; part_stride = m * ldq,
+    qs_stride = m) plus kea_quantize's arguments, and refuses what either would; its workspace holds the int8 parts,
+    then their scales, then any split-K slices, each 16-byte aligned. kea_lowbit_project_launch refuses a NULL plan,
+    missing x or y and a missing, short or unaligned workspace on the host (fake addresses: no device is touched)."""
+    L = _hip.lib()
+    P = ctypes.c_void_p
+
+    def plan(acc=None, split=1, part_stride=64 * 1024, qs_stride=64):
+        return L.kea_lowbit_gemm_plan(1, P(0x1000), part_stride, 1024, 1, P(0x2000), 0, qs_stride, P(0x3000), 256,
+                                      1024, P(0x4000), 0, 0, None, 0, P(0x10000), 0, 256, acc, 256 if acc else 0, 64,
+                                      0, split, 0, P(0x100000) if split > 1 else None, 1 << 20 if split > 1 else 0,
+                                      None, 0, 1.0)
+
+    def project(h, x_dtype=0, t=64, nw=None, nb=None):
+        return L.kea_lowbit_project_plan(h, x_dtype, 0, 1024, 1, t, nw, nb, 1e-5, 0)
+
+    assert not project(None) and b"plan is NULL" in L.kea_last_error()
+    for kwargs, message in (({"acc": P(0x20000)}, b"writes y only"), ({"part_stride": 65 * 1024}, b"part_stride"),
+                            ({"qs_stride": 128}, b"qs_stride")):
+        h = plan(**kwargs)
+        assert h, L.kea_last_error()
+        try:
+            assert not project(h) and message in L.kea_last_error()
+        finally:
+            L.kea_lowbit_gemm_plan_free(h)
+    h = plan()
+    try:
+        assert not project(h, x_dtype=2) and b"x dtype" in L.kea_last_error()
+        assert not project(h, t=0) and b"t must be" in L.kea_last_error()
+        assert not project(h, nw=P(0x5000)) and b"go together" in L.kea_last_error()
+        pp = project(h)
+        assert pp, L.kea_last_error()
+    finally:
+        L.kea_lowbit_gemm_plan_free(h)  # the projection plan holds its own copy
+    try:
+        need = L.kea_lowbit_project_workspace(pp)
+        assert need == 64 * 1024 + 64 * 4
+        call = L.kea_lowbit_project_launch
+        assert call(None, P(0x8000), P(0x10000), P(0x100000), need, None) == -1
+        assert call(pp, None, P(0x10000), P(0x100000), need, None) == -1
+        assert call(pp, P(0x8000), None, P(0x100000), need, None) == -1
+        assert call(pp, P(0x8000), P(0x10000), None, need, None) == -4
+        assert call(pp, P(0x8000), P(0x10000), P(0x100000), need - 1, None) == -4
+        assert call(pp, P(0x8000), P(0x10000), P(0x100008), need, None) == -2
+    finally:
+        L.kea_lowbit_project_plan_free(pp)
+    hs = plan(split=4)
+    assert hs, L.kea_last_error()
+    try:
+        pp = project(hs)
+        assert pp, L.kea_last_error()
+        assert L.kea_lowbit_project_workspace(pp) == 64 * 1024 + 64 * 4 + L.kea_lowbit_gemm_plan_workspace(hs)
+        L.kea_lowbit_project_plan_free(pp)
+    finally:
+        L.kea_lowbit_gemm_plan_free(hs)
+    L.kea_lowbit_project_plan_free(None)
