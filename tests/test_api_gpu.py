@@ -331,6 +331,31 @@ def test_cached_dot_split_k_workspace_and_acc_out():
     assert layer.launches is not old
 
 
+@pytest.mark.parametrize("parts,tile,split", [(1, 1, 4), (3, 1, 4), (2, 13, 2), (3, 23, 4)])
+@torch.inference_mode()
+def test_projection_plan_with_split_k_slices_in_its_workspace(parts, tile, split):
+    """A projection plan whose GEMM splits K (LDS-ring tile 16x64 and wave-split tiles 16x128 k/4, 16x16 k/4): the
+    int32 slices sit in the one workspace after the int8 parts and their scales; repeated calls on new inputs give
+    the bits of the checked quantize() + gemm() with the same configuration, f16 output."""
+    n, k, m = 256, 4096, 50
+    codes, scale, _ = _weights(n, k, seed=90 + parts)
+    layer = layer_parts.LAYERS[parts].prepare(codes, scale, None, k, "cuda")
+    cfg = GemmConfig(tile=tile, split=split)
+    g = torch.Generator().manual_seed(parts)
+    for _ in range(3):
+        x = torch.randn(m, k, generator=g).cuda()
+        rows = (0, x.stride(0), x.stride(1), m)
+        y = torch.empty(m, n, device="cuda", dtype=torch.float16)
+        e = layer.launches.project(x, rows, m, parts, y, config=cfg)
+        assert e and e.need >= parts * m * k + split * parts * m * n * 4
+        q, qs, _ = lowbit.quantize(x, rows, m, k, parts)
+        want = torch.empty_like(y)
+        lowbit.gemm(1, q, qs, layer.words, n, k, layer.scale, None, want, None, m=m, config=cfg)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+    assert len(layer.launches) == 1
+
+
 @torch.inference_mode()
 def test_ternary_int8_matmul_cached_equals_checked_path():
     n, k = 200, 640
