@@ -676,7 +676,10 @@ def trace_summary(csv_path: str) -> dict:
     """--trace-summary: a rocprofv3 kernel trace (`<name>_kernel_trace.csv`) of this benchmark read the way the
     benchmark times: every run of back-to-back dispatches of one kernel that directly follows a bounded spin kernel
     (the queued regions of the headline figure and of the graph replays) gives (last end - first start) / dispatches,
-    beside the mean and median of the traced per-dispatch durations of the same dispatches. Nanosecond timestamps."""
+    beside the mean and median of the traced per-dispatch durations of the same dispatches, and the median over the
+    isolated ones: dispatches that start at least 1 us after the previous one ended, whose traced duration holds no
+    wait behind the previous dispatch (where the profiler lets dispatches abut, their start timestamps can precede the
+    previous kernel's completion processing). Nanosecond timestamps."""
     import csv
     import statistics
     with open(csv_path, newline="") as handle:
@@ -695,12 +698,16 @@ def trace_summary(csv_path: str) -> dict:
                 durations = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in run]
                 span = int(run[-1]["End_Timestamp"]) - int(run[0]["Start_Timestamp"])
                 gaps = [int(b["Start_Timestamp"]) - int(a["End_Timestamp"]) for a, b in zip(run, run[1:])]
+                isolated = [d for d, gap in zip(durations[1:], gaps) if gap >= 1000]
                 label = name.replace("void ", "", 1).replace("(anonymous namespace)::", "")
                 regions.append({"kernel": label[:label.find("(")] if "(" in label else label, "dispatches": len(run),
                                 "span_us_per_dispatch": round(span / len(run) / 1e3, 4),
                                 "mean_duration_us": round(statistics.fmean(durations) / 1e3, 4),
                                 "median_duration_us": round(statistics.median(durations) / 1e3, 4),
-                                "median_gap_us": round(statistics.median(gaps) / 1e3, 4) if gaps else None})
+                                "median_gap_us": round(statistics.median(gaps) / 1e3, 4) if gaps else None,
+                                "isolated_dispatches": len(isolated),
+                                "isolated_median_us": round(statistics.median(isolated) / 1e3, 4) if isolated
+                                else None})
                 i = k
                 continue
         i += 1
