@@ -393,7 +393,7 @@ class Launches:
         strides, dtypes, device) from which the operator derives every argument it checks and passes, so that a call
         with the same key may skip to launch(). Up to `max_entries` keys (the oldest is dropped first)."""
         if len(self._calls) >= self.max_entries:
-            self._calls.pop(next(iter(self._calls)))
+            self._calls.pop(next(iter(self._calls)), None)
         self._calls[key] = (e, out_shape)
 
     def _resolve(self, key, x, rows, m, parts, y, silu, order, norm, input_activation, config) -> _Entry:
@@ -422,7 +422,7 @@ class Launches:
         e.plan = pp
         e.need = int(L.kea_lowbit_project_workspace(pp))
         if len(self._entries) >= self.max_entries:
-            self._entries.pop(next(iter(self._entries)))
+            self._entries.pop(next(iter(self._entries)), None)
         self._entries[key] = e
         return e
 
@@ -451,7 +451,7 @@ class Launches:
                 _hip.check(-1, "kea_lowbit_gemm_plan")
             e.need = int(L.kea_lowbit_gemm_plan_workspace(e.plan))
             if len(self._entries) >= self.max_entries:
-                self._entries.pop(next(iter(self._entries)))
+                self._entries.pop(next(iter(self._entries)), None)
             self._entries[key] = e
         if torch.is_grad_enabled() and (q.requires_grad or qs.requires_grad):
             raise RuntimeError("the low-bit GEMM is inference only: an input requires grad")
