@@ -202,6 +202,42 @@ def test_every_wave_split_tile_on_ragged_small_m_shapes(wbits, m, n, k, parts):
     assert ran >= 3  # at least three tiles take every one of these shapes
 
 
+def _random_cases(count, seed):
+    """Seeded shapes, part counts, tiles, splits, output and scale types, biases and SiLU flags drawn at random:
+    combinations no hand-written case covers."""
+    rng = np.random.default_rng(seed)
+    out_dtypes = [torch.float32, torch.float16, torch.bfloat16]
+    for i in range(count):
+        yield dict(wbits=int(rng.integers(1, 3)), p=int(rng.integers(1, 4)), m=int(rng.integers(1, 260)),
+                   n=int(rng.integers(1, 600)), k=int(rng.integers(1, 2200)), tile=int(rng.integers(0, 24)),
+                   split=int(rng.choice([0, 1, 2, 4])), out_dtype=out_dtypes[int(rng.integers(0, 3))],
+                   scale_dtype=[torch.float32, torch.float16][int(rng.integers(0, 2))], bias=bool(rng.integers(0, 2)),
+                   order=int(rng.integers(0, 2)), seed=seed * 1000 + i)
+
+
+@pytest.mark.parametrize("seed", [11, 12, 13])
+@torch.inference_mode()
+def test_seeded_random_cases_bitwise(seed):
+    """Random shapes (ragged M, N and K with garbage padding), 1 to 3 parts, any tile (0: the library's choice) and
+    split, f32 / f16 / bf16 output, f32 / f16 scales, with and without bias, both epilogue orders: int32 accumulators
+    and outputs bitwise the oracle's. Configurations the library refuses (a tile that cannot hold the parts, a split
+    without a second slice, an unsplit ragged K range too long for one workgroup) are skipped, not counted."""
+    ran = 0
+    for c in _random_cases(12, seed):
+        case = Case(c["wbits"], c["p"], c["m"], c["n"], c["k"], seed=c["seed"], scale_dtype=c["scale_dtype"],
+                    bias=c["bias"], pad_garbage=True)
+        config = kernels.GemmConfig(tile=c["tile"], split=c["split"]) if c["tile"] else None
+        try:
+            y, acc = case.run(out_dtype=c["out_dtype"], order=c["order"], config=config)
+        except ValueError as e:
+            if any(s in str(e) for s in ("does not fit", "unsplit K range", "split", "slices")):
+                continue
+            raise
+        assert_parity(case, y, acc, out_dtype=c["out_dtype"], order=c["order"])
+        ran += 1
+    assert ran >= 6, ran
+
+
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
 @torch.inference_mode()
 def test_silu_epilogue_within_tolerance(out_dtype):
