@@ -306,6 +306,49 @@ def test_cached_launches_are_bitwise_the_checked_path(parts):
                                       torch.float32))
 
 
+@pytest.mark.parametrize("seed", [21, 22, 23])
+@torch.inference_mode()
+def test_seeded_random_operator_calls_equal_the_checked_path(seed):
+    """Int8MmaPartsLayer.linear / .conv on random shapes (1-, 2-, 3- and 4-D inputs, column-sliced rows, f32 / f16
+    input, f32 / f16 / bf16 output, 1 to 3 parts, with and without bias), each layout called twice (the second call
+    takes the kept launch): every output bitwise the checked quantize() + gemm() on the same rows."""
+    rng = np.random.default_rng(seed)
+    dtypes = [torch.float32, torch.float16, torch.bfloat16]
+    for i in range(8):
+        parts, n, k = int(rng.integers(1, 4)), int(rng.integers(1, 700)), int(rng.integers(1, 2100))
+        codes, scale, _ = _weights(n, k, seed=seed * 100 + i)
+        bias = torch.randn(n, generator=torch.Generator().manual_seed(i)) if rng.integers(0, 2) else None
+        layer = layer_parts.LAYERS[parts].prepare(codes, scale, bias, k, "cuda")
+        out_dtype = dtypes[int(rng.integers(0, 3))]
+        x_dtype = [torch.float32, torch.float16][int(rng.integers(0, 2))]
+        dims, conv = int(rng.integers(1, 5)), bool(rng.integers(0, 4) == 0)
+        lead = [int(rng.integers(1, 40)) for _ in range(dims - 1)]
+        for _ in range(2):
+            g = torch.Generator().manual_seed(int(rng.integers(0, 1 << 30)))
+            if conv:
+                b, t = int(rng.integers(1, 4)), int(rng.integers(1, 60))
+                x = torch.randn(b, k, t, generator=g).to("cuda", x_dtype)
+                got = layer.conv(x, out_dtype=out_dtype).transpose(1, 2).reshape(b * t, n)
+                xr, rows, m = x, (x.stride(0), x.stride(2), x.stride(1), t), b * t
+            else:
+                wide = bool(rng.integers(0, 2))  # rows that are a column slice of a wider tensor
+                full = torch.randn(*lead, k + (7 if wide else 0), generator=g).to("cuda", x_dtype)
+                x = full[..., 3:3 + k] if wide else full
+                got = layer.linear(x, out_dtype=out_dtype)
+                assert got.shape == (*lead, n)
+                m = got.numel() // n
+                got = got.reshape(m, n)
+                xr = x.reshape(-1, x.shape[-2], x.shape[-1]) if x.dim() >= 3 else x
+                rows = ((xr.stride(0), xr.stride(1), xr.stride(2), xr.shape[1]) if x.dim() >= 3 else
+                        (0, x.stride(0), x.stride(1), m) if x.dim() == 2 else (0, 0, x.stride(0), 1))
+            want = torch.empty(m, n, device="cuda", dtype=out_dtype)
+            q, qs, _ = lowbit.quantize(xr, rows, m, k, parts)
+            lowbit.gemm(1, q, qs, layer.words, n, k, layer.scale, layer.bias, want, None, m=m)
+            torch.cuda.synchronize()
+            assert torch.equal(got.view(torch.int16 if out_dtype != torch.float32 else torch.int32),
+                               want.view(torch.int16 if out_dtype != torch.float32 else torch.int32)), (seed, i)
+
+
 @torch.inference_mode()
 def test_cached_dot_split_k_workspace_and_acc_out():
     """dot through the cached plan: a split-K configuration (its workspace allocated per call) and raw
