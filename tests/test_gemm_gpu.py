@@ -595,6 +595,42 @@ def test_group_scales_on_every_wave_split_tile(wbits, p, m, n, k, ws_group):
     assert ran >= 1
 
 
+@pytest.mark.parametrize("seed", [31, 32])
+@torch.inference_mode()
+def test_seeded_random_group_scale_cases_bitwise(seed):
+    """Per-group scales on random shapes: groups of 64, 128 or 256, ragged K, 1 to 3 parts, f32 / f16 scales, f32 / f16
+    output, with and without bias, both epilogue orders, the library's tile choice (wave-split group tiles where K
+    fits one workgroup, else the ring's group tiles) and, where K is a whole number of k-steps of 64 for 4 or 8
+    waves, every wave-split tile that takes groups: y and acc_out bitwise the oracle's per-group rule."""
+    rng = np.random.default_rng(seed)
+    ran = 0
+    for i in range(10):
+        wbits, parts, ws_group = int(rng.integers(1, 3)), int(rng.integers(1, 4)), int(rng.choice([64, 128, 256]))
+        m, n = int(rng.integers(1, 130)), int(rng.integers(1, 500))
+        k = int(rng.choice([64 * 4 * int(rng.integers(1, 9)), 64 * 8 * int(rng.integers(1, 5)),
+                            int(rng.integers(1, 2500))]))
+        out_dtype = [torch.float32, torch.float16][int(rng.integers(0, 2))]
+        case = Case(wbits, parts, m, n, k, seed=seed * 100 + i, bias=bool(rng.integers(0, 2)),
+                    scale_dtype=[torch.float32, torch.float16][int(rng.integers(0, 2))])
+        g = torch.Generator().manual_seed(seed * 100 + i)
+        alpha_g = (torch.rand(n, -(-k // ws_group), generator=g) * 0.09 + 0.01).to(case.qs.dtype)
+        order = int(rng.integers(0, 2))
+        ref_y, ref_acc = _group_ref(case, ws_group, alpha_g, order=order)
+        tiles = [None] + [t for t in range(1, kernels.tile_count() + 1) if " k/" in kernels.config_name(t)]
+        for tile in tiles:
+            config = None if tile is None else kernels.GemmConfig(tile=tile, split=1)
+            try:
+                y, acc = _group_run(case, ws_group, alpha_g, out_dtype=out_dtype, order=order, config=config)
+            except ValueError as e:
+                assert tile is not None and ("per-group weight scales on wave-split tile" in str(e)
+                                             or "does not fit" in str(e)), str(e)
+                continue
+            assert np.array_equal(acc, ref_acc), (seed, i, tile)
+            assert np.array_equal(_gpu_bits(y, out_dtype), _bits(ref_y, out_dtype)), (seed, i, tile)
+            ran += 1
+    assert ran >= 10
+
+
 @pytest.mark.parametrize("k", [17, 300, 4096 + 64])
 @torch.inference_mode()
 def test_group_scales_ragged_k_and_silu(k):
