@@ -234,8 +234,9 @@ void kea_lowbit_gemm_plan_free(kea_gemm_plan *plan);
  * residual replace the pointers the plan was made with (each present exactly where the plan has one; their shapes,
  * strides and dtypes are the plan's), the weights and scales stay the plan's. workspace: kea_lowbit_gemm_plan_workspace
  * bytes (0: none needed). The plan is not modified, so one plan may be launched from several threads. This is the
- * per-call path of the operators' cached launches (an operator resolves a plan once per call layout, then binds each
- * call's buffers), which replaces the reference's per-call validation and launch (kk/binary/layer.py:182-209,
+ * per-call path of the operators' cached dot() launches on caller-made parts (an operator resolves a plan once per
+ * call layout, then binds each call's buffers; its quantize-and-GEMM calls use the projection plan below), which
+ * replaces the reference's per-call validation and launch (kk/binary/layer.py:182-209,
  * kk/ternary/fused_kernels.py:139-160). */
 int kea_lowbit_gemm_plan_launch_with(const kea_gemm_plan *plan, const int8_t *q_dev, const void *qs_dev, void *y_dev,
                                      int32_t *acc_out_dev, const float *residual_dev, void *workspace_dev,
